@@ -1,0 +1,226 @@
+#!/usr/bin/env python3
+"""bench.py — CSR SpMV throughput on one MI355X.
+
+One step = one y = A·x (pf_plan_execute) over the whole matrix, inputs already
+resident in HBM.  Default workload: C2, the 5-point Laplacian on a 2048x2048
+grid (n = 4,194,304, nnz = 20,963,328, fp64) — configs[1] of BASELINE.json,
+the single-GPU configuration the metric is quoted on.  --config 1..5 selects
+the other configurations (C4 also in fp32 with --dtype f32).
+
+Prints ONE JSON line.  `value` is GFLOP/s (2*nnz per step) from the host clock
+around exactly --steps back-to-back steps, bracketed by device
+synchronisation.  `roofline.achieved` is the effective-byte model of the
+reference harness (test/test_cdspmv.cpp:305: nnz*(val+4) + (rows+cols)*val +
+(rows+1)*4) divided by the kernel time per step measured with HIP events on
+the launch stream.  `cold` repeats the measurement with a 1 GiB write between
+steps so that no part of the matrix is served from the 256 MB MALL.
+`cpu_baseline` times the OpenMP restatement of the reference's spmv_serial
+(oracle/, all host cores) on the same matrix.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(REPO, "prefree-public_amd")
+METRIC = "fp64 SpMV GFLOP/s and achieved HBM GB/s (% of peak) on 1 MI355X"
+PEAK_HBM_GBS = 8000.0
+WORKLOADS = {
+    1: "C1 uniform random 4096x4096, 16 nnz/row",
+    2: "C2 5-point Laplacian 2048x2048",
+    3: "C3 power-law n=2,000,000 (Pareto 2.1, cap 200,000)",
+    4: "C4 very sparse n=20,000,000 (Poisson 2.5, banded +-4096, 10% outliers)",
+    5: "C5 mixed n=1,000,000 (0.1% dense rows of 50k-500k nnz)",
+}
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location("prefree_amd", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["prefree_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def traffic_from_profiles(key):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), if committed."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f).get(key)
+        return None if t is None else int(t["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def cpu_baseline(rp, col, val, x, seconds, nnz):
+    sys.path.insert(0, REPO)
+    import numpy as np
+    import oracle
+
+    threads = oracle.omp_max_threads()
+    y = np.zeros(len(rp) - 1, dtype=val.dtype)
+    oracle.spmv_omp(rp, col, val, x, y=y)  # warm-up (page-in)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        y[:] = 0
+        oracle.spmv_omp(rp, col, val, x, y=y)
+        reps += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and reps >= 3) or reps >= 100000:
+            break
+    ms = el * 1e3 / reps
+    return {"value": round(2.0 * nnz / (ms * 1e6), 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "ms_per_spmv": round(ms, 4),
+            "sample": f"full matrix, {reps} SpMVs in {el:.1f} s (OpenMP restatement of spmv_serial, "
+                      f"test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads)"}, y
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
+    ap.add_argument("--dtype", default="f64", choices=["f64", "f32"])
+    ap.add_argument("--variant", default="auto", choices=["auto", "adaptive", "flat", "prefree"])
+    ap.add_argument("--tile", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cold-steps", type=int, default=100)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the sharded design is described in DESIGN.md, no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    pf = load_pkg()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = args.dtype
+    vb = 8 if dt == "f64" else 4
+    tdt = torch.float64 if dt == "f64" else torch.float32
+
+    rp, col, vals = pf.synth_csr(args.config, seed=args.seed, dtypes=(dt,))
+    val = vals[dt]
+    m = len(rp) - 1
+    n = m
+    nnz = len(col)
+    x = pf.synth_x(args.config, n, seed=args.seed, dtypes=(dt,))[dt]
+
+    stream = torch.cuda.current_stream()
+    d_rp = torch.from_numpy(rp).to(dev)
+    d_col = torch.from_numpy(col).to(dev)
+    d_val = torch.from_numpy(val).to(dev)
+    d_x = torch.from_numpy(x).to(dev)
+    d_y = torch.full((m,), float("nan"), dtype=tdt, device=dev)
+    torch.cuda.synchronize()
+
+    t_plan = time.perf_counter()
+    plan = pf.Plan(d_rp, d_col, m, n, nnz, dt, args.variant, args.tile, stream=stream)
+    t_plan = (time.perf_counter() - t_plan) * 1e3
+    info = plan.info.as_dict()
+
+    def step():
+        plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    plan.check(stream=stream)
+
+    # Timed region: exactly --steps steps, device-synchronised on both sides.
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    ms_kernel = e0.elapsed_time(e1) / args.steps
+    plan.check(stream=stream)
+
+    # Cold: a 1 GiB write between steps evicts the matrix from L2 and MALL.
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    cold_ms = 0.0
+    c0 = torch.cuda.Event(enable_timing=True)
+    c1 = torch.cuda.Event(enable_timing=True)
+    for _ in range(args.cold_steps):
+        flush.zero_()
+        c0.record(stream)
+        step()
+        c1.record(stream)
+        c1.synchronize()
+        cold_ms += c0.elapsed_time(c1)
+    cold_ms /= max(1, args.cold_steps)
+    del flush
+
+    y_gpu = d_y.cpu().numpy()
+    bytes_eff = (nnz + m + n) * vb + nnz * 4 + (m + 1) * 4          # test/test_cdspmv.cpp:305
+    bytes_gather = (2 * nnz + m) * vb + nnz * 4 + (m + 1) * 4       # test/test_cdspmv.cpp:306
+    gbs = bytes_eff / (ms_kernel * 1e-3) / 1e9
+    key = f"C{args.config}-{dt}-{info['variant_name']}-{info['tile']}"
+
+    result = {
+        "metric": METRIC,
+        "value": round(2.0 * nnz / (ms_step * 1e6), 3),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dt,
+        "data": "synthetic (seeded generator prefree-public_amd/host/synth.cpp, U[-1,1] values)",
+        "config": {"workload": WORKLOADS[args.config] + ("" if dt == "f64" else " (fp32)"),
+                   "cfg": f"C{args.config}", "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
+                   "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
+                   "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3)},
+        "gbps_effective": round(gbs, 1),
+        "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "bytes_model": {"effective": bytes_eff, "gather": bytes_gather,
+                        "source": "test/test_cdspmv.cpp:305-306"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profiles(key),
+                     "kernel": "k_tiles" if info["variant_name"] != "prefree" else "k_prefree",
+                     "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
+                     "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
+                              if info["needs_fixup"] else "step = one tile-kernel launch")},
+        "cold": {"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
+                 "flush": "1 GiB write before each step"},
+        "device": pf.device_name(),
+    }
+    if not args.no_cpu:
+        cpu, y_cpu = cpu_baseline(rp, col, val, x, args.cpu_seconds, nnz)
+        import oracle
+        err, zero_bad, _ = oracle.rownorm_maxerr(rp, col, val, x, y_cpu, y_gpu)
+        result["cpu_baseline"] = cpu
+        result["parity"] = {"max_rownorm_err_vs_cpu": err, "zero_rows_bad": zero_bad,
+                            "tol": 1e-12 if dt == "f64" else 1e-5}
+        result["speedup_vs_cpu"] = round(cpu["ms_per_spmv"] / ms_step, 1)
+    else:
+        result["cpu_baseline"] = None
+    plan.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,41 @@
+/*
+ * PreFree.h — drop-in replacement for the reference's include/PreFree.h:3-5.
+ *
+ *   void preFreeSpMV(valT *csrVal, int *csrRowPtr, int *csrColInd,
+ *                    valT *X_val, valT *Y_val, int rowA, int colA, int nnzA,
+ *                    double *cdTime, double *cdPre);
+ *
+ * Same C++ linkage and argument meaning as the reference
+ * (src/spmv_kernel/preFreeSpMV.cu:563-662): all pointers are host memory owned
+ * by the caller; the call allocates device memory, copies the CSR matrix and
+ * x, runs 200 warm-up and 4000 timed SpMVs, writes the mean kernel time per
+ * SpMV in ms to *cdTime, computes Y_val = A·x (overwritten) and frees
+ * everything.  Differences, all deliberate:
+ *   - *cdPre is the one-time analysis cost in ms (row statistics, variant
+ *     selection, workspace) — the kernels need no per-call pre-pass;
+ *   - exactly rowA+1 row_ptr entries are read (the reference copies rowA+2);
+ *   - fatal errors print one line to stderr and exit(EXIT_FAILURE), as the
+ *     reference's CUDA_CHECK_ERROR (include/common.h:49-58) does.
+ * Environment knobs (all optional): PREFREE_VARIANT=auto|prefree|adaptive|flat,
+ * PREFREE_TILE=<keys per tile>, PREFREE_WARMUP=<n> (200), PREFREE_ITERS=<n> (4000).
+ *
+ * valT is double (the reference's default -Dfp64 build).  Defining
+ * PREFREE_VALT_FLOAT before including this header selects the float overload.
+ */
+#ifndef PREFREE_DROPIN_H
+#define PREFREE_DROPIN_H
+
+#ifndef valT
+#ifdef PREFREE_VALT_FLOAT
+#define valT float
+#else
+#define valT double
+#endif
+#endif
+
+void preFreeSpMV(double *csrVal, int *csrRowPtr, int *csrColInd, double *X_val, double *Y_val, int rowA, int colA,
+                 int nnzA, double *cdTime, double *cdPre);
+void preFreeSpMV(float *csrVal, int *csrRowPtr, int *csrColInd, float *X_val, float *Y_val, int rowA, int colA,
+                 int nnzA, double *cdTime, double *cdPre);
+
+#endif

@@ -1,0 +1,147 @@
+/*
+ * prefree_c.h — C ABI of the MI355X CSR SpMV library (libprefree.so).
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device memory on the
+ * current device; `stream` is a hipStream_t passed as void* (NULL = the null
+ * stream).  Every function returns a pf_status (0 = success) unless noted.
+ *
+ * Reference counterpart: the reference exposes exactly one entry point,
+ *   void preFreeSpMV(valT*, int*, int*, valT*, valT*, int, int, int, double*, double*)
+ *   (include/PreFree.h:3-5, defined at src/spmv_kernel/preFreeSpMV.cu:563-662),
+ * which allocates, copies, pre-processes, times and computes in one call.
+ * That call is kept as the C++ drop-in in include/PreFree.h.  The entries
+ * below split it into the parts a caller that already holds device buffers
+ * needs: analyse once (pf_plan_create, replacing the pre-pass launch at
+ * preFreeSpMV.cu:599), then y = A·x many times (pf_plan_execute, replacing the
+ * kernel launches at preFreeSpMV.cu:634-645).
+ */
+#ifndef PREFREE_C_H
+#define PREFREE_C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------- */
+enum pf_status {
+    PF_OK = 0,
+    PF_ERR_INVALID = 1,     /* bad argument (negative size, NULL pointer, unknown enum) */
+    PF_ERR_ALIGN = 2,       /* col / val not 16-byte aligned */
+    PF_ERR_HIP = 3,         /* a HIP runtime call failed (see pf_last_error) */
+    PF_ERR_NOMEM = 4,       /* device or host allocation failed */
+    PF_ERR_UNSUPPORTED = 5, /* variant / tile combination not compiled in */
+    PF_ERR_CSR = 6,         /* malformed CSR: row_ptr[0]!=0, decreasing, row_ptr[m]!=nnz, col out of range */
+    PF_ERR_KERNEL = 7       /* a kernel found an inconsistent tile (corrupted row_ptr after planning) */
+};
+
+/* ---- value types ----------------------------------------------------------- */
+enum pf_dtype { PF_F64 = 0, PF_F32 = 1 };
+
+/* ---- kernel variants (all compute y = A·x, y overwritten) ------------------
+ * PF_AUTO      pick from row-length statistics (pf_select)
+ * PF_PREFREE   the reference's algorithm: fixed 512-nnz tiles, per-tile first
+ *              row found in-kernel (no pre-pass), thread / 4-lane / block
+ *              reduction ladder, atomics on tile-boundary rows over a zeroed y
+ *              (preFreeSpMV.cu:407-483, ladder "code 3")
+ * PF_ADAPTIVE  CSR-adaptive row blocks found on the fly: tiles of the merged
+ *              (row, nnz) key space, whole short rows per tile, long rows split
+ *              across tiles and combined deterministically (no atomics)
+ * PF_FLAT      flat fixed-nnz tiles: every row crossing a tile edge is split
+ *              and combined deterministically (no atomics)                  */
+enum pf_variant { PF_AUTO = 0, PF_PREFREE = 1, PF_ADAPTIVE = 2, PF_FLAT = 3 };
+
+/* Row-length statistics of a CSR matrix (one pass over row_ptr). */
+typedef struct pf_row_stats {
+    long long m;
+    long long nnz;
+    long long max_row_len;
+    long long min_row_len;
+    long long n_empty_rows;
+    long long n_decreasing;   /* rows with row_ptr[r+1] < row_ptr[r] (must be 0) */
+    long long row_ptr_first;  /* row_ptr[0] (must be 0) */
+    long long row_ptr_last;   /* row_ptr[m] (must be nnz) */
+    long long n_bad_cols;     /* col[j] outside [0,n); -1 when columns were not checked */
+    long long hist_log2[33];  /* [0]: empty rows; [k]: rows with 2^(k-1) <= len < 2^k */
+} pf_row_stats;
+
+/* Launch configuration chosen for a matrix. */
+typedef struct pf_plan_info {
+    int variant;          /* resolved pf_variant (never PF_AUTO) */
+    int dtype;            /* pf_dtype */
+    int tile;             /* keys per tile (ADAPTIVE: rows+nnz, FLAT/PREFREE: nnz) */
+    int long_row_min;     /* ADAPTIVE: rows longer than this are split across tiles */
+    int guess_spread;     /* row search: spacing of the interpolated first probe round, 0 = none */
+    int needs_fixup;      /* 1 when split rows need the combine kernel */
+    long long ntiles;     /* logical tiles */
+    long long grid;       /* workgroups launched (tiles rounded up to a multiple of the XCD count) */
+    size_t workspace_bytes;
+} pf_plan_info;
+
+typedef struct pf_plan pf_plan;
+
+/* Version as 10000*major + 100*minor + patch. */
+int pf_version(void);
+const char *pf_status_string(int status);
+/* Text of the last HIP error seen by this thread ("" if none). */
+const char *pf_last_error(void);
+
+/* Row statistics of a device CSR (synchronises `stream`).  d_col may be NULL;
+ * otherwise col is range-checked against n (n_bad_cols). */
+int pf_row_stats_compute(const int *d_row_ptr, const int *d_col, int m, int n, long long nnz,
+                         pf_row_stats *out, void *stream);
+
+/* Variant and tile selection from statistics (host only, no GPU call). */
+int pf_select(const pf_row_stats *stats, int dtype, int variant, pf_plan_info *out);
+
+/* Analyse a device CSR, choose a variant (PF_AUTO) or honour the requested
+ * one, allocate the plan's workspace.  d_col may be NULL to skip the column
+ * range check.  Synchronises `stream`.  The plan keeps no pointer to the
+ * matrix; it is valid for any matrix with the same row_ptr. */
+int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz,
+                   int dtype, int variant, void *stream);
+/* Same, with an explicit tile size (0 = default) — used by the tuner. */
+int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n,
+                         int nnz, int dtype, int variant, int tile, void *stream);
+int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out);
+int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
+
+/* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).
+ * val/x/y are double* for PF_F64 and float* for PF_F32.  Calls that share one
+ * plan must be ordered on one stream (the plan's workspace is reused). */
+int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val,
+                    const void *d_x, void *d_y, void *stream);
+/* Reads and clears the plan's device error flag (synchronises `stream`);
+ * returns PF_ERR_KERNEL if a kernel saw an inconsistent tile since the last check. */
+int pf_plan_check(pf_plan *plan, void *stream);
+int pf_plan_destroy(pf_plan *plan);
+
+/* One-shot y = A·x: plan, execute, synchronise, destroy. */
+int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
+            int m, int n, int nnz, int dtype, int variant, void *stream);
+
+/* ---- synthetic matrices (the benchmark configurations) --------------------
+ * cfg 1..5 = C1..C5: 1 uniform 4096^2 16/row, 2 5-point Laplacian 2048^2,
+ * 3 power-law n=2M, 4 very sparse n=20M, 5 mixed dense rows n=1M.  Scaled-down
+ * shapes for tests: `scale_n` > 0 replaces n (C2: grid side).  Generation is
+ * deterministic in (cfg, seed, scale_n) and independent of the thread count.
+ * vals: 0 = the configuration's values (U[-1,1], C2 stencil), 1 = initVec
+ * known-answer values (v[i] = i % 15, include/common.h:126-133). */
+int pf_synth_dims(int cfg, uint64_t seed, int scale_n, int *m, int *n, long long *nnz);
+int pf_synth_csr(int cfg, uint64_t seed, int scale_n, int vals, int *row_ptr, int *col,
+                 double *val_f64, float *val_f32);
+int pf_synth_x(int cfg, uint64_t seed, int n, int vals, double *x_f64, float *x_f32);
+
+/* ---- runtime helpers for hosts without HIP headers (thin wrappers) -------- */
+int pf_device_malloc(void **ptr, size_t bytes);
+int pf_device_free(void *ptr);
+int pf_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int pf_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int pf_stream_synchronize(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

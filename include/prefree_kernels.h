@@ -1,0 +1,90 @@
+/*
+ * prefree_kernels.h — thin extern "C" HIP layer (libprefree_kernels.so).
+ *
+ * The gfx950 kernels and the HIP runtime calls the C++ host layer needs.  Only
+ * libprefree.so (host C++, g++) calls these; applications use prefree_c.h.
+ * Every function returns 0 on success, or a pf_status code (prefree_c.h).
+ *
+ * Reference counterparts (wang-luhan/preFree-public):
+ *   pfk_spmv_prefree      preFreeSpMV_kernel<4,128> launches, src/spmv_kernel/preFreeSpMV.cu:634-645,
+ *                         with pre_start_rowPerTile (:3-28, launched :599) folded into the kernel
+ *   pfk_spmv_adaptive     no counterpart: CSR-adaptive row blocks found on the fly
+ *   pfk_spmv_flat         no counterpart launch: the flat nnz tiling of :407-428 without atomics
+ *   pfk_spmv_fixup        no counterpart: replaces the cross-tile atomicAdd (:67,:91,:142)
+ *   pfk_row_stats         test/statistic.cu:38-98 (per-tile statistics), reduced to row-length stats
+ *   pfk_debug_*           expose in-kernel index computations for bit-exact tests
+ *   pfk_malloc ... pfk_event_*  CUDA runtime calls of preFreeSpMV.cu:571-661 and CudaTimer
+ *                         (include/common.h:66-124)
+ */
+#ifndef PREFREE_KERNELS_H
+#define PREFREE_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Arguments of one SpMV launch.  val/x/y are double* or float* by dtype. */
+typedef struct pfk_spmv_args {
+    const int *row_ptr;
+    const int *col;
+    const void *val;
+    const void *x;
+    void *y;
+    int m;
+    int n;
+    int nnz;
+    int tile;          /* keys (ADAPTIVE) or nnz (FLAT, PREFREE) per tile */
+    int guess_spread;  /* 0 = plain 64-ary search */
+    long long ntiles;
+    void *head_slot;   /* [ntiles] partial of the split row entering a tile */
+    void *tail_slot;   /* [ntiles] partial of the split row leaving a tile */
+    int *owner_row;    /* [ntiles] row whose split starts in the tile, or -1 */
+    int *err_flag;     /* [1] set non-zero by a kernel that finds an inconsistent tile */
+} pfk_spmv_args;
+
+int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream);
+int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream);
+int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream);
+int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
+/* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count. */
+int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap);
+/* Long-row threshold the ADAPTIVE kernel uses for a tile size (-1 if unsupported). */
+int pfk_adaptive_long_row_min(int dtype, int tile);
+
+/* Row statistics.  d_out: 44 unsigned long long (layout in prefree_kernels.hip). */
+int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,
+                  unsigned long long *d_out, void *stream);
+
+/* Tile descriptors of ADAPTIVE (merged=1) / FLAT (merged=0) for every tile:
+ * d_out[8*t + 0..5] = first row, row count, first nnz, end nnz, head split, tail split. */
+int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int *d_out, void *stream);
+/* PREFREE's in-kernel first row of every 512-nnz tile, d_out[0..ntiles] (ntiles+1 entries,
+ * the last one = m), the map the reference pre-pass writes. */
+int pfk_debug_prefree_rows(const int *row_ptr, int m, int nnz, int tile, int *d_out, void *stream);
+
+/* Runtime wrappers. */
+int pfk_malloc(void **p, size_t bytes);
+int pfk_free(void *p);
+int pfk_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int pfk_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+int pfk_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
+int pfk_fill_zero(void *p, size_t bytes, void *stream);  /* a fill kernel, not hipMemsetAsync */
+int pfk_stream_create(void **s);
+int pfk_stream_destroy(void *s);
+int pfk_stream_sync(void *s);
+int pfk_event_create(void **e);
+int pfk_event_destroy(void *e);
+int pfk_event_record(void *e, void *s);
+int pfk_event_sync(void *e);
+int pfk_event_elapsed_ms(float *ms, void *start, void *stop);
+int pfk_device_count(int *n);
+int pfk_device_name(char *buf, int len);
+const char *pfk_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,329 @@
+"""prefree_amd — Python binding of the MI355X CSR SpMV library.
+
+ctypes over the C ABI of ``lib/libprefree.so`` (include/prefree_c.h) and, for
+index-level tests, ``lib/libprefree_kernels.so`` (include/prefree_kernels.h).
+Device buffers are passed as raw pointers; anything with ``data_ptr()`` (a
+torch tensor on the GPU) is accepted.  Streams are HIP stream handles (torch's
+``stream.cuda_stream``); ``None`` is the null stream.
+
+The binding never falls back to a CPU path: if the native libraries are not
+built, importing the functions raises ``RuntimeError``.
+
+Reference counterpart: the single entry point ``preFreeSpMV`` of
+include/PreFree.h:3-5 (wang-luhan/preFree-public), kept in C++ as the drop-in
+(include/PreFree.h of this repo); ``Plan`` exposes its two halves, analysis
+and SpMV, on device memory.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(_HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libprefree.so")
+KLIB_PATH = os.path.join(LIB_DIR, "libprefree_kernels.so")
+
+F64, F32 = 0, 1
+AUTO, PREFREE, ADAPTIVE, FLAT = 0, 1, 2, 3
+VARIANTS = {"auto": AUTO, "prefree": PREFREE, "adaptive": ADAPTIVE, "flat": FLAT}
+VARIANT_NAMES = {v: k for k, v in VARIANTS.items()}
+DTYPES = {"f64": F64, "f32": F32}
+STATUS = {0: "PF_OK", 1: "PF_ERR_INVALID", 2: "PF_ERR_ALIGN", 3: "PF_ERR_HIP", 4: "PF_ERR_NOMEM",
+          5: "PF_ERR_UNSUPPORTED", 6: "PF_ERR_CSR", 7: "PF_ERR_KERNEL"}
+
+
+class PrefreeError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {STATUS.get(status, status)} ({_last_error()})")
+
+
+class RowStats(ctypes.Structure):
+    _fields_ = [("m", ctypes.c_longlong), ("nnz", ctypes.c_longlong), ("max_row_len", ctypes.c_longlong),
+                ("min_row_len", ctypes.c_longlong), ("n_empty_rows", ctypes.c_longlong),
+                ("n_decreasing", ctypes.c_longlong), ("row_ptr_first", ctypes.c_longlong),
+                ("row_ptr_last", ctypes.c_longlong), ("n_bad_cols", ctypes.c_longlong),
+                ("hist_log2", ctypes.c_longlong * 33)]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k, _ in self._fields_ if k != "hist_log2"}
+        d["hist_log2"] = list(self.hist_log2)
+        return d
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [("variant", ctypes.c_int), ("dtype", ctypes.c_int), ("tile", ctypes.c_int),
+                ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
+                ("ntiles", ctypes.c_longlong), ("grid", ctypes.c_longlong), ("workspace_bytes", ctypes.c_size_t)]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k, _ in self._fields_}
+        d["variant_name"] = VARIANT_NAMES.get(self.variant, "?")
+        return d
+
+
+class SpmvArgs(ctypes.Structure):
+    """pfk_spmv_args, include/prefree_kernels.h."""
+    _fields_ = [("row_ptr", ctypes.c_void_p), ("col", ctypes.c_void_p), ("val", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("m", ctypes.c_int), ("n", ctypes.c_int),
+                ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
+                ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
+                ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p)]
+
+
+_lib = None
+_klib = None
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+
+
+def _sig(f, args, res=ctypes.c_int):
+    f.argtypes = args
+    f.restype = res
+
+
+def lib() -> ctypes.CDLL:
+    """The C ABI library; raises if it is not built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"native library {LIB_PATH} is missing: run __graft_entry__.build() "
+                               "(make -C prefree-public_amd)")
+        L = ctypes.CDLL(LIB_PATH)
+        _sig(L.pf_version, [])
+        _sig(L.pf_status_string, [_i], ctypes.c_char_p)
+        _sig(L.pf_last_error, [], ctypes.c_char_p)
+        _sig(L.pf_row_stats_compute, [_vp, _vp, _i, _i, _ll, ctypes.POINTER(RowStats), _vp])
+        _sig(L.pf_select, [ctypes.POINTER(RowStats), _i, _i, ctypes.POINTER(PlanInfo)])
+        _sig(L.pf_plan_create, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _vp])
+        _sig(L.pf_plan_create_tuned, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
+        _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
+        _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
+        _sig(L.pf_plan_execute, [_vp, _vp, _vp, _vp, _vp, _vp, _vp])
+        _sig(L.pf_plan_check, [_vp, _vp])
+        _sig(L.pf_plan_destroy, [_vp])
+        _sig(L.pf_spmv, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
+        _sig(L.pf_synth_dims, [_i, ctypes.c_uint64, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                               ctypes.POINTER(_ll)])
+        _sig(L.pf_synth_csr, [_i, ctypes.c_uint64, _i, _i, _vp, _vp, _vp, _vp])
+        _sig(L.pf_synth_x, [_i, ctypes.c_uint64, _i, _i, _vp, _vp])
+        _sig(L.pf_device_malloc, [ctypes.POINTER(_vp), ctypes.c_size_t])
+        _sig(L.pf_device_free, [_vp])
+        _sig(L.pf_memcpy_h2d, [_vp, _vp, ctypes.c_size_t, _vp])
+        _sig(L.pf_memcpy_d2h, [_vp, _vp, ctypes.c_size_t, _vp])
+        _sig(L.pf_stream_synchronize, [_vp])
+        _lib = L
+    return _lib
+
+
+def klib() -> ctypes.CDLL:
+    """The thin HIP layer (for the index-level debug entry points)."""
+    global _klib
+    if _klib is None:
+        lib()
+        K = ctypes.CDLL(KLIB_PATH)
+        _sig(K.pfk_debug_tile_desc, [_i, _i, ctypes.POINTER(SpmvArgs), _vp, _vp])
+        _sig(K.pfk_debug_prefree_rows, [_vp, _i, _i, _i, _vp, _vp])
+        _sig(K.pfk_adaptive_long_row_min, [_i, _i])
+        _sig(K.pfk_supported_tiles, [_i, _i, ctypes.POINTER(_i), _i])
+        _sig(K.pfk_device_name, [ctypes.c_char_p, _i])
+        _sig(K.pfk_last_error, [], ctypes.c_char_p)
+        _klib = K
+    return _klib
+
+
+def _last_error() -> str:
+    try:
+        return (lib().pf_last_error() or b"").decode()
+    except Exception:  # pragma: no cover - the library itself failed to load
+        return ""
+
+
+def _check(status: int, what: str):
+    if status != 0:
+        raise PrefreeError(status, what)
+
+
+def _p(obj):
+    """Raw device pointer of a torch tensor / int / None."""
+    if obj is None:
+        return None
+    if isinstance(obj, int):
+        return obj
+    return obj.data_ptr()
+
+
+def _s(stream):
+    if stream is None:
+        return None
+    return stream if isinstance(stream, int) else stream.cuda_stream
+
+
+def dtype_code(d) -> int:
+    if isinstance(d, int):
+        return d
+    if d in DTYPES:
+        return DTYPES[d]
+    name = getattr(d, "name", None) or str(d)
+    if "float64" in name or name == "double":
+        return F64
+    if "float32" in name or name == "float":
+        return F32
+    raise ValueError(f"unsupported dtype {d}")
+
+
+def variant_code(v) -> int:
+    return v if isinstance(v, int) else VARIANTS[v]
+
+
+# ---- analysis and execution -------------------------------------------------
+
+def row_stats(row_ptr, col, m, n, nnz, stream=None) -> RowStats:
+    s = RowStats()
+    _check(lib().pf_row_stats_compute(_p(row_ptr), _p(col), m, n, nnz, ctypes.byref(s), _s(stream)),
+           "pf_row_stats_compute")
+    return s
+
+
+def select(stats: RowStats, dtype="f64", variant="auto") -> PlanInfo:
+    info = PlanInfo()
+    _check(lib().pf_select(ctypes.byref(stats), dtype_code(dtype), variant_code(variant), ctypes.byref(info)),
+           "pf_select")
+    return info
+
+
+class Plan:
+    """Analysis of one CSR structure (pf_plan_create); execute() computes y = A·x."""
+
+    def __init__(self, row_ptr, col, m, n, nnz, dtype="f64", variant="auto", tile=0, stream=None):
+        h = ctypes.c_void_p()
+        _check(lib().pf_plan_create_tuned(ctypes.byref(h), _p(row_ptr), _p(col), int(m), int(n), int(nnz),
+                                          dtype_code(dtype), variant_code(variant), int(tile), _s(stream)),
+               "pf_plan_create")
+        self._h = h
+        self.m, self.n, self.nnz = int(m), int(n), int(nnz)
+
+    @property
+    def info(self) -> PlanInfo:
+        i = PlanInfo()
+        _check(lib().pf_plan_get_info(self._h, ctypes.byref(i)), "pf_plan_get_info")
+        return i
+
+    @property
+    def stats(self) -> RowStats:
+        s = RowStats()
+        _check(lib().pf_plan_get_stats(self._h, ctypes.byref(s)), "pf_plan_get_stats")
+        return s
+
+    def execute(self, row_ptr, col, val, x, y, stream=None):
+        _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),
+               "pf_plan_execute")
+
+    def check(self, stream=None):
+        _check(lib().pf_plan_check(self._h, _s(stream)), "pf_plan_check")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().pf_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def spmv(row_ptr, col, val, x, y, m, n, nnz, dtype="f64", variant="auto", stream=None):
+    """One-shot y = A·x (plan, execute, synchronise, destroy)."""
+    _check(lib().pf_spmv(_p(row_ptr), _p(col), _p(val), _p(x), _p(y), int(m), int(n), int(nnz),
+                         dtype_code(dtype), variant_code(variant), _s(stream)), "pf_spmv")
+
+
+def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, stream=None):
+    """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT into `out` (int32[8*ntiles])."""
+    total = nnz + m if merged else nnz
+    ntiles = max(1, -(-total // tile))
+    a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread, ntiles=ntiles,
+                 err_flag=_p(err_flag))
+    _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
+           "pfk_debug_tile_desc")
+    return ntiles
+
+
+def prefree_rows(row_ptr, m, nnz, tile, out, stream=None):
+    """pfk_debug_prefree_rows: in-kernel first row of every tile (ntiles+1 entries, last = m)."""
+    _check(klib().pfk_debug_prefree_rows(_p(row_ptr), m, nnz, tile, _p(out), _s(stream)),
+           "pfk_debug_prefree_rows")
+
+
+def adaptive_long_row_min(dtype, tile) -> int:
+    return int(klib().pfk_adaptive_long_row_min(dtype_code(dtype), int(tile)))
+
+
+def supported_tiles(variant, dtype):
+    buf = (ctypes.c_int * 8)()
+    n = klib().pfk_supported_tiles(variant_code(variant), dtype_code(dtype), buf, 8)
+    return [buf[i] for i in range(n)]
+
+
+def device_name() -> str:
+    buf = ctypes.create_string_buffer(256)
+    _check(klib().pfk_device_name(buf, 256), "pfk_device_name")
+    return buf.value.decode()
+
+
+# ---- synthetic matrices ------------------------------------------------------
+
+CONFIGS = {1: "C1 uniform 4096^2 16/row", 2: "C2 5-point Laplacian 2048^2", 3: "C3 power-law n=2M",
+           4: "C4 very sparse n=20M", 5: "C5 mixed dense rows n=1M"}
+
+
+def synth_dims(cfg, seed=1, scale_n=0):
+    m, n, nnz = ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
+    _check(lib().pf_synth_dims(int(cfg), int(seed), int(scale_n), ctypes.byref(m), ctypes.byref(n),
+                               ctypes.byref(nnz)), "pf_synth_dims")
+    return m.value, n.value, nnz.value
+
+
+def synth_csr(cfg, seed=1, scale_n=0, vals=0, dtypes=("f64",), out=None):
+    """(row_ptr, col, {dtype: val}) of configuration `cfg` as numpy arrays.
+
+    `out` may supply preallocated arrays (dict with keys row_ptr, col, f64, f32),
+    e.g. pinned host memory."""
+    m, n, nnz = synth_dims(cfg, seed, scale_n)
+    out = dict(out or {})
+    rp = out.get("row_ptr")
+    rp = np.empty(m + 1, dtype=np.int32) if rp is None else rp
+    col = out.get("col")
+    col = np.empty(nnz, dtype=np.int32) if col is None else col
+    vals_out = {}
+    for d in dtypes:
+        a = out.get(d)
+        vals_out[d] = np.empty(nnz, dtype=np.float64 if d == "f64" else np.float32) if a is None else a
+    _check(lib().pf_synth_csr(int(cfg), int(seed), int(scale_n), int(vals), rp.ctypes.data, col.ctypes.data,
+                              vals_out["f64"].ctypes.data if "f64" in vals_out else None,
+                              vals_out["f32"].ctypes.data if "f32" in vals_out else None), "pf_synth_csr")
+    return rp, col, vals_out
+
+
+def synth_x(cfg, n, seed=1, vals=0, dtypes=("f64",)):
+    xs = {d: np.empty(n, dtype=np.float64 if d == "f64" else np.float32) for d in dtypes}
+    _check(lib().pf_synth_x(int(cfg), int(seed), int(n), int(vals),
+                            xs["f64"].ctypes.data if "f64" in xs else None,
+                            xs["f32"].ctypes.data if "f32" in xs else None), "pf_synth_x")
+    return xs
+
+
+def version() -> int:
+    return int(lib().pf_version())

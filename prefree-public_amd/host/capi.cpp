@@ -1,0 +1,332 @@
+// capi.cpp — the public C ABI (include/prefree_c.h): row statistics, variant
+// selection, plans and execution.  Host C++ only; every GPU action goes
+// through the thin HIP layer of include/prefree_kernels.h.
+#include "prefree_c.h"
+#include "prefree_kernels.h"
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int status, const std::string &msg)
+{
+    g_err = msg;
+    return status;
+}
+
+int from_kernel_layer(int status, const char *what)
+{
+    if (status != PF_OK)
+        g_err = std::string(what) + ": " + pfk_last_error();
+    return status;
+}
+
+#define PF_TRY(call, what)                                   \
+    do {                                                     \
+        int st_ = (call);                                    \
+        if (st_ != PF_OK) return from_kernel_layer(st_, what); \
+    } while (0)
+
+constexpr int kXcds = 8;
+
+int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : 0; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int default_tile(int variant, int dtype)
+{
+    if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
+    return dtype == PF_F64 ? 2048 : 4096;
+}
+
+bool tile_supported(int variant, int dtype, int tile)
+{
+    int t[8];
+    const int n = pfk_supported_tiles(variant, dtype, t, 8);
+    for (int i = 0; i < n; ++i)
+        if (t[i] == tile) return true;
+    return false;
+}
+
+// Fills everything in `info` that follows from (stats, dtype, variant, tile).
+int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan_info *info)
+{
+    if (!tile_supported(variant, dtype, tile))
+        return fail(PF_ERR_UNSUPPORTED, "tile " + std::to_string(tile) + " not compiled for this variant/dtype");
+    pf_plan_info r;
+    std::memset(&r, 0, sizeof r);
+    r.variant = variant;
+    r.dtype = dtype;
+    r.tile = tile;
+    const long long m = s.m, nnz = s.nnz;
+    // A regular matrix keeps row index and key position nearly proportional:
+    // one interpolated probe round of 64 rows spaced 64 apart brackets the row.
+    const bool regular = s.max_row_len <= 64;
+    r.guess_spread = regular ? 64 : 0;
+    const long long vb = value_bytes(dtype);
+    if (variant == PF_ADAPTIVE) {
+        r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
+        const long long total = nnz + m;
+        r.ntiles = total > 0 ? (total + tile - 1) / tile : 1;
+        r.needs_fixup = s.max_row_len > r.long_row_min;
+        r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
+    } else if (variant == PF_FLAT) {
+        r.long_row_min = 0;
+        r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
+        r.needs_fixup = r.ntiles > 1;
+        r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
+    } else if (variant == PF_PREFREE) {
+        r.long_row_min = 0;
+        r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
+        r.needs_fixup = 0;
+        r.workspace_bytes = 256;
+    } else {
+        return fail(PF_ERR_INVALID, "unknown variant");
+    }
+    r.grid = ((r.ntiles + kXcds - 1) / kXcds) * kXcds;
+    *info = r;
+    return PF_OK;
+}
+
+}  // namespace
+
+struct pf_plan {
+    int m = 0, n = 0, nnz = 0;
+    pf_plan_info info{};
+    pf_row_stats stats{};
+    void *ws = nullptr;
+    void *head = nullptr;
+    void *tail = nullptr;
+    int *owner = nullptr;
+    int *err = nullptr;
+};
+
+extern "C" {
+
+int pf_version(void) { return 100; }  // 0.1.0
+
+const char *pf_status_string(int status)
+{
+    switch (status) {
+    case PF_OK: return "success";
+    case PF_ERR_INVALID: return "invalid argument";
+    case PF_ERR_ALIGN: return "col/val pointer not 16-byte aligned";
+    case PF_ERR_HIP: return "HIP runtime error";
+    case PF_ERR_NOMEM: return "out of memory";
+    case PF_ERR_UNSUPPORTED: return "unsupported variant/tile/dtype";
+    case PF_ERR_CSR: return "malformed CSR matrix";
+    case PF_ERR_KERNEL: return "kernel found an inconsistent tile";
+    }
+    return "unknown status";
+}
+
+const char *pf_last_error(void) { return g_err.c_str(); }
+
+int pf_row_stats_compute(const int *d_row_ptr, const int *d_col, int m, int n, long long nnz,
+                         pf_row_stats *out, void *stream)
+{
+    if (!out || !d_row_ptr || m < 0 || n < 0 || nnz < 0)
+        return fail(PF_ERR_INVALID, "pf_row_stats_compute: bad argument");
+    unsigned long long *d = nullptr;
+    unsigned long long h[44];
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), sizeof h), "stats buffer");
+    int st = pfk_row_stats(d_row_ptr, d_col, m, n, nnz, d, stream);
+    if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream);
+    pfk_free(d);
+    if (st != PF_OK) return from_kernel_layer(st, "row statistics");
+    std::memset(out, 0, sizeof *out);
+    out->m = m;
+    out->nnz = nnz;
+    out->max_row_len = (long long)h[0];
+    out->min_row_len = m > 0 ? (long long)h[1] : 0;
+    out->n_empty_rows = (long long)h[2];
+    out->n_decreasing = (long long)h[3];
+    out->row_ptr_first = (long long)h[4];
+    out->row_ptr_last = (long long)h[5];
+    out->n_bad_cols = (d_col && nnz > 0) ? (long long)h[6] : (nnz > 0 ? -1 : 0);
+    for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
+    return PF_OK;
+}
+
+int pf_select(const pf_row_stats *stats, int dtype, int variant, pf_plan_info *out)
+{
+    if (!stats || !out || value_bytes(dtype) == 0)
+        return fail(PF_ERR_INVALID, "pf_select: bad argument");
+    if (variant == PF_AUTO)
+        variant = PF_ADAPTIVE;
+    return finish_info(*stats, dtype, variant, default_tile(variant, dtype), out);
+}
+
+int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz,
+                         int dtype, int variant, int tile, void *stream)
+{
+    if (!plan) return fail(PF_ERR_INVALID, "plan is NULL");
+    *plan = nullptr;
+    if (m < 0 || n < 0 || nnz < 0 || value_bytes(dtype) == 0 || variant < PF_AUTO || variant > PF_FLAT)
+        return fail(PF_ERR_INVALID, "pf_plan_create: bad size, dtype or variant");
+    if (m > 0 && !d_row_ptr) return fail(PF_ERR_INVALID, "row_ptr is NULL");
+    if ((unsigned long long)nnz + (unsigned long long)m >= 0xFFFFFFFFull)
+        return fail(PF_ERR_UNSUPPORTED, "nnz + m must stay below 2^32");
+    if (d_col && !aligned16(d_col)) return fail(PF_ERR_ALIGN, "col not 16-byte aligned");
+    if (nnz > 0 && m == 0) return fail(PF_ERR_CSR, "nnz > 0 with no rows");
+
+    pf_row_stats s;
+    std::memset(&s, 0, sizeof s);
+    s.m = m;
+    s.nnz = nnz;
+    if (m > 0) {
+        const int st = pf_row_stats_compute(d_row_ptr, d_col, m, n, nnz, &s, stream);
+        if (st != PF_OK) return st;
+        if (s.row_ptr_first != 0 || s.row_ptr_last != nnz || s.n_decreasing != 0 || s.n_bad_cols > 0)
+            return fail(PF_ERR_CSR, "row_ptr[0]=" + std::to_string(s.row_ptr_first) + " row_ptr[m]=" +
+                                        std::to_string(s.row_ptr_last) + " decreasing=" +
+                                        std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
+    }
+    if (variant == PF_AUTO) variant = PF_ADAPTIVE;
+    pf_plan_info info;
+    const int st = finish_info(s, dtype, variant, tile > 0 ? tile : default_tile(variant, dtype), &info);
+    if (st != PF_OK) return st;
+
+    pf_plan *p = new pf_plan();
+    p->m = m;
+    p->n = n;
+    p->nnz = nnz;
+    p->info = info;
+    p->stats = s;
+    int rc = pfk_malloc(&p->ws, info.workspace_bytes);
+    if (rc != PF_OK) {
+        delete p;
+        return from_kernel_layer(rc, "plan workspace");
+    }
+    char *w = static_cast<char *>(p->ws);
+    p->err = reinterpret_cast<int *>(w);
+    if (info.variant != PF_PREFREE) {
+        const size_t vb = (size_t)value_bytes(dtype);
+        const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
+        p->head = w + 256;
+        p->tail = w + 256 + slots;
+        p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
+    }
+    rc = pfk_fill_zero(p->err, 256, stream);
+    if (rc == PF_OK) rc = pfk_stream_sync(stream);
+    if (rc != PF_OK) {
+        pfk_free(p->ws);
+        delete p;
+        return from_kernel_layer(rc, "plan workspace init");
+    }
+    *plan = p;
+    return PF_OK;
+}
+
+int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz, int dtype,
+                   int variant, void *stream)
+{
+    return pf_plan_create_tuned(plan, d_row_ptr, d_col, m, n, nnz, dtype, variant, 0, stream);
+}
+
+int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out)
+{
+    if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
+    *out = plan->info;
+    return PF_OK;
+}
+
+int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out)
+{
+    if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
+    *out = plan->stats;
+    return PF_OK;
+}
+
+int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x,
+                    void *d_y, void *stream)
+{
+    if (!plan) return fail(PF_ERR_INVALID, "NULL plan");
+    if (plan->m == 0) return PF_OK;
+    if (!d_row_ptr || !d_y || (plan->nnz > 0 && (!d_col || !d_val || !d_x)))
+        return fail(PF_ERR_INVALID, "NULL matrix or vector pointer");
+    if (!aligned16(d_col) || !aligned16(d_val)) return fail(PF_ERR_ALIGN, "col/val not 16-byte aligned");
+    pfk_spmv_args a;
+    a.row_ptr = d_row_ptr;
+    a.col = d_col;
+    a.val = d_val;
+    a.x = d_x;
+    a.y = d_y;
+    a.m = plan->m;
+    a.n = plan->n;
+    a.nnz = plan->nnz;
+    a.tile = plan->info.tile;
+    a.guess_spread = plan->info.guess_spread;
+    a.ntiles = plan->info.ntiles;
+    a.head_slot = plan->head;
+    a.tail_slot = plan->tail;
+    a.owner_row = plan->owner;
+    a.err_flag = plan->err;
+    const int dt = plan->info.dtype;
+    switch (plan->info.variant) {
+    case PF_ADAPTIVE:
+        PF_TRY(pfk_spmv_adaptive(dt, &a, stream), "adaptive kernel");
+        if (plan->info.needs_fixup) PF_TRY(pfk_spmv_fixup(dt, 1, &a, stream), "split-row combine");
+        return PF_OK;
+    case PF_FLAT:
+        PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");
+        if (plan->info.needs_fixup) PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
+        return PF_OK;
+    case PF_PREFREE:
+        PF_TRY(pfk_spmv_prefree(dt, &a, stream), "prefree kernel");
+        return PF_OK;
+    }
+    return fail(PF_ERR_INVALID, "plan has an unknown variant");
+}
+
+int pf_plan_check(pf_plan *plan, void *stream)
+{
+    if (!plan) return fail(PF_ERR_INVALID, "NULL plan");
+    int flag = 0;
+    PF_TRY(pfk_memcpy_d2h(&flag, plan->err, sizeof flag, stream), "read error flag");
+    PF_TRY(pfk_stream_sync(stream), "synchronise");
+    if (flag) {
+        PF_TRY(pfk_fill_zero(plan->err, 256, stream), "clear error flag");
+        return fail(PF_ERR_KERNEL, "a tile found row_ptr inconsistent with the planned matrix");
+    }
+    return PF_OK;
+}
+
+int pf_plan_destroy(pf_plan *plan)
+{
+    if (!plan) return PF_OK;
+    const int st = pfk_free(plan->ws);
+    delete plan;
+    return st == PF_OK ? PF_OK : from_kernel_layer(st, "free workspace");
+}
+
+int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y, int m, int n,
+            int nnz, int dtype, int variant, void *stream)
+{
+    pf_plan *p = nullptr;
+    int st = pf_plan_create(&p, d_row_ptr, d_col, m, n, nnz, dtype, variant, stream);
+    if (st != PF_OK) return st;
+    st = pf_plan_execute(p, d_row_ptr, d_col, d_val, d_x, d_y, stream);
+    if (st == PF_OK) st = pf_plan_check(p, stream);
+    const int st2 = pf_plan_destroy(p);
+    return st != PF_OK ? st : st2;
+}
+
+int pf_device_malloc(void **ptr, size_t bytes) { return from_kernel_layer(pfk_malloc(ptr, bytes), "device malloc"); }
+int pf_device_free(void *ptr) { return from_kernel_layer(pfk_free(ptr), "device free"); }
+int pf_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return from_kernel_layer(pfk_memcpy_h2d(dst, src, bytes, stream), "copy to device");
+}
+int pf_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return from_kernel_layer(pfk_memcpy_d2h(dst, src, bytes, stream), "copy to host");
+}
+int pf_stream_synchronize(void *stream) { return from_kernel_layer(pfk_stream_sync(stream), "synchronise"); }
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+// dropin.cpp — the reference's one-call API, preFreeSpMV (include/PreFree.h),
+// on top of the C ABI.  Restates the host orchestration of
+// src/spmv_kernel/preFreeSpMV.cu:563-662: allocate, copy in, analyse (the
+// reference's pre-pass slot), time 200 warm-up + 4000 SpMVs with events on one
+// stream, compute the checked y, copy out, free.
+#include "PreFree.h"
+#include "prefree_c.h"
+#include "prefree_kernels.h"
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+namespace {
+
+[[noreturn]] void die(const char *what, int status)
+{
+    std::fprintf(stderr, "PreFree error: %s failed: %s (%s)\n", what, pf_status_string(status), pf_last_error());
+    std::exit(EXIT_FAILURE);
+}
+
+void check(int status, const char *what)
+{
+    if (status != PF_OK) die(what, status);
+}
+
+int env_int(const char *name, int dflt)
+{
+    const char *v = std::getenv(name);
+    return (v && *v) ? std::atoi(v) : dflt;
+}
+
+int env_variant()
+{
+    const char *v = std::getenv("PREFREE_VARIANT");
+    if (!v || !*v) return PF_AUTO;
+    const std::string s(v);
+    if (s == "prefree") return PF_PREFREE;
+    if (s == "adaptive") return PF_ADAPTIVE;
+    if (s == "flat") return PF_FLAT;
+    if (s == "auto") return PF_AUTO;
+    std::fprintf(stderr, "PreFree error: unknown PREFREE_VARIANT=%s\n", v);
+    std::exit(EXIT_FAILURE);
+}
+
+template <typename T>
+void run(T *csrVal, int *csrRowPtr, int *csrColInd, T *X_val, T *Y_val, int rowA, int colA, int nnzA,
+         double *cdTime, double *cdPre)
+{
+    const int dtype = sizeof(T) == 8 ? PF_F64 : PF_F32;
+    if (rowA < 0 || colA < 0 || nnzA < 0) die("argument check", PF_ERR_INVALID);
+    void *stream = nullptr;
+    check(pfk_stream_create(&stream), "stream create");
+
+    void *d_y = nullptr, *d_x = nullptr, *d_val = nullptr, *d_col = nullptr, *d_rp = nullptr;
+    check(pf_device_malloc(&d_y, sizeof(T) * (size_t)rowA), "device allocation");
+    check(pf_device_malloc(&d_x, sizeof(T) * (size_t)colA), "device allocation");
+    check(pf_device_malloc(&d_val, sizeof(T) * (size_t)nnzA), "device allocation");
+    check(pf_device_malloc(&d_col, sizeof(int) * (size_t)nnzA), "device allocation");
+    check(pf_device_malloc(&d_rp, sizeof(int) * ((size_t)rowA + 1)), "device allocation");
+    check(pf_memcpy_h2d(d_val, csrVal, sizeof(T) * (size_t)nnzA, stream), "copy val");
+    check(pf_memcpy_h2d(d_col, csrColInd, sizeof(int) * (size_t)nnzA, stream), "copy col");
+    check(pf_memcpy_h2d(d_rp, csrRowPtr, sizeof(int) * ((size_t)rowA + 1), stream), "copy row_ptr");
+    check(pf_memcpy_h2d(d_x, X_val, sizeof(T) * (size_t)colA, stream), "copy x");
+    check(pf_stream_synchronize(stream), "copy");
+
+    // One-time analysis (row statistics + selection + workspace), timed as cdPre.
+    const auto t0 = std::chrono::steady_clock::now();
+    pf_plan *plan = nullptr;
+    check(pf_plan_create_tuned(&plan, static_cast<int *>(d_rp), static_cast<int *>(d_col), rowA, colA, nnzA, dtype,
+                               env_variant(), env_int("PREFREE_TILE", 0), stream),
+          "plan");
+    const auto t1 = std::chrono::steady_clock::now();
+    *cdPre = std::chrono::duration<double, std::milli>(t1 - t0).count();
+
+    const int warm = env_int("PREFREE_WARMUP", 200), iters = env_int("PREFREE_ITERS", 4000);
+    auto spmv = [&]() {
+        check(pf_plan_execute(plan, static_cast<int *>(d_rp), static_cast<int *>(d_col), d_val, d_x, d_y, stream),
+              "spmv");
+    };
+    for (int i = 0; i < warm; ++i) spmv();
+    check(pf_stream_synchronize(stream), "warm-up");
+    void *e0 = nullptr, *e1 = nullptr;
+    check(pfk_event_create(&e0), "event");
+    check(pfk_event_create(&e1), "event");
+    check(pfk_event_record(e0, stream), "event record");
+    for (int i = 0; i < iters; ++i) spmv();
+    check(pfk_event_record(e1, stream), "event record");
+    check(pfk_event_sync(e1), "event sync");
+    float ms = 0.f;
+    check(pfk_event_elapsed_ms(&ms, e0, e1), "event time");
+    *cdTime = iters > 0 ? (double)ms / iters : 0.0;
+
+    // The checked result: a fresh y, one SpMV (preFreeSpMV.cu:644-645).
+    check(pfk_fill_zero(d_y, sizeof(T) * (size_t)rowA, stream), "zero y");
+    spmv();
+    check(pf_plan_check(plan, stream), "spmv");
+    check(pf_memcpy_d2h(Y_val, d_y, sizeof(T) * (size_t)rowA, stream), "copy y");
+    check(pf_stream_synchronize(stream), "copy y");
+
+    pfk_event_destroy(e0);
+    pfk_event_destroy(e1);
+    pf_plan_destroy(plan);
+    pf_device_free(d_y);
+    pf_device_free(d_x);
+    pf_device_free(d_val);
+    pf_device_free(d_col);
+    pf_device_free(d_rp);
+    pfk_stream_destroy(stream);
+}
+
+}  // namespace
+
+void preFreeSpMV(double *csrVal, int *csrRowPtr, int *csrColInd, double *X_val, double *Y_val, int rowA, int colA,
+                 int nnzA, double *cdTime, double *cdPre)
+{
+    run<double>(csrVal, csrRowPtr, csrColInd, X_val, Y_val, rowA, colA, nnzA, cdTime, cdPre);
+}
+
+void preFreeSpMV(float *csrVal, int *csrRowPtr, int *csrColInd, float *X_val, float *Y_val, int rowA, int colA,
+                 int nnzA, double *cdTime, double *cdPre)
+{
+    run<float>(csrVal, csrRowPtr, csrColInd, X_val, Y_val, rowA, colA, nnzA, cdTime, cdPre);
+}

@@ -1,0 +1,62 @@
+"""Helpers shared by the GPU tests: device copies and one SpMV through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+import prefree_amd as pf
+
+DEV = "cuda:0"
+TOL = {"f64": 1e-12, "f32": 1e-5}   # per-row error normalised by sum_j |a_ij x_j|
+NP = {"f64": np.float64, "f32": np.float32}
+TORCH = {"f64": torch.float64, "f32": torch.float32}
+
+
+def dev(a, min_len=4):
+    a = np.ascontiguousarray(a)
+    if a.size < min_len:  # keep a real allocation behind empty arrays
+        a = np.concatenate([a, np.zeros(min_len - a.size, dtype=a.dtype)])
+    return torch.from_numpy(a).to(DEV)
+
+
+def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=1):
+    """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info)."""
+    m, n, nnz = len(rp) - 1, len(x), len(col)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    y = torch.full((max(m, 1),), fill, dtype=TORCH[dtype], device=DEV)
+    stream = torch.cuda.current_stream()
+    with pf.Plan(d_rp, d_col, m, n, nnz, dtype, variant, tile, stream=stream) as p:
+        for _ in range(repeat):
+            p.execute(d_rp, d_col, d_val, d_x, y, stream=stream)
+        torch.cuda.synchronize()
+        p.check(stream=stream)
+        info = p.info.as_dict()
+    return y[:m].cpu().numpy(), info
+
+
+def kat_exact_possible(rp, dtype):
+    """initVec values are integers <= 14; row sums stay exact below 2^53 (f64) / 2^24 (f32)."""
+    longest = int(np.max(np.diff(rp))) if len(rp) > 1 else 0
+    return longest * 196 < (2 ** 53 if dtype == "f64" else 2 ** 24)
+
+
+def assert_parity(rp, col, val, x, y, dtype, exact=False, what=""):
+    """exact: bit equality with the oracle in `dtype`.  Otherwise the normalised
+    per-row error against the oracle; for f32 the oracle is evaluated in f64 on
+    the same f32 data, because a sequential f32 sum of a row with 10^4-10^5
+    terms is itself off by more than 1e-5 of sum_j |a_ij x_j|."""
+    ref = oracle.spmv_serial(rp, col, val, x)
+    if exact:
+        bad = np.flatnonzero(ref != y)
+        assert bad.size == 0, f"{what}: {bad.size} rows differ, first {bad[:5]} ref {ref[bad[:3]]} got {y[bad[:3]]}"
+        return 0.0
+    if dtype == "f32":
+        v64, x64 = val.astype(np.float64), x.astype(np.float64)
+        err, zero_bad, worst = oracle.rownorm_maxerr(rp, col, v64, x64, oracle.spmv_serial(rp, col, v64, x64),
+                                                     y.astype(np.float64))
+    else:
+        err, zero_bad, worst = oracle.rownorm_maxerr(rp, col, val, x, ref, y)
+    assert zero_bad == 0, f"{what}: {zero_bad} empty-denominator rows not exactly zero"
+    assert err <= TOL[dtype], f"{what}: normalised error {err:.3e} at row {worst} (tol {TOL[dtype]})"
+    return err

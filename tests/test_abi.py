@@ -1,0 +1,121 @@
+"""C ABI surface and host logic — CPU only (no GPU call is made).
+
+* both libraries load and export every function their headers declare;
+* the C++ drop-in preFreeSpMV keeps the reference's signature
+  (include/PreFree.h:3-5 of wang-luhan/preFree-public) with C++ linkage;
+* pf_select (host only) resolves variants, tiles and tile counts;
+* argument validation fails before any GPU call.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import prefree_amd as pf
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = {
+    "prefree_c.h": pf.LIB_PATH,
+    "prefree_kernels.h": pf.KLIB_PATH,
+}
+
+
+def declared_functions(header):
+    text = open(os.path.join(REPO, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pfk?_[a-z0-9_]+)\s*\(", text)))
+
+
+def exported(lib_path):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+@pytest.mark.parametrize("header", sorted(HEADERS))
+def test_every_declared_symbol_is_exported(header):
+    names = declared_functions(header)
+    assert len(names) > 10
+    syms = exported(HEADERS[header])
+    missing = [n for n in names if n not in syms]
+    assert not missing, missing
+    lib = ctypes.CDLL(HEADERS[header])
+    for n in names:
+        getattr(lib, n)
+
+
+def test_dropin_cxx_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", pf.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "preFreeSpMV(double*, int*, int*, double*, double*, int, int, int, double*, double*)" in out
+    assert "preFreeSpMV(float*, int*, int*, float*, float*, int, int, int, double*, double*)" in out
+
+
+def test_kernel_library_targets_gfx950():
+    # the offload bundle embedded in our own build names its only target
+    blob = open(pf.KLIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+    assert b"gfx942" not in blob and b"gfx90a" not in blob
+
+
+def test_status_strings_and_version():
+    L = pf.lib()
+    for code in range(8):
+        assert L.pf_status_string(code)
+    assert L.pf_status_string(99) == b"unknown status"
+    assert pf.version() == 100
+
+
+def make_stats(m, nnz, max_len, empty=0):
+    s = pf.RowStats()
+    s.m, s.nnz, s.max_row_len, s.min_row_len, s.n_empty_rows = m, nnz, max_len, 0, empty
+    s.row_ptr_last = nnz
+    return s
+
+
+def test_select_auto_is_adaptive_with_default_tiles():
+    s = make_stats(4194304, 20963328, 5)
+    i = pf.select(s, "f64", "auto")
+    assert i.variant == pf.ADAPTIVE and i.tile == 2048
+    assert i.ntiles == -(-(20963328 + 4194304) // 2048)
+    assert i.grid % 8 == 0 and i.grid >= i.ntiles
+    assert i.needs_fixup == 0 and i.guess_spread == 64
+    assert i.long_row_min == pf.adaptive_long_row_min("f64", 2048) == 1020
+    i32 = pf.select(s, "f32", "auto")
+    assert i32.tile == 4096
+
+
+def test_select_long_rows_need_the_combine_kernel():
+    s = make_stats(2000000, 15000000, 200000)
+    i = pf.select(s, "f64", "adaptive")
+    assert i.needs_fixup == 1 and i.guess_spread == 0
+    f = pf.select(s, "f64", "flat")
+    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 2048) and f.needs_fixup == 1
+    p = pf.select(s, "f64", "prefree")
+    assert p.variant == pf.PREFREE and p.tile == 512 and p.ntiles == -(-15000000 // 512)
+
+
+def test_select_rejects_bad_arguments():
+    s = make_stats(10, 10, 1)
+    with pytest.raises(pf.PrefreeError):
+        pf.select(s, 7, "auto")
+
+
+def test_supported_tiles():
+    assert pf.supported_tiles("adaptive", "f64") == [1024, 2048, 4096]
+    assert pf.supported_tiles("flat", "f32") == [2048, 4096]
+    assert pf.supported_tiles("prefree", "f64") == [512, 1024]
+
+
+def test_validation_before_gpu():
+    L = pf.lib()
+    h = ctypes.c_void_p()
+    assert L.pf_plan_create(ctypes.byref(h), None, None, -1, 4, 0, 0, 0, None) == 1
+    assert L.pf_plan_create(ctypes.byref(h), None, None, 4, 4, 0, 9, 0, None) == 1
+    assert L.pf_plan_create(ctypes.byref(h), None, None, 4, 4, 0, 0, 11, None) == 1
+    assert L.pf_plan_create(ctypes.byref(h), 256, 8, 4, 4, 4, 0, 0, None) == 2   # misaligned col
+    assert L.pf_plan_execute(None, None, None, None, None, None, None) == 1
+    m, n, z = ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
+    assert L.pf_synth_dims(9, 1, 0, ctypes.byref(m), ctypes.byref(n), ctypes.byref(z)) == 1
+    assert L.pf_plan_destroy(None) == 0

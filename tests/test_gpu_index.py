@@ -1,0 +1,69 @@
+"""Index-level parity on the GPU (bit-exact integer work).
+
+* The row search each workgroup of k_tiles runs (with and without the
+  interpolated first probe round) must give exactly the tile descriptors of
+  the model in csr_cases.tile_model, which tests/test_tiling_model.py pins by
+  invariants.
+* k_prefree's in-kernel first row per tile must equal the reference pre-pass
+  map, oracle.pre_start_row (restating src/spmv_kernel/preFreeSpMV.cu:3-28).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import prefree_amd as pf
+from csr_cases import edge_cases, tile_model
+from gpu_util import DEV, dev
+
+pytestmark = pytest.mark.gpu
+
+LMAX = {1024: 508, 2048: 1020, 4096: 2044}
+
+
+def cases():
+    out = [(name, rp) for name, rp, _c, _n in edge_cases()]
+    for cfg, scale in ((1, 0), (2, 300), (3, 60000), (4, 400000), (5, 40000)):
+        rp, _, _ = pf.synth_csr(cfg, seed=6, scale_n=scale, dtypes=())
+        out.append((f"C{cfg}", rp))
+    return out
+
+
+CASES = cases()
+
+
+@pytest.mark.parametrize("spread", [0, 1, 64, 1000])
+@pytest.mark.parametrize("tile", [1024, 2048, 4096])
+@pytest.mark.parametrize("merged", [True, False], ids=["adaptive", "flat"])
+def test_tile_descriptors_match_model(merged, tile, spread):
+    for name, rp in CASES:
+        m, nnz = len(rp) - 1, int(rp[-1])
+        if m == 0:
+            continue
+        model = tile_model(rp, tile, merged, LMAX[tile] if merged else 0)
+        ntiles = len(model)
+        out = torch.full((8 * ntiles,), -7, dtype=torch.int32, device=DEV)
+        err = torch.zeros(64, dtype=torch.int32, device=DEV)
+        got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, merged, out, err, guess_spread=spread)
+        torch.cuda.synchronize()
+        assert got_tiles == ntiles
+        got = out.cpu().numpy().reshape(ntiles, 8)[:, :6].astype(np.int64)
+        assert int(err.cpu()[0]) == 0, name
+        bad = np.flatnonzero(np.any(got != model, axis=1))
+        assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
+
+
+@pytest.mark.parametrize("tile", [512, 1024])
+def test_prefree_rows_match_prepass(tile):
+    for name, rp in CASES:
+        m, nnz = len(rp) - 1, int(rp[-1])
+        if nnz == 0:
+            continue
+        ref = oracle.pre_start_row(rp, tile)
+        ntiles = len(ref) - 1
+        out = torch.full((ntiles + 1,), -7, dtype=torch.int32, device=DEV)
+        pf.prefree_rows(dev(rp), m, nnz, tile, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.array_equal(got[:ntiles], ref[:ntiles]), name
+        assert got[ntiles] == m

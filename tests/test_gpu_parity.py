@@ -1,0 +1,129 @@
+"""GPU parity of every variant against the CPU oracle (through the C ABI).
+
+Known-answer inputs (the reference's initVec values, include/common.h:126-133)
+must match the oracle bit for bit; U[-1,1] inputs must be within 1e-12 (f64)
+or 1e-5 (f32) per row, normalised by sum_j |a_ij x_j|, with empty rows exactly
+zero.  y is pre-filled with NaN, so every row must be written.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import prefree_amd as pf
+from csr_cases import edge_cases
+from gpu_util import NP, assert_parity, gpu_spmv, kat_exact_possible
+
+pytestmark = pytest.mark.gpu
+
+CASES = edge_cases()
+VARIANTS = ["adaptive", "flat", "prefree"]
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("case", range(len(CASES)), ids=[c[0] for c in CASES])
+def test_edge_case_kat(case, variant, dtype):
+    name, rp, col, n = CASES[case]
+    val = oracle.initvec(len(col), NP[dtype])
+    x = oracle.initvec(n, NP[dtype])
+    y, _ = gpu_spmv(rp, col, val, x, variant, dtype=dtype)
+    assert_parity(rp, col, val, x, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"{name}/{variant}")
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("case", range(len(CASES)), ids=[c[0] for c in CASES])
+def test_edge_case_random(case, variant, dtype):
+    name, rp, col, n = CASES[case]
+    rng = np.random.default_rng(case)
+    val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+    x = rng.uniform(-1, 1, n).astype(NP[dtype])
+    y, _ = gpu_spmv(rp, col, val, x, variant, dtype=dtype)
+    assert_parity(rp, col, val, x, y, dtype, what=f"{name}/{variant}")
+
+
+SCALED = [(1, 0), (2, 300), (3, 60000), (4, 400000), (5, 40000)]
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("variant", ["auto"] + VARIANTS)
+@pytest.mark.parametrize("cfg,scale", SCALED, ids=[f"C{c}" for c, _ in SCALED])
+def test_scaled_configs(cfg, scale, variant, dtype):
+    rp, col, v = pf.synth_csr(cfg, seed=11, scale_n=scale, dtypes=(dtype,))
+    x = pf.synth_x(cfg, len(rp) - 1, seed=11, dtypes=(dtype,))[dtype]
+    y, info = gpu_spmv(rp, col, v[dtype], x, variant, dtype=dtype)
+    assert_parity(rp, col, v[dtype], x, y, dtype, what=f"C{cfg}/{variant}")
+    kval = oracle.initvec(len(col), NP[dtype])
+    kx = oracle.initvec(len(x), NP[dtype])
+    ky, _ = gpu_spmv(rp, col, kval, kx, variant, dtype=dtype)
+    assert_parity(rp, col, kval, kx, ky, dtype, exact=kat_exact_possible(rp, dtype), what=f"C{cfg}/{variant}/kat")
+
+
+@pytest.mark.parametrize("variant", ["adaptive", "flat"])
+def test_tile_sizes(variant):
+    for dtype in ("f64", "f32"):
+        for tile in pf.supported_tiles(variant, dtype):
+            for name, rp, col, n in CASES[::3]:
+                rng = np.random.default_rng(tile)
+                val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+                x = rng.uniform(-1, 1, n).astype(NP[dtype])
+                y, info = gpu_spmv(rp, col, val, x, variant, tile=tile, dtype=dtype)
+                assert info["tile"] == tile
+                assert_parity(rp, col, val, x, y, dtype, what=f"{name}/{variant}/{tile}")
+
+
+def test_adaptive_short_rows_bit_exact():
+    """Rows of <= 16 products are summed in nnz order by one lane: the oracle's order exactly."""
+    for cfg, scale in ((2, 300), (4, 400000), (1, 0)):
+        rp, col, v = pf.synth_csr(cfg, seed=3, scale_n=scale)
+        x = pf.synth_x(cfg, len(rp) - 1, seed=3)["f64"]
+        y, info = gpu_spmv(rp, col, v["f64"], x, "adaptive")
+        assert info["needs_fixup"] == 0
+        assert_parity(rp, col, v["f64"], x, y, "f64", exact=True, what=f"C{cfg}")
+
+
+@pytest.mark.parametrize("variant", ["adaptive", "flat"])
+def test_deterministic(variant):
+    rp, col, v = pf.synth_csr(5, seed=4, scale_n=40000)
+    x = pf.synth_x(5, len(rp) - 1, seed=4)["f64"]
+    y1, _ = gpu_spmv(rp, col, v["f64"], x, variant)
+    y2, _ = gpu_spmv(rp, col, v["f64"], x, variant, repeat=3)
+    assert np.array_equal(y1, y2)
+
+
+def test_plan_reuse_and_one_shot():
+    import torch
+    from gpu_util import DEV, dev
+    rp, col, v = pf.synth_csr(3, seed=5, scale_n=50000)
+    m = len(rp) - 1
+    d_rp, d_col, d_val = dev(rp), dev(col), dev(v["f64"])
+    stream = torch.cuda.current_stream()
+    with pf.Plan(d_rp, d_col, m, m, len(col), "f64", "auto", stream=stream) as p:
+        for seed in (1, 2):
+            x = pf.synth_x(3, m, seed=seed)["f64"]
+            y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+            p.execute(d_rp, d_col, d_val, dev(x), y, stream=stream)
+            torch.cuda.synchronize()
+            assert_parity(rp, col, v["f64"], x, y.cpu().numpy(), "f64", what=f"reuse {seed}")
+        p.check(stream=stream)
+    x = pf.synth_x(3, m, seed=9)["f64"]
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+    pf.spmv(d_rp, d_col, d_val, dev(x), y, m, m, len(col), "f64", "auto", stream=stream)
+    assert_parity(rp, col, v["f64"], x, y.cpu().numpy(), "f64", what="one-shot")
+
+
+def test_malformed_csr_rejected_at_planning():
+    from gpu_util import dev
+    rp = np.array([0, 2, 1, 4], dtype=np.int32)        # decreasing
+    col = np.array([0, 1, 2, 0], dtype=np.int32)
+    with pytest.raises(pf.PrefreeError) as e:
+        pf.Plan(dev(rp), dev(col), 3, 3, 4, "f64")
+    assert e.value.status == 6
+    rp = np.array([0, 2, 4], dtype=np.int32)
+    col = np.array([0, 5, 1, 2], dtype=np.int32)       # column out of range
+    with pytest.raises(pf.PrefreeError) as e:
+        pf.Plan(dev(rp), dev(col), 2, 3, 4, "f64")
+    assert e.value.status == 6
+    with pytest.raises(pf.PrefreeError) as e:          # row_ptr[m] != nnz
+        pf.Plan(dev(rp), dev(col), 2, 3, 3, "f64")
+    assert e.value.status == 6
