@@ -75,6 +75,7 @@ typedef struct pf_plan_info {
     int long_row_min;     /* ADAPTIVE: rows longer than this are split across tiles */
     int guess_spread;     /* row search: spacing of the interpolated first probe round, 0 = none */
     int needs_fixup;      /* 1 when split rows need the combine kernel */
+    int run_tiles;        /* ADAPTIVE: consecutive tiles walked by one wave64 */
     long long ntiles;     /* logical tiles */
     long long grid;       /* workgroups launched (tiles rounded up to a multiple of the XCD count) */
     size_t workspace_bytes;
@@ -106,6 +107,8 @@ int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m
 int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n,
                          int nnz, int dtype, int variant, int tile, void *stream);
 int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out);
+/* Tuning: consecutive tiles per wave64 of the ADAPTIVE kernel (1..256). */
+int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).

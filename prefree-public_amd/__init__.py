@@ -57,7 +57,8 @@ class RowStats(ctypes.Structure):
 class PlanInfo(ctypes.Structure):
     _fields_ = [("variant", ctypes.c_int), ("dtype", ctypes.c_int), ("tile", ctypes.c_int),
                 ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
-                ("ntiles", ctypes.c_longlong), ("grid", ctypes.c_longlong), ("workspace_bytes", ctypes.c_size_t)]
+                ("run_tiles", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("grid", ctypes.c_longlong),
+                ("workspace_bytes", ctypes.c_size_t)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -70,7 +71,7 @@ class SpmvArgs(ctypes.Structure):
     _fields_ = [("row_ptr", ctypes.c_void_p), ("col", ctypes.c_void_p), ("val", ctypes.c_void_p),
                 ("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("m", ctypes.c_int), ("n", ctypes.c_int),
                 ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
-                ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
+                ("run_tiles", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p)]
 
 
@@ -102,6 +103,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_create, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _vp])
         _sig(L.pf_plan_create_tuned, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
         _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
+        _sig(L.pf_plan_set_run_tiles, [_vp, _i])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
         _sig(L.pf_plan_execute, [_vp, _vp, _vp, _vp, _vp, _vp, _vp])
         _sig(L.pf_plan_check, [_vp, _vp])
@@ -219,6 +221,9 @@ class Plan:
         _check(lib().pf_plan_get_stats(self._h, ctypes.byref(s)), "pf_plan_get_stats")
         return s
 
+    def set_run_tiles(self, run_tiles):
+        _check(lib().pf_plan_set_run_tiles(self._h, int(run_tiles)), "pf_plan_set_run_tiles")
+
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),
                "pf_plan_execute")
@@ -250,12 +255,12 @@ def spmv(row_ptr, col, val, x, y, m, n, nnz, dtype="f64", variant="auto", stream
                          dtype_code(dtype), variant_code(variant), _s(stream)), "pf_spmv")
 
 
-def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, stream=None):
+def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, run_tiles=0, stream=None):
     """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT into `out` (int32[8*ntiles])."""
     total = nnz + m if merged else nnz
     ntiles = max(1, -(-total // tile))
-    a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread, ntiles=ntiles,
-                 err_flag=_p(err_flag))
+    a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
+                 run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag))
     _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
            "pfk_debug_tile_desc")
     return ntiles

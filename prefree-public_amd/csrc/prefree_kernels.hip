@@ -37,6 +37,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 using namespace pfdev;
 
 namespace {
@@ -58,16 +60,20 @@ struct Args {
     int nnz;
     int guess_spread;
     long long ntiles;
-    long long g8;        // tiles per XCD (ceil(ntiles / 8))
+    long long g8;        // k_tiles: tiles per XCD (ceil(ntiles / 8))
+    long long tx;        // k_stream: tiles per XCD
+    long long tpw;       // k_stream: tiles per workgroup
     T *__restrict__ head;
     T *__restrict__ tail;
     int *__restrict__ owner;
     int *__restrict__ err;
 };
 
-// Long-row threshold of ADAPTIVE for tile size K: keeps a tile's nnz span
-// (at most K + LMAX - 1, plus 3 for 16-byte alignment) within 1.5 K.
-constexpr int adaptive_lmax(int K) { return K / 2 - 4; }
+// Long-row threshold of ADAPTIVE for tile size K (keys per wave tile).  A
+// tile's nnz span is at most K + LMAX - 1 plus 3 for 16-byte alignment; the
+// sizes are chosen so that it fits one (fp64) or two (fp32) 4-nnz vectors per
+// lane of a wave64.
+constexpr int adaptive_lmax(int K) { return K <= 188 ? 64 : (K <= 440 ? 64 : K / 2 - 4); }
 
 // Logical tile of this workgroup: XCD x (= blockIdx % 8) takes the contiguous
 // tiles [x*g8, (x+1)*g8), so neighbouring rows (and their x entries) share an L2.
@@ -77,43 +83,46 @@ __device__ __forceinline__ long long xcd_tile(long long g8)
     return (b % kXcds) * g8 + b / kXcds;
 }
 
-// ---- 16-byte streaming loads of 4 consecutive nnz -------------------------
+// ---- 16-byte streaming loads through buffer resources ----------------------
+//
+// Every col / val / row_ptr load is a raw buffer load against a resource that
+// spans exactly the bytes the workgroup may read.  The hardware range-checks
+// each dword (a 16-byte load straddling the end returns the dwords inside and
+// zeros for the rest, without touching memory beyond it), so the loads need no
+// per-lane bounds branch and a lane past the end costs no traffic.
 
-__device__ __forceinline__ void load4(const int *__restrict__ col, const double *__restrict__ val,
-                                      int e0, int nnz, int (&c)[4], double (&v)[4])
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit elements
+constexpr int kAuxNt = 2;               // cache policy bit 1: non-temporal (streamed once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, long long bytes)
 {
-    if (e0 + 4 <= nnz) {
-        const i32x4 cc = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(col + e0));
-        const f64x2 v0 = __builtin_nontemporal_load(reinterpret_cast<const f64x2 *>(val + e0));
-        const f64x2 v1 = __builtin_nontemporal_load(reinterpret_cast<const f64x2 *>(val + e0 + 2));
-        c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
-        v[0] = v0.x; v[1] = v0.y; v[2] = v1.x; v[3] = v1.y;
-    } else {  // the last vector of the matrix
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool in = e0 + j < nnz;
-            c[j] = in ? col[e0 + j] : 0;
-            v[j] = in ? val[e0 + j] : 0.0;
-        }
-    }
+    const long long b = bytes < 0 ? 0 : (bytes > 0x40000000ll ? 0x40000000ll : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)b, kRsrcWord3);
 }
 
-__device__ __forceinline__ void load4(const int *__restrict__ col, const float *__restrict__ val,
-                                      int e0, int nnz, int (&c)[4], float (&v)[4])
+// col and val of the 4 consecutive nnz at 16-byte vector `vec` of a resource pair.
+__device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
+                                      double (&v)[4])
 {
-    if (e0 + 4 <= nnz) {
-        const i32x4 cc = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(col + e0));
-        const f32x4 vv = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(val + e0));
-        c[0] = cc.x; c[1] = cc.y; c[2] = cc.z; c[3] = cc.w;
-        v[0] = vv.x; v[1] = vv.y; v[2] = vv.z; v[3] = vv.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool in = e0 + j < nnz;
-            c[j] = in ? col[e0 + j] : 0;
-            v[j] = in ? val[e0 + j] : 0.0f;
-        }
-    }
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, kAuxNt);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32, 0, kAuxNt);
+    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32 + 16, 0, kAuxNt);
+    c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
+    v[0] = __hiloint2double((int)v0.y, (int)v0.x);
+    v[1] = __hiloint2double((int)v0.w, (int)v0.z);
+    v[2] = __hiloint2double((int)v1.y, (int)v1.x);
+    v[3] = __hiloint2double((int)v1.w, (int)v1.z);
+}
+
+__device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
+                                      float (&v)[4])
+{
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, kAuxNt);
+    const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 16, 0, kAuxNt);
+    c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
+    v[0] = __int_as_float((int)vv.x); v[1] = __int_as_float((int)vv.y);
+    v[2] = __int_as_float((int)vv.z); v[3] = __int_as_float((int)vv.w);
 }
 
 __device__ __forceinline__ void store4(double *s, const double (&p)[4])
@@ -231,6 +240,132 @@ struct TileShape {
     static constexpr int kBlockCap = (K + LMAX) / (kWaveMax + 1) + 1;
 };
 
+// ---- pieces shared by k_tiles and k_stream ---------------------------------
+
+// Issue the 16-byte loads of the tile's col/val vectors (4 nnz each,
+// lane-strided) for the nnz range [base, B); lanes past B read zeros.
+template <typename T, int VPT>
+__device__ __forceinline__ void issue_cv(const Args<T> &a, int base, int B, int nvec, int (&c)[VPT][4],
+                                         T (&v)[VPT][4])
+{
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + base, (long long)(B - base) * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + base, (long long)(B - base) * (long long)sizeof(T));
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+        if (k * kBS < nvec)  // uniform: skip whole vector slots past the tile
+            load4(rc, rv, (int)threadIdx.x + k * kBS, c[k], v[k]);
+}
+
+// Gather x (ordinary loads: x stays in L2 / MALL).  Lanes past the tile hold
+// column 0 and gather x[0]; their products are masked later.
+template <typename T, int VPT>
+__device__ __forceinline__ void gather_x(const Args<T> &a, int nvec, const int (&c)[VPT][4], T (&xv)[VPT][4])
+{
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+        if (k * kBS < nvec)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[k][j] = a.x[c[k][j]];
+}
+
+// val * x, rounded, into LDS (no contraction with the later sums).
+template <typename T, int VPT>
+__device__ __forceinline__ void products_to_lds(T *s_prod, int base, int nvec, int A, int B, const T (&v)[VPT][4],
+                                                const T (&xv)[VPT][4])
+{
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int vec = threadIdx.x + k * kBS;
+        if (vec < nvec) {
+            T p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = base + 4 * vec + j;
+                p[j] = (e >= A && e < B) ? v[k][j] * xv[k][j] : T(0);
+            }
+            store4(s_prod + 4 * vec, p);
+        }
+    }
+}
+
+template <typename T, int WCAP, int BCAP>
+struct ReduceLds {
+    int nw, nb;
+    int wl[WCAP], wa[WCAP], wb[WCAP];
+    int bl[BCAP], ba[BCAP], bb[BCAP];
+    T red[kWaves];
+};
+
+// Row sums of a tile whose products sit in s_prod (index = nnz - base).
+// bounds(i, ra, rb) gives row_ptr[r], row_ptr[r+1] of local row i; put(i, s)
+// stores the sum.  Rows of <= kThreadMax products: one lane each, summed in
+// nnz order; <= kWaveMax: one wave each (DPP sum); longer: the workgroup.
+// Whole workgroup; L.nw / L.nb must be 0 on entry and are 0 again on exit.
+template <typename T, int WCAP, int BCAP, typename Bounds, typename Put>
+__device__ __forceinline__ void reduce_tile(const T *s_prod, ReduceLds<T, WCAP, BCAP> &L, int base, int A, int B,
+                                            int nr, Bounds bounds, Put put)
+{
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    for (int i = tid; i < nr; i += kBS) {
+        int ra, rb;
+        bounds(i, ra, rb);
+        ra = max(ra, A);
+        rb = min(rb, B);
+        const int a0 = ra - base;
+        const int len = rb - ra;
+        if (len <= kThreadMax) {
+            T s = T(0);
+            for (int q = 0; q < len; ++q)
+                s += s_prod[a0 + q];
+            put(i, s);
+        } else if (len <= kWaveMax) {
+            const int j = atomicAdd(&L.nw, 1);
+            if (j < WCAP) { L.wl[j] = i; L.wa[j] = a0; L.wb[j] = a0 + len; }
+        } else {
+            const int j = atomicAdd(&L.nb, 1);
+            if (j < BCAP) { L.bl[j] = i; L.ba[j] = a0; L.bb[j] = a0 + len; }
+        }
+    }
+    __syncthreads();
+    const int nw = min(L.nw, WCAP);
+    for (int j = wave; j < nw; j += kWaves) {
+        T s = T(0);
+        for (int q = L.wa[j] + lane; q < L.wb[j]; q += kWave)
+            s += s_prod[q];
+        s = wave_sum(s);
+        if (lane == 0)
+            put(L.wl[j], s);
+    }
+    const int nb = min(L.nb, BCAP);
+    for (int j = 0; j < nb; ++j) {
+        T s = T(0);
+        for (int q = L.ba[j] + tid; q < L.bb[j]; q += kBS)
+            s += s_prod[q];
+        s = wave_sum(s);
+        if (lane == 0)
+            L.red[wave] = s;
+        __syncthreads();
+        if (tid == 0) {
+            T tot = L.red[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w)
+                tot += L.red[w];
+            put(L.bl[j], tot);
+        }
+        __syncthreads();
+    }
+    __syncthreads();
+    if (tid == 0) {
+        L.nw = 0;
+        L.nb = 0;
+    }
+}
+
+// ---- k_tiles: one tile per workgroup (FLAT, and the reference for k_stream) --
+
 template <typename T, bool MERGE, int K, int LMAX>
 __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
 {
@@ -238,14 +373,9 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     __shared__ __attribute__((aligned(16))) T s_prod[S::kProd];
     __shared__ int s_rows[2];
     __shared__ int s_desc[6];
-    __shared__ int s_nw, s_nb;
-    __shared__ int s_wl[S::kWaveCap], s_wa[S::kWaveCap], s_wb[S::kWaveCap];
-    __shared__ int s_bl[S::kBlockCap], s_ba[S::kBlockCap], s_bb[S::kBlockCap];
-    __shared__ T s_red[kWaves];
+    __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
 
     const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = tid / kWave;
     const long long t = xcd_tile(a.g8);
     if (t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping
@@ -260,8 +390,8 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
                                                                 s_rows[1], a.err);
         s_desc[0] = d.lo_row; s_desc[1] = d.nr; s_desc[2] = d.A; s_desc[3] = d.B;
         s_desc[4] = d.head; s_desc[5] = d.tail;
-        s_nw = 0;
-        s_nb = 0;
+        L.nw = 0;
+        L.nb = 0;
         a.owner[t] = d.tail ? d.lo_row + d.nr - 1 : -1;
     }
     __syncthreads();
@@ -270,91 +400,445 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     const int base = A & ~3;
     const int nvec = B > A ? (B - base + 3) >> 2 : 0;
 
-    // Stream col/val (16-byte non-temporal loads), gather x, products -> LDS.
     int c[S::kVPT][4];
-    T v[S::kVPT][4];
+    T v[S::kVPT][4], xv[S::kVPT][4];
+    issue_cv(a, base, B, nvec, c, v);
+    gather_x(a, nvec, c, xv);
+    products_to_lds(s_prod, base, nvec, A, B, v, xv);
+    __syncthreads();
+
+    const int *__restrict__ rp = a.rp;
+    reduce_tile(
+        s_prod, L, base, A, B, nr,
+        [&](int i, int &ra, int &rb) { ra = rp[lo_row + i]; rb = rp[lo_row + i + 1]; },
+        [&](int i, T s) {
+            if (head && i == 0) a.head[t] = s;
+            else if (tail && i == nr - 1) a.tail[t] = s;
+            else a.y[lo_row + i] = s;
+        });
+}
+
+// ---- k_wave: wave-granular persistent, software-pipelined ADAPTIVE kernel ----
+//
+// Every wave64 is an independent streaming agent: it walks a contiguous run of
+// tiles (XCD x owns tiles [x*tx, (x+1)*tx), split evenly over the waves
+// resident on it) with no workgroup barrier anywhere.  Only the first tile of
+// a run searches row_ptr; every later tile starts at the row where the
+// previous one stopped and finds its last row by a ballot over a block of
+// row_ptr held in registers (lane i holds entries i, i+64, i+128).  Three
+// tiles are in flight per wave: while the products of tile t are summed, the
+// col/val stream of tile t+1 and the row_ptr block of tile t+2 are loading.
+// LDS is wave-private scratch (products, row bounds, long-row list); LDS
+// operations of one wave execute in order, so no barrier is needed.
+//
+// The loop body issues a fixed sequence of memory operations: every load and
+// store is an unconditional buffer operation, lanes with nothing to do use an
+// offset outside the resource (dropped by the hardware, no traffic).  The
+// compiler can then count outstanding operations exactly and waits only for
+// the data it consumes, so the next tiles' loads stay in flight.
+
+constexpr uint32_t kOob = 0xFFFFFFF0u;  // byte offset beyond every resource
+
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, double v)
+{
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, int v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32((unsigned int)v, r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, double *)
+{
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// A resource over a whole array addressed with 32-bit byte offsets (the plan
+// guarantees it stays below 4 GiB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_full(const void *base, long long bytes)
+{
+    const long long b = bytes < 0 ? 0 : (bytes > (long long)kOob ? (long long)kOob : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)(unsigned int)b, kRsrcWord3);
+}
+
+__device__ __forceinline__ int rlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+template <typename T, int K, int LMAX>
+struct WaveShape {
+    static constexpr int kSpanMax = K + LMAX + 2;              // B - (A & ~3) <= K + LMAX - 1 + 3
+    static constexpr int kVecMax = (kSpanMax + 3) / 4;
+    static constexpr int kVPT = (kVecMax + kWave - 1) / kWave; // 4-nnz vector slots per lane
+    static constexpr int kProd = kVPT * kWave * 4;             // products per wave
+    static constexpr int kRPL = 3;                             // row_ptr entries per lane per round
+    static constexpr int kRB = kRPL * kWave;                   // entries per round
+    static constexpr int kRpCap = K + 2;                       // rows + 2 of any tile
+    static constexpr int kRounds = (kRpCap + kRB - 1) / kRB;
+    static constexpr int kQ = (K + 1 + kWave - 1) / kWave;     // local-row slots per lane (<= K+1 rows)
+    static constexpr int kListCap = (K + LMAX) / (kThreadMax + 1) + 1;
+};
+
+constexpr int kWaveWG = 256;  // 4 independent waves per workgroup
+
+struct WaveDesc {
+    int f;       // first owned row; block entry j = row_ptr[f-1+j]
+    int l;       // one past the last owned row
+    int lo_row, nr, A, B, head, tail;
+};
+
+// Round `r0` of the row_ptr block of a tile whose owned rows start at f:
+// entry j = row_ptr[f-1+j] for j in [r0*kRB, (r0+1)*kRB); 0 for j = 0 when
+// f == 0 and past row m.  valid == false reads nothing.
+template <int RPL>
+__device__ __forceinline__ void rp_issue(const int *__restrict__ rp, int m, int f, bool valid, int r0, int (&rr)[RPL])
+{
+    const int b0 = f > 0 ? f - 1 : 0;
+    const int shift = f - 1 - b0;  // -1 when f == 0: entry 0 addresses byte -4, out of range
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(rp + b0, valid ? (long long)(m + 1 - b0) * 4 : 0);
+    const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-    for (int k = 0; k < S::kVPT; ++k) {
-        const int vec = tid + k * kBS;
-        if (vec < nvec)
-            load4(a.col, a.val, base + 4 * vec, a.nnz, c[k], v[k]);
+    for (int q = 0; q < RPL; ++q)
+        rr[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(r, (r0 * RPL * kWave + q * kWave + lane + shift) * 4, 0, 0);
+}
+
+// Entry j of a block round held in registers (j uniform, 0 <= j < kRB).
+template <int RPL>
+__device__ __forceinline__ int rp_entry(const int (&rr)[RPL], int j)
+{
+    int v = 0;
+#pragma unroll
+    for (int q = 0; q < RPL; ++q)
+        if (j >= q * kWave && j < (q + 1) * kWave) v = rlane(rr[q], j - q * kWave);
+    return v;
+}
+
+// Smallest block index j >= 1 in round r0 whose row reaches key ke (rows past
+// m count as reaching it), or -1.
+template <int RPL>
+__device__ __forceinline__ int rp_find(const int (&rr)[RPL], int r0, int f, int m, uint32_t ke)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int q = 0; q < RPL; ++q) {
+        const int j = r0 * RPL * kWave + q * kWave + lane;
+        const int row = f - 1 + j;
+        const bool ge = j >= 1 && (row >= m || (uint32_t)rr[q] + (uint32_t)row >= ke);
+        const uint64_t mask = __ballot(ge);
+        if (mask) return r0 * RPL * kWave + q * kWave + __ffsll((long long)mask) - 1;
     }
-#pragma unroll
-    for (int k = 0; k < S::kVPT; ++k) {
-        const int vec = tid + k * kBS;
-        if (vec < nvec) {
-            T p[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int e = base + 4 * vec + j;
-                p[j] = (e >= A && e < B) ? v[k][j] * a.x[c[k][j]] : T(0);
+    return -1;
+}
+
+// The tile descriptor of a tile with keys [kb, ke) whose owned rows start at
+// f.  rr holds round 0 of its row_ptr block; a tile with more than kRB-1 rows
+// scans further rounds with synchronous loads.  Wave-uniform result.
+template <int RPL, int ROUNDS, int LMAX, int SPAN_MAX>
+__device__ __forceinline__ WaveDesc wave_desc(const int *__restrict__ rp, int m, int nnz, int f, uint32_t kb,
+                                              uint32_t ke, const int (&rr)[RPL], int &err)
+{
+    constexpr int RB = RPL * kWave;
+    int js = rp_find(rr, 0, f, m, ke);
+    int pe = 0, qe = 0;
+    if (js >= 1) {
+        pe = rp_entry(rr, js - 1);
+        qe = js < RB ? rp_entry(rr, js) : 0;
+    }
+    if (js < 0 || js >= RB) {  // rare: the tile's last row lies beyond round 0
+        int tmp[RPL];
+        int prev = rp_entry(rr, RB - 1);
+        int r = 1;
+        if (js >= RB) r = 1;  // js == RB impossible (index < RB); kept for clarity
+        for (js = -1; r < ROUNDS && js < 0; ++r) {
+            rp_issue(rp, m, f, true, r, tmp);
+            js = rp_find(tmp, r, f, m, ke);
+            if (js >= 0) {
+                const int jl = js - r * RB;
+                pe = jl >= 1 ? rp_entry(tmp, jl - 1) : prev;
+                qe = rp_entry(tmp, jl);
+            } else {
+                prev = rp_entry(tmp, RB - 1);
             }
-            store4(s_prod + 4 * vec, p);
+        }
+        if (js < 0) {  // more rows than keys: row_ptr changed after planning
+            err = 1;
+            js = 1;
+            pe = qe = rp_entry(rr, 1);
         }
     }
-    __syncthreads();
-
-    auto put = [&](int i, T s) {
-        if (head && i == 0)
-            a.head[t] = s;
-        else if (tail && i == nr - 1)
-            a.tail[t] = s;
-        else
-            a.y[lo_row + i] = s;
-    };
-
-    // Rows of <= kThreadMax products: one lane each, sequential in nnz order.
-    for (int i = tid; i < nr; i += kBS) {
-        const int r = lo_row + i;
-        const int ra = max(a.rp[r], A);
-        const int rb = min(a.rp[r + 1], B);
-        const int a0 = ra - base;
-        const int len = rb - ra;
-        if (len <= kThreadMax) {
-            T s = T(0);
-            for (int q = 0; q < len; ++q)
-                s += s_prod[a0 + q];
-            put(i, s);
-        } else if (len <= kWaveMax) {
-            const int j = atomicAdd(&s_nw, 1);
-            if (j < S::kWaveCap) { s_wl[j] = i; s_wa[j] = a0; s_wb[j] = a0 + len; }
+    const int l = f - 1 + js;
+    WaveDesc d{f, l, 0, 0, 0, 0, 0, 0};
+    const int h = f - 1;
+    const int ph = rp_entry(rr, 0), qh = rp_entry(rr, 1);
+    if (h >= 0) {
+        const long long jk = (long long)kb - h;
+        if (qh - ph > LMAX && jk < qh) {
+            d.head = 1;
+            d.A = (int)jk;
+        }
+    }
+    d.lo_row = d.head ? h : f;
+    if (f < l) {
+        if (!d.head) d.A = qh;
+        const long long jend = (long long)ke - (l - 1);
+        if (qe - pe > LMAX && (long long)qe > jend) {
+            d.B = (int)jend;
+            d.tail = 1;
         } else {
-            const int j = atomicAdd(&s_nb, 1);
-            if (j < S::kBlockCap) { s_bl[j] = i; s_ba[j] = a0; s_bb[j] = a0 + len; }
+            d.B = qe;
         }
+    } else if (d.head) {
+        const long long jend = (long long)ke - h;
+        d.B = (long long)qh < jend ? qh : (int)jend;
     }
-    __syncthreads();
-
-    // Rows of <= kWaveMax products: one wave each.
-    const int nw = min(s_nw, S::kWaveCap);
-    for (int j = wave; j < nw; j += kWaves) {
-        T s = T(0);
-        for (int q = s_wa[j] + lane; q < s_wb[j]; q += kWave)
-            s += s_prod[q];
-        s = wave_sum(s);
-        if (lane == 0)
-            put(s_wl[j], s);
+    d.nr = l - d.lo_row;
+    const bool ok = d.lo_row >= 0 && d.nr >= 0 && (long long)d.lo_row + d.nr <= m && d.A >= 0 && d.A <= d.B &&
+                    d.B <= nnz && d.B - (d.A & ~3) <= SPAN_MAX;
+    if (!ok) {
+        err = 1;
+        d.lo_row = f; d.nr = 0; d.A = 0; d.B = 0; d.head = 0; d.tail = 0;
     }
+    return d;
+}
 
-    // Longer rows: the whole workgroup.
-    const int nb = min(s_nb, S::kBlockCap);
-    for (int j = 0; j < nb; ++j) {
-        T s = T(0);
-        for (int q = s_ba[j] + tid; q < s_bb[j]; q += kBS)
-            s += s_prod[q];
-        s = wave_sum(s);
-        if (lane == 0)
-            s_red[wave] = s;
-        __syncthreads();
-        if (tid == 0) {
-            T tot = s_red[0];
+// col/val of a tile (an empty descriptor reads nothing).
+template <typename T, int VPT>
+__device__ __forceinline__ void wave_issue_cv(const Args<T> &a, const WaveDesc &d, int (&c)[VPT][4], T (&v)[VPT][4])
+{
+    const int base = d.A & ~3;
+    const long long n = d.B > d.A ? d.B - base : 0;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + base, n * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + base, n * (long long)sizeof(T));
+    const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w)
-                tot += s_red[w];
-            put(s_bl[j], tot);
-        }
-        __syncthreads();
+    for (int k = 0; k < VPT; ++k)
+        load4(rc, rv, lane + k * kWave, c[k], v[k]);
+}
+
+template <typename T, int VPT>
+__device__ __forceinline__ void wave_gather(__amdgpu_buffer_rsrc_t rx, int nvec, const int (&c)[VPT][4],
+                                            T (&xv)[VPT][4])
+{
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const bool in = lane + k * kWave < nvec;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xv[k][j] = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
     }
+}
+
+// Row bounds of a tile into the wave's LDS block: round 0 from registers,
+// the rare rows beyond it straight from row_ptr.
+template <int RPL, int CAP>
+__device__ __forceinline__ void rp_to_lds(const int *__restrict__ rp, const WaveDesc &d, const int (&rr)[RPL], int *s_rpb)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+    for (int q = 0; q < RPL; ++q)
+        if (q * kWave + lane < CAP) s_rpb[q * kWave + lane] = rr[q];
+    const int nent = d.l - d.f + 2;  // entries f-1 .. l
+    if (nent > RPL * kWave)
+        for (int j = RPL * kWave + lane; j < nent && j < CAP; j += kWave)
+            s_rpb[j] = rp[d.f - 1 + j];
+}
+
+// DESC_ONLY: write every tile's descriptor to dbg (8 ints per tile) instead of
+// computing y — the index test of this exact code path.
+// Waves per SIMD the register allocation targets: 7 (72 VGPRs) for one
+// 4-nnz vector per lane, fewer for larger tiles.
+template <typename T, int K, int LMAX>
+constexpr int wave_occupancy() { return WaveShape<T, K, LMAX>::kVPT == 1 ? 7 : 4; }
+
+template <typename T, int K, int LMAX, bool DESC_ONLY, int WPE = wave_occupancy<T, K, LMAX>()>
+__global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_wave(Args<T> a, int *__restrict__ dbg)
+{
+    using S = WaveShape<T, K, LMAX>;
+    constexpr int VPT = S::kVPT, Q = S::kQ, RPL = S::kRPL, LCAP = S::kListCap, CAP = S::kRpCap;
+    constexpr int NW = kWaveWG / kWave;
+    __shared__ __attribute__((aligned(16))) T s_prod_all[NW][DESC_ONLY ? 4 : S::kProd];
+    __shared__ int s_rpb_all[NW][2][DESC_ONLY ? 4 : CAP];
+    __shared__ int s_la_all[NW][LCAP], s_lb_all[NW][LCAP];
+    __shared__ T s_ls_all[NW][LCAP];
+    __shared__ T s_chunk_all[NW][2];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    T *s_prod = s_prod_all[wave];
+    int *s_la = s_la_all[wave];
+    int *s_lb = s_lb_all[wave];
+    T *s_ls = s_ls_all[wave];
+    T *s_chunk = s_chunk_all[wave];
+
+    // Run of a.tpw consecutive tiles: XCD x owns runs [x*tx, (x+1)*tx), taken
+    // in dispatch order, so the tiles in flight on an XCD form a narrow front
+    // and their x entries stay in its L2.
+    const long long xcd = blockIdx.x % kXcds;
+    const long long wx = (blockIdx.x / kXcds) * NW + wave;  // run index inside its XCD
+    if (wx >= a.tx)
+        return;  // whole wave: no barrier in this kernel
+    long long t = (xcd * a.tx + wx) * a.tpw;
+    long long t_end = t + a.tpw;
+    if (t_end > a.ntiles) t_end = a.ntiles;
+    if (t >= t_end)
+        return;
+
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc_full(a.y, (long long)a.m * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rowner = make_rsrc_full(a.owner, a.ntiles * 4);
+    int err = 0;
+
+    uint32_t kb, ke;
+    bool last;
+    tile_keys<true>(t, a.ntiles, K, a.m, a.nnz, kb, ke, last);
+    const int f0 = wave_search_lt<true>(a.rp, a.m, kb, key_guess<true>(kb, a.m, a.nnz), a.guess_spread, lane) + 1;
+    int rr[RPL];
+    rp_issue(a.rp, a.m, f0, true, 0, rr);
+    WaveDesc d = wave_desc<RPL, S::kRounds, LMAX, S::kSpanMax>(a.rp, a.m, a.nnz, f0, kb, ke, rr, err);
+    int buf = 0;
+    if (!DESC_ONLY) rp_to_lds<RPL, CAP>(a.rp, d, rr, s_rpb_all[wave][0]);
+    rp_issue(a.rp, a.m, d.l, t + 1 < t_end, 0, rr);
+    int c[VPT][4];
+    T v[VPT][4];
+    if (!DESC_ONLY) wave_issue_cv(a, d, c, v);
+
+    for (;;) {
+        if (DESC_ONLY && lane == 0) {
+            int *o = dbg + 8 * t;
+            o[0] = d.lo_row; o[1] = d.nr; o[2] = d.A; o[3] = d.B; o[4] = d.head; o[5] = d.tail;
+            o[6] = d.f; o[7] = d.l;
+        }
+        const int base = d.A & ~3;
+        const int nvec = d.B > d.A ? (d.B - base + 3) >> 2 : 0;
+        T xv[VPT][4], vt[VPT][4];
+        if (!DESC_ONLY) {
+            wave_gather(rx, nvec, c, xv);
+#pragma unroll
+            for (int k = 0; k < VPT; ++k)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vt[k][j] = v[k][j];
+        }
+
+        // Next tile: its row_ptr block was issued one iteration ago.
+        const bool more = t + 1 < t_end;
+        WaveDesc dn{d.l, d.l, d.l, 0, 0, 0, 0, 0};
+        if (more) {
+            uint32_t kbn, ken;
+            bool lastn;
+            tile_keys<true>(t + 1, a.ntiles, K, a.m, a.nnz, kbn, ken, lastn);
+            dn = wave_desc<RPL, S::kRounds, LMAX, S::kSpanMax>(a.rp, a.m, a.nnz, d.l, kbn, ken, rr, err);
+            if (!DESC_ONLY) rp_to_lds<RPL, CAP>(a.rp, dn, rr, s_rpb_all[wave][buf ^ 1]);
+        }
+        rp_issue(a.rp, a.m, dn.l, t + 2 < t_end, 0, rr);
+        if (!DESC_ONLY) wave_issue_cv(a, dn, c, v);
+
+        if (!DESC_ONLY) {
+            const int *s_rpb = s_rpb_all[wave][buf];
+            // Products of tile t (waits for its x gathers only).
+#pragma unroll
+            for (int k = 0; k < VPT; ++k) {
+                const int vec = lane + k * kWave;
+                T p[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = base + 4 * vec + j;
+                    p[j] = (e >= d.A && e < d.B) ? vt[k][j] * xv[k][j] : T(0);
+                }
+                store4(s_prod + 4 * vec, p);
+            }
+            __builtin_amdgcn_wave_barrier();
+
+            // Pass 1: rows of <= kThreadMax products, one lane each in nnz
+            // order, stored at once; longer rows are listed for the wave.
+            // Every lane issues exactly Q stores here and Q in pass 3.
+            const int jo = d.lo_row - (d.f - 1);  // block index of local row 0
+            int tag[Q];
+            int nl = 0;
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int i = lane + q * kWave;
+                tag[q] = -1;
+                bool lng = false;
+                int a0 = 0, a1 = 0;
+                T s = T(0);
+                if (q * kWave < d.nr) {
+                    if (i < d.nr) {
+                        a0 = max(s_rpb[jo + i], d.A) - base;
+                        a1 = min(s_rpb[jo + i + 1], d.B) - base;
+                        if (a1 - a0 <= kThreadMax) {
+#pragma unroll 4
+                            for (int p = a0; p < a1; ++p)
+                                s += s_prod[p];
+                        } else {
+                            lng = true;
+                        }
+                    }
+                    const uint64_t mask = __ballot(lng);
+                    if (mask) {
+                        const int pos = nl + (int)__builtin_amdgcn_mbcnt_hi(
+                                                 (unsigned)(mask >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
+                        if (lng && pos < LCAP) { s_la[pos] = a0; s_lb[pos] = a1; tag[q] = pos; }
+                        nl += __popcll(mask);
+                    }
+                }
+                const bool in = i < d.nr && !lng;
+                const bool hd = d.head && i == 0;
+                const bool tl = d.tail && i == d.nr - 1;
+                if (in && hd) s_chunk[0] = s;
+                if (in && tl) s_chunk[1] = s;
+                buf_store(ry, in && !hd && !tl ? (uint32_t)(d.lo_row + i) * (uint32_t)sizeof(T) : kOob, s);
+            }
+            __builtin_amdgcn_wave_barrier();
+            // Pass 2: one listed row at a time, all 64 lanes, DPP sum.
+            nl = min(nl, LCAP);
+            for (int j = 0; j < nl; ++j) {
+                T s = T(0);
+                const int e1 = s_lb[j];
+                for (int p = s_la[j] + lane; p < e1; p += kWave)
+                    s += s_prod[p];
+                s = wave_sum(s);
+                if (lane == 0) s_ls[j] = s;
+            }
+            __builtin_amdgcn_wave_barrier();
+            // Pass 3: the listed rows, Q stores per lane.
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int i = lane + q * kWave;
+                const bool in = tag[q] >= 0;
+                const T s = in ? s_ls[tag[q]] : T(0);
+                const bool hd = d.head && i == 0;
+                const bool tl = d.tail && i == d.nr - 1;
+                if (in && hd) s_chunk[0] = s;
+                if (in && tl) s_chunk[1] = s;
+                buf_store(ry, in && !hd && !tl ? (uint32_t)(d.lo_row + i) * (uint32_t)sizeof(T) : kOob, s);
+            }
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t tslot = (uint32_t)t * (uint32_t)sizeof(T);
+            buf_store(rhead, lane == 0 && d.head ? tslot : kOob, s_chunk[0]);
+            buf_store(rtail, lane == 0 && d.tail ? tslot : kOob, s_chunk[1]);
+            buf_store(rowner, lane == 0 ? (uint32_t)t * 4u : kOob, d.tail ? d.lo_row + d.nr - 1 : -1);
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (!more)
+            break;
+        ++t;
+        d = dn;
+        buf ^= 1;
+    }
+    if (err && lane == 0) atomicOr(a.err, 1);
 }
 
 // Debug: the descriptor every tile of k_tiles computes.
@@ -461,20 +945,23 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
         if (lane == 0) s_rows[1] = r;
     }
 
-    // Product stage (:416-428), 16-byte loads.
+    // Product stage (:416-428): 16-byte buffer loads of this tile's nnz;
+    // positions past nnz read zeros and give zero products.
+    const int tile_nnz = min(TT, a.nnz - (int)first);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + first, (long long)tile_nnz * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + first, (long long)tile_nnz * (long long)sizeof(T));
+    int c[VPT][4];
+    T v[VPT][4];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k)
+        load4(rc, rv, tid + k * kPfBS, c[k], v[k]);
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int off = 4 * (tid + k * kPfBS);
-        const int e0 = (int)first + off;
-        T p[4] = {T(0), T(0), T(0), T(0)};
-        if (e0 < a.nnz) {
-            int c[4];
-            T v[4];
-            load4(a.col, a.val, e0, a.nnz, c, v);
+        T p[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                p[j] = (e0 + j < a.nnz) ? v[j] * a.x[c[j]] : T(0);
-        }
+        for (int j = 0; j < 4; ++j)
+            p[j] = (off + j < tile_nnz) ? v[k][j] * a.x[c[k][j]] : T(0);
         store4(s_prod + off, p);
     }
     __syncthreads();
@@ -681,6 +1168,8 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.guess_spread = a->guess_spread;
     r.ntiles = a->ntiles;
     r.g8 = (a->ntiles + kXcds - 1) / kXcds;
+    r.tx = r.g8;
+    r.tpw = 1;
     r.head = static_cast<T *>(a->head_slot);
     r.tail = static_cast<T *>(a->tail_slot);
     r.owner = a->owner_row;
@@ -713,33 +1202,82 @@ int launch_tiles(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
-template <typename T, bool MERGE>
-int dispatch_tiles(const pfk_spmv_args *a, void *stream)
+int device_cus()
+{
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus[dev] = 256;
+    return cus[dev];
+}
+
+// Runs of `run` consecutive tiles, one run per wave, 4 waves per workgroup;
+// XCD x takes runs [x*tx, (x+1)*tx).
+template <typename T>
+void wave_grid(Args<T> &r, int run, long long &grid)
+{
+    constexpr long long NW = kWaveWG / kWave;
+    const long long nruns = (r.ntiles + run - 1) / run;
+    r.tpw = run;
+    r.tx = (nruns + kXcds - 1) / kXcds;
+    grid = ((r.tx + NW - 1) / NW) * kXcds;
+}
+
+template <typename T, int K, int LMAX, bool DESC_ONLY>
+int launch_stream(const pfk_spmv_args *a, int *dbg, void *stream)
+{
+    Args<T> r = make_args<T>(a);
+    long long grid = 0;
+    wave_grid<T>(r, a->run_tiles > 0 ? a->run_tiles : 8, grid);
+    hipLaunchKernelGGL((k_wave<T, K, LMAX, DESC_ONLY>), dim3((unsigned)grid), dim3(kWaveWG), 0, S(stream), r, dbg);
+    PFK_LAUNCHED("k_wave");
+    return PF_OK;
+}
+
+template <typename T>
+int dispatch_adaptive(const pfk_spmv_args *a, void *stream)
 {
     if constexpr (sizeof(T) == 8) {
         switch (a->tile) {
-        case 1024: return launch_tiles<T, MERGE, 1024, MERGE ? adaptive_lmax(1024) : 0>(a, stream);
-        case 2048: return launch_tiles<T, MERGE, 2048, MERGE ? adaptive_lmax(2048) : 0>(a, stream);
-        case 4096: return launch_tiles<T, MERGE, 4096, MERGE ? adaptive_lmax(4096) : 0>(a, stream);
+        case 188: return launch_stream<T, 188, adaptive_lmax(188), false>(a, nullptr, stream);
+        case 512: return launch_stream<T, 512, adaptive_lmax(512), false>(a, nullptr, stream);
         }
     } else {
         switch (a->tile) {
-        case 2048: return launch_tiles<T, MERGE, 2048, MERGE ? adaptive_lmax(2048) : 0>(a, stream);
-        case 4096: return launch_tiles<T, MERGE, 4096, MERGE ? adaptive_lmax(4096) : 0>(a, stream);
+        case 440: return launch_stream<T, 440, adaptive_lmax(440), false>(a, nullptr, stream);
+        case 1024: return launch_stream<T, 1024, adaptive_lmax(1024), false>(a, nullptr, stream);
         }
     }
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
     return PF_ERR_UNSUPPORTED;
 }
 
-template <bool MERGE, int K>
-int launch_desc(const pfk_spmv_args *a, int *out, void *stream)
+template <typename T>
+int dispatch_flat(const pfk_spmv_args *a, void *stream)
 {
-    constexpr int LMAX = MERGE ? adaptive_lmax(K) : 0;
+    if constexpr (sizeof(T) == 8) {
+        switch (a->tile) {
+        case 1024: return launch_tiles<T, false, 1024, 0>(a, stream);
+        case 2048: return launch_tiles<T, false, 2048, 0>(a, stream);
+        case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
+        }
+    } else {
+        switch (a->tile) {
+        case 2048: return launch_tiles<T, false, 2048, 0>(a, stream);
+        case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
+        }
+    }
+    snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
+    return PF_ERR_UNSUPPORTED;
+}
+
+template <int K>
+int launch_flat_desc(const pfk_spmv_args *a, int *out, void *stream)
+{
     Args<double> r = make_args<double>(a);
     const long long grid = r.g8 * kXcds;
-    hipLaunchKernelGGL((k_tile_desc<MERGE, K, LMAX, K + LMAX + 2>), dim3((unsigned)grid), dim3(kBS), 0,
-                       S(stream), r, out);
+    hipLaunchKernelGGL((k_tile_desc<false, K, 0, K + 2>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, out);
     PFK_LAUNCHED("k_tile_desc");
     return PF_OK;
 }
@@ -752,16 +1290,16 @@ int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream)
 {
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, true)) return PF_ERR_INVALID;
-    return dtype == PF_F64 ? dispatch_tiles<double, true>(a, stream)
-         : dtype == PF_F32 ? dispatch_tiles<float, true>(a, stream) : PF_ERR_INVALID;
+    return dtype == PF_F64 ? dispatch_adaptive<double>(a, stream)
+         : dtype == PF_F32 ? dispatch_adaptive<float>(a, stream) : PF_ERR_INVALID;
 }
 
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
 {
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, true)) return PF_ERR_INVALID;
-    return dtype == PF_F64 ? dispatch_tiles<double, false>(a, stream)
-         : dtype == PF_F32 ? dispatch_tiles<float, false>(a, stream) : PF_ERR_INVALID;
+    return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
+         : dtype == PF_F32 ? dispatch_flat<float>(a, stream) : PF_ERR_INVALID;
 }
 
 int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream)
@@ -811,17 +1349,19 @@ int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream)
 
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
 {
-    static const int f64_tiles[] = {1024, 2048, 4096};
-    static const int f32_tiles[] = {2048, 4096};
-    static const int pf_tiles[] = {512, 1024};
+    static const int ad64[] = {188, 512};        // k_wave: keys per wave tile
+    static const int ad32[] = {440, 1024};
+    static const int fl64[] = {1024, 2048, 4096}; // k_tiles: nnz per workgroup tile
+    static const int fl32[] = {2048, 4096};
+    static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
     if (variant == PF_PREFREE) { src = pf_tiles; n = 2; }
-    else if (variant == PF_ADAPTIVE || variant == PF_FLAT) {
-        if (dtype == PF_F64) { src = f64_tiles; n = 3; }
-        else if (dtype == PF_F32) { src = f32_tiles; n = 2; }
-        else return 0;
-    } else return 0;
+    else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 2; }
+    else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 2; }
+    else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 3; }
+    else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 2; }
+    else return 0;
     for (int i = 0; i < n && i < cap; ++i) tiles[i] = src[i];
     return n;
 }
@@ -858,10 +1398,17 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
 {
     (void)dtype;
     if (!a || !a->row_ptr || !d_out || !a->err_flag || a->m <= 0 || a->ntiles < 1) return PF_ERR_INVALID;
-    switch (a->tile) {
-    case 1024: return merged_keys ? launch_desc<true, 1024>(a, d_out, stream) : launch_desc<false, 1024>(a, d_out, stream);
-    case 2048: return merged_keys ? launch_desc<true, 2048>(a, d_out, stream) : launch_desc<false, 2048>(a, d_out, stream);
-    case 4096: return merged_keys ? launch_desc<true, 4096>(a, d_out, stream) : launch_desc<false, 4096>(a, d_out, stream);
+    if (merged_keys) {  // the descriptors of the k_stream code path itself
+        switch (a->tile) {
+        case 188: return launch_stream<double, 188, adaptive_lmax(188), true>(a, d_out, stream);
+        case 512: return launch_stream<double, 512, adaptive_lmax(512), true>(a, d_out, stream);
+        }
+    } else {
+        switch (a->tile) {
+        case 1024: return launch_flat_desc<1024>(a, d_out, stream);
+        case 2048: return launch_flat_desc<2048>(a, d_out, stream);
+        case 4096: return launch_flat_desc<4096>(a, d_out, stream);
+        }
     }
     return PF_ERR_UNSUPPORTED;
 }

@@ -40,6 +40,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int default_tile(int variant, int dtype)
 {
     if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
+    if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 188 : 440;
     return dtype == PF_F64 ? 2048 : 4096;
 }
 
@@ -69,6 +70,7 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     r.guess_spread = regular ? 64 : 0;
     const long long vb = value_bytes(dtype);
     if (variant == PF_ADAPTIVE) {
+        r.run_tiles = 8;
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
         const long long total = nnz + m;
         r.ntiles = total > 0 ? (total + tile - 1) / tile : 1;
@@ -172,6 +174,10 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
     if (m > 0 && !d_row_ptr) return fail(PF_ERR_INVALID, "row_ptr is NULL");
     if ((unsigned long long)nnz + (unsigned long long)m >= 0xFFFFFFFFull)
         return fail(PF_ERR_UNSUPPORTED, "nnz + m must stay below 2^32");
+    // x and y are addressed through buffer resources with 32-bit byte offsets.
+    if ((unsigned long long)n * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull ||
+        (unsigned long long)m * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull)
+        return fail(PF_ERR_UNSUPPORTED, "x and y must each stay below 4 GiB");
     if (d_col && !aligned16(d_col)) return fail(PF_ERR_ALIGN, "col not 16-byte aligned");
     if (nnz > 0 && m == 0) return fail(PF_ERR_CSR, "nnz > 0 with no rows");
 
@@ -236,6 +242,13 @@ int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out)
     return PF_OK;
 }
 
+int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles)
+{
+    if (!plan || run_tiles < 1 || run_tiles > 256) return fail(PF_ERR_INVALID, "run_tiles must be in 1..256");
+    plan->info.run_tiles = run_tiles;
+    return PF_OK;
+}
+
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out)
 {
     if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
@@ -262,6 +275,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.nnz = plan->nnz;
     a.tile = plan->info.tile;
     a.guess_spread = plan->info.guess_spread;
+    a.run_tiles = plan->info.run_tiles;
     a.ntiles = plan->info.ntiles;
     a.head_slot = plan->head;
     a.tail_slot = plan->tail;

@@ -77,13 +77,13 @@ def make_stats(m, nnz, max_len, empty=0):
 def test_select_auto_is_adaptive_with_default_tiles():
     s = make_stats(4194304, 20963328, 5)
     i = pf.select(s, "f64", "auto")
-    assert i.variant == pf.ADAPTIVE and i.tile == 2048
-    assert i.ntiles == -(-(20963328 + 4194304) // 2048)
+    assert i.variant == pf.ADAPTIVE and i.tile == 188
+    assert i.ntiles == -(-(20963328 + 4194304) // 188)
     assert i.grid % 8 == 0 and i.grid >= i.ntiles
     assert i.needs_fixup == 0 and i.guess_spread == 64
-    assert i.long_row_min == pf.adaptive_long_row_min("f64", 2048) == 1020
+    assert i.long_row_min == pf.adaptive_long_row_min("f64", 188) == 64
     i32 = pf.select(s, "f32", "auto")
-    assert i32.tile == 4096
+    assert i32.tile == 440
 
 
 def test_select_long_rows_need_the_combine_kernel():
@@ -103,7 +103,9 @@ def test_select_rejects_bad_arguments():
 
 
 def test_supported_tiles():
-    assert pf.supported_tiles("adaptive", "f64") == [1024, 2048, 4096]
+    assert pf.supported_tiles("adaptive", "f64") == [188, 512]
+    assert pf.supported_tiles("adaptive", "f32") == [440, 1024]
+    assert pf.supported_tiles("flat", "f64") == [1024, 2048, 4096]
     assert pf.supported_tiles("flat", "f32") == [2048, 4096]
     assert pf.supported_tiles("prefree", "f64") == [512, 1024]
 

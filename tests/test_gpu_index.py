@@ -18,7 +18,7 @@ from gpu_util import DEV, dev
 
 pytestmark = pytest.mark.gpu
 
-LMAX = {1024: 508, 2048: 1020, 4096: 2044}
+LMAX = {188: 64, 440: 64, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
 
 
 def cases():
@@ -32,10 +32,13 @@ def cases():
 CASES = cases()
 
 
-@pytest.mark.parametrize("spread", [0, 1, 64, 1000])
-@pytest.mark.parametrize("tile", [1024, 2048, 4096])
-@pytest.mark.parametrize("merged", [True, False], ids=["adaptive", "flat"])
-def test_tile_descriptors_match_model(merged, tile, spread):
+TILES = [(True, t) for t in pf.supported_tiles("adaptive", "f64")] + \
+        [(False, t) for t in pf.supported_tiles("flat", "f64")]
+
+
+@pytest.mark.parametrize("spread,run", [(0, 0), (1, 1), (64, 3), (1000, 8), (64, 64)])
+@pytest.mark.parametrize("merged,tile", TILES, ids=[("adaptive" if mg else "flat") + str(t) for mg, t in TILES])
+def test_tile_descriptors_match_model(merged, tile, spread, run):
     for name, rp in CASES:
         m, nnz = len(rp) - 1, int(rp[-1])
         if m == 0:
@@ -44,7 +47,7 @@ def test_tile_descriptors_match_model(merged, tile, spread):
         ntiles = len(model)
         out = torch.full((8 * ntiles,), -7, dtype=torch.int32, device=DEV)
         err = torch.zeros(64, dtype=torch.int32, device=DEV)
-        got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, merged, out, err, guess_spread=spread)
+        got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, merged, out, err, guess_spread=spread, run_tiles=run)
         torch.cuda.synchronize()
         assert got_tiles == ntiles
         got = out.cpu().numpy().reshape(ntiles, 8)[:, :6].astype(np.int64)

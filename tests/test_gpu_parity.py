@@ -72,6 +72,29 @@ def test_tile_sizes(variant):
                 assert_parity(rp, col, val, x, y, dtype, what=f"{name}/{variant}/{tile}")
 
 
+@pytest.mark.parametrize("run", [1, 2, 5, 16, 64])
+def test_adaptive_run_lengths(run):
+    """Any number of consecutive tiles per wave gives the same (bit-identical) y."""
+    import torch
+    from gpu_util import DEV, dev
+    for cfg, scale in ((3, 60000), (5, 40000), (4, 400000)):
+        rp, col, v = pf.synth_csr(cfg, seed=8, scale_n=scale)
+        m = len(rp) - 1
+        x = pf.synth_x(cfg, m, seed=8)["f64"]
+        d = [dev(rp), dev(col), dev(v["f64"]), dev(x)]
+        ys = []
+        for r in (8, run):
+            y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+            with pf.Plan(d[0], d[1], m, m, len(col), "f64", "adaptive") as p:
+                p.set_run_tiles(r)
+                p.execute(*d, y)
+                torch.cuda.synchronize()
+                p.check()
+            ys.append(y.cpu().numpy())
+        assert np.array_equal(ys[0], ys[1])
+        assert_parity(rp, col, v["f64"], x, ys[1], "f64", what=f"C{cfg} run {run}")
+
+
 def test_adaptive_short_rows_bit_exact():
     """Rows of <= 16 products are summed in nnz order by one lane: the oracle's order exactly."""
     for cfg, scale in ((2, 300), (4, 400000), (1, 0)):

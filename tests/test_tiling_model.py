@@ -12,7 +12,7 @@ import pytest
 import prefree_amd as pf
 from csr_cases import check_tiling, edge_cases, tile_model
 
-LMAX = {1024: 508, 2048: 1020, 4096: 2044}
+LMAX = {188: 64, 440: 64, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
 
 
 def all_cases():
@@ -23,7 +23,7 @@ def all_cases():
     return cases
 
 
-@pytest.mark.parametrize("tile", [1024, 2048, 4096])
+@pytest.mark.parametrize("tile", [188, 440, 512, 1024, 2048, 4096])
 @pytest.mark.parametrize("merged", [True, False], ids=["adaptive", "flat"])
 def test_model_satisfies_invariants(tile, merged):
     lmax = LMAX[tile] if merged else 0
@@ -34,14 +34,15 @@ def test_model_satisfies_invariants(tile, merged):
 
 def test_adaptive_tiles_are_balanced():
     for name, rp in all_cases():
-        desc = tile_model(rp, 2048, True, 1020)
+        desc = tile_model(rp, 188, True, 64)
         work = desc[:, 1] + (desc[:, 3] - desc[:, 2])   # rows + nnz of each tile
-        assert work.max() <= 2048 + 1020 + 1, name
+        assert work.max() <= 188 + 64 + 1, name
 
 
 def test_lmax_matches_kernel_library():
-    for tile, lmax in LMAX.items():
-        assert pf.adaptive_long_row_min("f64", tile) == lmax
+    for dt in ("f64", "f32"):
+        for tile in pf.supported_tiles("adaptive", dt):
+            assert pf.adaptive_long_row_min(dt, tile) == LMAX[tile]
 
 
 @pytest.mark.parametrize("mutation", ["shift_A", "drop_row", "flip_head", "flip_tail", "short_B"])
