@@ -438,6 +438,10 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
 // the data it consumes, so the next tiles' loads stay in flight.
 
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // byte offset beyond every resource
+#ifndef PF_STORE_AUX
+#define PF_STORE_AUX 0
+#endif
+constexpr int kStoreAux = PF_STORE_AUX;  // cache policy of the y stores
 
 __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, double v)
 {
@@ -453,6 +457,21 @@ __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off
 __device__ __forceinline__ void buf_store(__amdgpu_buffer_rsrc_t r, uint32_t off, int v)
 {
     __builtin_amdgcn_raw_buffer_store_b32((unsigned int)v, r, (int)off, 0, 0);
+}
+
+// 16 bytes of consecutive values; the hardware range check drops the dwords
+// past the resource's end, so a lane straddling it writes only its in-range rows.
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, const double (&w)[2])
+{
+    const u32x4 v = {(unsigned)__double2loint(w[0]), (unsigned)__double2hiint(w[0]), (unsigned)__double2loint(w[1]),
+                     (unsigned)__double2hiint(w[1])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kStoreAux);
+}
+
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&w)[4])
+{
+    const u32x4 v = {__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]), __float_as_uint(w[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kStoreAux);
 }
 
 __device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, double *)
@@ -487,6 +506,8 @@ struct WaveShape {
     static constexpr int kRounds = (kRpCap + kRB - 1) / kRB;
     static constexpr int kQ = (K + 1 + kWave - 1) / kWave;     // local-row slots per lane (<= K+1 rows)
     static constexpr int kListCap = (K + LMAX) / (kThreadMax + 1) + 1;
+    static constexpr int kQS = (K + 1 + kWave * (16 / (int)sizeof(T)) - 1) / (kWave * (16 / (int)sizeof(T)));  // 16-byte y stores per lane
+    static_assert(kProd >= K + 1, "row sums are staged in the product buffer");
 };
 
 constexpr int kWaveWG = 256;  // 4 independent waves per workgroup
@@ -671,7 +692,11 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     __shared__ int s_rpb_all[NW][2][DESC_ONLY ? 4 : CAP];
     __shared__ int s_la_all[NW][LCAP], s_lb_all[NW][LCAP];
     __shared__ T s_ls_all[NW][LCAP];
-    __shared__ T s_chunk_all[NW][2];
+    // Row sums staged for the y stores: a buffer of their own when LDS allows
+    // (one 4-nnz vector per lane), else the product buffer after the sums.
+    constexpr bool YL = S::kVPT == 1 && !DESC_ONLY;
+    __shared__ __attribute__((aligned(16))) T s_y_all[NW][YL ? K + 1 : 1];
+    __shared__ int s_li_all[NW][YL ? LCAP : 1];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -679,7 +704,8 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     int *s_la = s_la_all[wave];
     int *s_lb = s_lb_all[wave];
     T *s_ls = s_ls_all[wave];
-    T *s_chunk = s_chunk_all[wave];
+    T *s_y = YL ? s_y_all[wave] : s_prod;
+    int *s_li = s_li_all[wave];
 
     // Run of a.tpw consecutive tiles: XCD x owns runs [x*tx, (x+1)*tx), taken
     // in dispatch order, so the tiles in flight on an XCD form a narrow front
@@ -762,26 +788,29 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             __builtin_amdgcn_wave_barrier();
 
             // Pass 1: rows of <= kThreadMax products, one lane each in nnz
-            // order, stored at once; longer rows are listed for the wave.
-            // Every lane issues exactly Q stores here and Q in pass 3.
+            // order; longer rows are listed for pass 2.  The sums go to s_y
+            // (YL) or are kept in registers until the products are consumed.
             const int jo = d.lo_row - (d.f - 1);  // block index of local row 0
-            int tag[Q];
+            int tag[YL ? 1 : Q];
+            T sq[YL ? 1 : Q];
             int nl = 0;
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
                 const int i = lane + q * kWave;
-                tag[q] = -1;
-                bool lng = false;
-                int a0 = 0, a1 = 0;
-                T s = T(0);
+                if (!YL) { tag[q] = -1; sq[q] = T(0); }
                 if (q * kWave < d.nr) {
+                    bool lng = false;
+                    int a0 = 0, a1 = 0;
                     if (i < d.nr) {
                         a0 = max(s_rpb[jo + i], d.A) - base;
                         a1 = min(s_rpb[jo + i + 1], d.B) - base;
                         if (a1 - a0 <= kThreadMax) {
+                            T s = T(0);
 #pragma unroll 4
                             for (int p = a0; p < a1; ++p)
                                 s += s_prod[p];
+                            if (!YL) sq[q] = s;
+                            if (YL) s_y[i] = s;
                         } else {
                             lng = true;
                         }
@@ -790,16 +819,14 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
                     if (mask) {
                         const int pos = nl + (int)__builtin_amdgcn_mbcnt_hi(
                                                  (unsigned)(mask >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
-                        if (lng && pos < LCAP) { s_la[pos] = a0; s_lb[pos] = a1; tag[q] = pos; }
+                        if (lng && pos < LCAP) {
+                            s_la[pos] = a0;
+                            s_lb[pos] = a1;
+                            if (YL) s_li[pos] = i; else tag[q] = pos;
+                        }
                         nl += __popcll(mask);
                     }
                 }
-                const bool in = i < d.nr && !lng;
-                const bool hd = d.head && i == 0;
-                const bool tl = d.tail && i == d.nr - 1;
-                if (in && hd) s_chunk[0] = s;
-                if (in && tl) s_chunk[1] = s;
-                buf_store(ry, in && !hd && !tl ? (uint32_t)(d.lo_row + i) * (uint32_t)sizeof(T) : kOob, s);
             }
             __builtin_amdgcn_wave_barrier();
             // Pass 2: one listed row at a time, all 64 lanes, DPP sum.
@@ -810,25 +837,46 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
                 for (int p = s_la[j] + lane; p < e1; p += kWave)
                     s += s_prod[p];
                 s = wave_sum(s);
-                if (lane == 0) s_ls[j] = s;
+                if (lane == 0) {
+                    if (YL) s_y[s_li[j]] = s; else s_ls[j] = s;
+                }
             }
             __builtin_amdgcn_wave_barrier();
-            // Pass 3: the listed rows, Q stores per lane.
+            // Pass 3 (registers): every row sum into s_prod[local row].
+            if (!YL) {
 #pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const int i = lane + q * kWave;
-                const bool in = tag[q] >= 0;
-                const T s = in ? s_ls[tag[q]] : T(0);
-                const bool hd = d.head && i == 0;
-                const bool tl = d.tail && i == d.nr - 1;
-                if (in && hd) s_chunk[0] = s;
-                if (in && tl) s_chunk[1] = s;
-                buf_store(ry, in && !hd && !tl ? (uint32_t)(d.lo_row + i) * (uint32_t)sizeof(T) : kOob, s);
+                for (int q = 0; q < Q; ++q) {
+                    const int i = lane + q * kWave;
+                    if (q * kWave < d.nr && i < d.nr)
+                        s_y[i] = tag[q] >= 0 ? s_ls[tag[q]] : sq[q];
+                }
+                __builtin_amdgcn_wave_barrier();
             }
-            __builtin_amdgcn_wave_barrier();
+            // 16-byte stores of consecutive rows: a fixed number of store
+            // instructions, the resource spanning exactly the rows this tile
+            // owns (the split rows at its edges go to the head / tail slots).
+            const int r0 = d.head;                 // first local row written to y
+            const int nw = d.nr - d.head - d.tail; // rows written to y
+            const __amdgpu_buffer_rsrc_t ryt =
+                make_rsrc(a.y + (d.lo_row + r0), (long long)nw * (long long)sizeof(T));
+#pragma unroll
+            for (int q = 0; q < S::kQS; ++q) {
+                constexpr int P = 16 / (int)sizeof(T);
+                const int j = (q * kWave + lane) * P;
+                T w[P];
+#pragma unroll
+                for (int p = 0; p < P; ++p) w[p] = T(0);
+                if (j < nw) {
+#pragma unroll
+                    for (int p = 0; p < P; ++p) w[p] = s_y[r0 + j + p < K + 1 ? r0 + j + p : 0];
+                }
+                buf_store16(ryt, j < nw ? (uint32_t)j * (uint32_t)sizeof(T) : kOob, w);
+            }
             const uint32_t tslot = (uint32_t)t * (uint32_t)sizeof(T);
-            buf_store(rhead, lane == 0 && d.head ? tslot : kOob, s_chunk[0]);
-            buf_store(rtail, lane == 0 && d.tail ? tslot : kOob, s_chunk[1]);
+            const T hv = s_y[0];
+            const T tv = s_y[d.nr > 0 ? d.nr - 1 : 0];
+            buf_store(rhead, lane == 0 && d.head ? tslot : kOob, hv);
+            buf_store(rtail, lane == 0 && d.tail ? tslot : kOob, tv);
             buf_store(rowner, lane == 0 ? (uint32_t)t * 4u : kOob, d.tail ? d.lo_row + d.nr - 1 : -1);
             __builtin_amdgcn_wave_barrier();
         }
@@ -865,6 +913,12 @@ __global__ __launch_bounds__(kBS) void k_tile_desc(Args<double> a, int *__restri
 
 // ---- k_fixup: combine the partials of split rows in tile order -------------
 
+// One thread per tile: a split row that ends within kFixSerial tiles of the
+// tile where it starts is summed by that thread, head slots in tile order; a
+// longer one is listed and summed by a wave (lane-strided partials, DPP sum).
+// Both orders are fixed functions of the tiling, so y is reproducible.
+constexpr int kFixSerial = 16;
+
 template <typename T, bool MERGE>
 __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
 {
@@ -876,21 +930,32 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
     if (tid == 0) s_n = 0;
     __syncthreads();
     const long long t0 = (long long)blockIdx.x * kBS;
-    if (t0 + tid < a.ntiles && a.owner[t0 + tid] >= 0)
-        s_list[atomicAdd(&s_n, 1)] = tid;
+    const long long t = t0 + tid;
+    const int r = t < a.ntiles ? a.owner[t] : -1;
+    if (r >= 0) {
+        const long long last_key = (long long)a.rp[r + 1] - 1 + (MERGE ? r : 0);
+        const long long tb = last_key / K;  // last tile holding a piece of row r
+        if (tb - t <= kFixSerial) {
+            T s = T(0);
+            for (long long u = t + 1; u <= tb; ++u)
+                s += a.head[u];
+            a.y[r] = a.tail[t] + s;
+        } else {
+            s_list[atomicAdd(&s_n, 1)] = tid;
+        }
+    }
     __syncthreads();
     const int n = s_n;
     for (int j = wave; j < n; j += kWaves) {
-        const long long t = t0 + s_list[j];
-        const int r = a.owner[t];
-        const long long last_key = (long long)a.rp[r + 1] - 1 + (MERGE ? r : 0);
-        const long long tb = last_key / K;  // last tile holding a piece of row r
+        const long long tl = t0 + s_list[j];
+        const int rl = a.owner[tl];
+        const long long tb = ((long long)a.rp[rl + 1] - 1 + (MERGE ? rl : 0)) / K;
         T s = T(0);
-        for (long long u = t + 1 + lane; u <= tb; u += kWave)
+        for (long long u = tl + 1 + lane; u <= tb; u += kWave)
             s += a.head[u];
         s = wave_sum(s);
         if (lane == 0)
-            a.y[r] = a.tail[t] + s;
+            a.y[rl] = a.tail[tl] + s;
     }
 }
 
