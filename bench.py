@@ -39,6 +39,9 @@ WORKLOADS = {
 }
 
 
+KERNELS = {"adaptive": "k_wave", "flat": "k_tiles", "prefree": "k_prefree"}
+
+
 def load_pkg():
     spec = importlib.util.spec_from_file_location("prefree_amd", os.path.join(PKG_DIR, "__init__.py"),
                                                   submodule_search_locations=[PKG_DIR])
@@ -95,6 +98,9 @@ def main():
     ap.add_argument("--cold-steps", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the measurement, copy a 256 MiB buffer 3 times (known bytes, for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -171,11 +177,20 @@ def main():
     cold_ms /= max(1, args.cold_steps)
     del flush
 
+    if args.copy_calibration:
+        src = torch.ones(1 << 25, dtype=torch.float64, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     y_gpu = d_y.cpu().numpy()
     bytes_eff = (nnz + m + n) * vb + nnz * 4 + (m + 1) * 4          # test/test_cdspmv.cpp:305
     bytes_gather = (2 * nnz + m) * vb + nnz * 4 + (m + 1) * 4       # test/test_cdspmv.cpp:306
     gbs = bytes_eff / (ms_kernel * 1e-3) / 1e9
-    key = f"C{args.config}-{dt}-{info['variant_name']}-{info['tile']}"
+    key = f"C{args.config}-{dt}-{info['variant_name']}-{info['tile']}" + (
+        f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "")
 
     result = {
         "metric": METRIC,
@@ -193,6 +208,7 @@ def main():
         "config": {"workload": WORKLOADS[args.config] + ("" if dt == "f64" else " (fp32)"),
                    "cfg": f"C{args.config}", "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
                    "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
+                   "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
                    "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3)},
         "gbps_effective": round(gbs, 1),
         "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
@@ -200,7 +216,7 @@ def main():
                         "source": "test/test_cdspmv.cpp:305-306"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profiles(key),
-                     "kernel": "k_tiles" if info["variant_name"] != "prefree" else "k_prefree",
+                     "kernel": KERNELS[info["variant_name"]],
                      "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
                      "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},

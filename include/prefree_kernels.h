@@ -54,6 +54,9 @@ int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap);
 /* Long-row threshold the ADAPTIVE kernel uses for a tile size (-1 if unsupported). */
 int pfk_adaptive_long_row_min(int dtype, int tile);
+/* Wave64s of the ADAPTIVE kernel for (dtype, tile) resident on the current device at once
+ * (occupancy per CU x CUs); sizes the tile runs so that one dispatch round covers the matrix. */
+int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves);
 
 /* Row statistics.  d_out: 44 unsigned long long (layout in prefree_kernels.hip). */
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,

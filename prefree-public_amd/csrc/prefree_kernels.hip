@@ -1300,7 +1300,19 @@ int launch_stream(const pfk_spmv_args *a, int *dbg, void *stream)
     return PF_OK;
 }
 
+// Wave64s of k_wave<T, K> resident on the whole device at once.
+template <typename T, int K>
+int wave_residency(long long *waves)
+{
+    int per_cu = 0;
+    PFK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void *>(&k_wave<T, K, adaptive_lmax(K), false>), kWaveWG, 0));
+    *waves = (long long)per_cu * (kWaveWG / kWave) * device_cus();
+    return PF_OK;
+}
+
 template <typename T>
+
 int dispatch_adaptive(const pfk_spmv_args *a, void *stream)
 {
     if constexpr (sizeof(T) == 8) {
@@ -1365,6 +1377,18 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     if (!args_ok(a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream) : PF_ERR_INVALID;
+}
+
+int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves)
+{
+    if (!waves) return PF_ERR_INVALID;
+    *waves = 0;
+    if (dtype == PF_F64 && tile == 188) return wave_residency<double, 188>(waves);
+    if (dtype == PF_F64 && tile == 512) return wave_residency<double, 512>(waves);
+    if (dtype == PF_F32 && tile == 440) return wave_residency<float, 440>(waves);
+    if (dtype == PF_F32 && tile == 1024) return wave_residency<float, 1024>(waves);
+    snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", tile);
+    return PF_ERR_UNSUPPORTED;
 }
 
 int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream)

@@ -40,8 +40,47 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int default_tile(int variant, int dtype)
 {
     if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
-    if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 188 : 440;
-    return dtype == PF_F64 ? 2048 : 4096;
+    if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 512 : 440;
+    return 4096;
+}
+
+// Wave64s of the ADAPTIVE kernel resident at once on an MI355X (256 CUs x 4
+// SIMDs x the waves per SIMD the gfx950 build of each tile size reaches).
+// Used when no device is queried (pf_select); plans ask the device.
+long long nominal_resident_waves(int dtype, int tile)
+{
+    const int per_simd = dtype == PF_F64 ? (tile == 188 ? 7 : 3) : (tile == 440 ? 5 : 2);
+    return 256LL * 4 * per_simd;
+}
+
+// Consecutive tiles per wave: enough that every resident wave gets one run
+// (a single dispatch round, no tail of half-empty rounds), at most 16 so the
+// runs in flight on an XCD stay close together in x.
+int choose_run(long long ntiles, long long resident)
+{
+    if (resident <= 0) return 8;
+    long long r = (ntiles + resident - 1) / resident;
+    return (int)(r < 1 ? 1 : (r > 16 ? 16 : r));
+}
+
+// PF_AUTO: FLAT for very short rows (fewer than 3 nnz per row on average: the
+// merged tiles spend most keys on rows) and for short-row matrices that also
+// hold split rows (power-law); ADAPTIVE otherwise, with the small tile when the
+// matrix is too small to give every resident wave of the large one a tile.
+void auto_choice(const pf_row_stats &s, int dtype, int &variant, int &tile)
+{
+    const long long m = s.m, nnz = s.nnz;
+    const int big = default_tile(PF_ADAPTIVE, dtype);
+    const bool very_short = m > 0 && nnz < 3 * m;
+    const bool split_rows = s.max_row_len > pfk_adaptive_long_row_min(dtype, big);
+    if (very_short || (split_rows && nnz < 16 * m)) {
+        variant = PF_FLAT;
+        tile = default_tile(PF_FLAT, dtype);
+        return;
+    }
+    variant = PF_ADAPTIVE;
+    tile = big;
+    if (dtype == PF_F64 && (nnz + m) / big < nominal_resident_waves(dtype, big) / 2) tile = 188;
 }
 
 bool tile_supported(int variant, int dtype, int tile)
@@ -51,6 +90,20 @@ bool tile_supported(int variant, int dtype, int tile)
     for (int i = 0; i < n; ++i)
         if (t[i] == tile) return true;
     return false;
+}
+
+// Workgroups launched: ADAPTIVE runs of run_tiles tiles, four waves per
+// workgroup, runs dealt evenly to the XCDs; one tile per workgroup otherwise.
+void set_grid(pf_plan_info &r)
+{
+    if (r.variant == PF_ADAPTIVE) {
+        const long long run = r.run_tiles > 0 ? r.run_tiles : 1;
+        const long long nruns = (r.ntiles + run - 1) / run;
+        const long long tx = (nruns + kXcds - 1) / kXcds;
+        r.grid = ((tx + 3) / 4) * kXcds;
+    } else {
+        r.grid = ((r.ntiles + kXcds - 1) / kXcds) * kXcds;
+    }
 }
 
 // Fills everything in `info` that follows from (stats, dtype, variant, tile).
@@ -70,10 +123,10 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     r.guess_spread = regular ? 64 : 0;
     const long long vb = value_bytes(dtype);
     if (variant == PF_ADAPTIVE) {
-        r.run_tiles = 8;
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
         const long long total = nnz + m;
         r.ntiles = total > 0 ? (total + tile - 1) / tile : 1;
+        r.run_tiles = choose_run(r.ntiles, nominal_resident_waves(dtype, tile));
         r.needs_fixup = s.max_row_len > r.long_row_min;
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
     } else if (variant == PF_FLAT) {
@@ -89,7 +142,7 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     } else {
         return fail(PF_ERR_INVALID, "unknown variant");
     }
-    r.grid = ((r.ntiles + kXcds - 1) / kXcds) * kXcds;
+    set_grid(r);
     *info = r;
     return PF_OK;
 }
@@ -159,9 +212,12 @@ int pf_select(const pf_row_stats *stats, int dtype, int variant, pf_plan_info *o
 {
     if (!stats || !out || value_bytes(dtype) == 0)
         return fail(PF_ERR_INVALID, "pf_select: bad argument");
+    int tile = 0;
     if (variant == PF_AUTO)
-        variant = PF_ADAPTIVE;
-    return finish_info(*stats, dtype, variant, default_tile(variant, dtype), out);
+        auto_choice(*stats, dtype, variant, tile);
+    else
+        tile = default_tile(variant, dtype);
+    return finish_info(*stats, dtype, variant, tile, out);
 }
 
 int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz,
@@ -193,10 +249,21 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
                                         std::to_string(s.row_ptr_last) + " decreasing=" +
                                         std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
     }
-    if (variant == PF_AUTO) variant = PF_ADAPTIVE;
     pf_plan_info info;
+    if (variant == PF_AUTO) {  // an explicit tile is kept only if the chosen variant has it
+        int t = 0;
+        auto_choice(s, dtype, variant, t);
+        if (tile <= 0 || !tile_supported(variant, dtype, tile)) tile = t;
+    }
     const int st = finish_info(s, dtype, variant, tile > 0 ? tile : default_tile(variant, dtype), &info);
     if (st != PF_OK) return st;
+    if (info.variant == PF_ADAPTIVE) {
+        long long resident = 0;
+        if (pfk_adaptive_resident_waves(dtype, info.tile, &resident) == PF_OK && resident > 0) {
+            info.run_tiles = choose_run(info.ntiles, resident);
+            set_grid(info);
+        }
+    }
 
     pf_plan *p = new pf_plan();
     p->m = m;
@@ -246,6 +313,7 @@ int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles)
 {
     if (!plan || run_tiles < 1 || run_tiles > 256) return fail(PF_ERR_INVALID, "run_tiles must be in 1..256");
     plan->info.run_tiles = run_tiles;
+    set_grid(plan->info);
     return PF_OK;
 }
 

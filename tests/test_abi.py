@@ -74,24 +74,55 @@ def make_stats(m, nnz, max_len, empty=0):
     return s
 
 
-def test_select_auto_is_adaptive_with_default_tiles():
+def run_for(ntiles, resident):
+    return max(1, min(16, -(-ntiles // resident)))
+
+
+def test_select_auto_banded_is_adaptive_large_tile():
+    """C2 shape: short regular rows -> ADAPTIVE, 512 keys per tile, runs sized to 3072 resident waves."""
     s = make_stats(4194304, 20963328, 5)
     i = pf.select(s, "f64", "auto")
-    assert i.variant == pf.ADAPTIVE and i.tile == 188
-    assert i.ntiles == -(-(20963328 + 4194304) // 188)
-    assert i.grid % 8 == 0 and i.grid >= i.ntiles
+    assert i.variant == pf.ADAPTIVE and i.tile == 512
+    assert i.ntiles == -(-(20963328 + 4194304) // 512)
+    assert i.run_tiles == run_for(i.ntiles, 256 * 4 * 3) == 16
+    nruns = -(-i.ntiles // i.run_tiles)
+    assert i.grid % 8 == 0 and i.grid * 4 >= nruns and (i.grid - 8) * 4 < nruns
     assert i.needs_fixup == 0 and i.guess_spread == 64
-    assert i.long_row_min == pf.adaptive_long_row_min("f64", 188) == 64
+    assert i.long_row_min == pf.adaptive_long_row_min("f64", 512) == 252
     i32 = pf.select(s, "f32", "auto")
-    assert i32.tile == 440
+    assert i32.variant == pf.ADAPTIVE and i32.tile == 440
+
+
+def test_select_auto_small_matrix_takes_small_tile():
+    """C1 shape: too few 512-key tiles for the device -> 188-key tiles, one per run."""
+    s = make_stats(4096, 65536, 16)
+    i = pf.select(s, "f64", "auto")
+    assert i.variant == pf.ADAPTIVE and i.tile == 188 and i.run_tiles == 1
+    assert i.long_row_min == 64
+
+
+def test_select_auto_very_short_rows_is_flat():
+    """C4 shape: 2.5 nnz per row -> FLAT 4096."""
+    s = make_stats(20000000, 50000000, 14, empty=1640000)
+    for dt in ("f64", "f32"):
+        i = pf.select(s, dt, "auto")
+        assert i.variant == pf.FLAT and i.tile == 4096 and i.needs_fixup == 1
+
+
+def test_select_auto_power_law_is_flat_dense_rows_adaptive():
+    """C3 shape (short rows plus split rows) -> FLAT; C5 shape (long mean row) -> ADAPTIVE with the combine kernel."""
+    c3 = pf.select(make_stats(2000000, 15200000, 200000), "f64", "auto")
+    assert c3.variant == pf.FLAT
+    c5 = pf.select(make_stats(1000000, 315647995, 499000), "f64", "auto")
+    assert c5.variant == pf.ADAPTIVE and c5.tile == 512 and c5.needs_fixup == 1 and c5.run_tiles == 16
 
 
 def test_select_long_rows_need_the_combine_kernel():
     s = make_stats(2000000, 15000000, 200000)
     i = pf.select(s, "f64", "adaptive")
-    assert i.needs_fixup == 1 and i.guess_spread == 0
+    assert i.needs_fixup == 1 and i.guess_spread == 0 and i.tile == 512
     f = pf.select(s, "f64", "flat")
-    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 2048) and f.needs_fixup == 1
+    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 4096) and f.needs_fixup == 1
     p = pf.select(s, "f64", "prefree")
     assert p.variant == pf.PREFREE and p.tile == 512 and p.ntiles == -(-15000000 // 512)
 
