@@ -99,8 +99,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="after the measurement, copy a 256 MiB buffer 3 times (known bytes, for scaling "
-                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+                    help="after the measurement, run a plain copy kernel over 256 MiB 3 times (known bytes, "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -181,7 +181,7 @@ def main():
         src = torch.ones(1 << 25, dtype=torch.float64, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)  # an elementwise kernel: reads 256 MiB, writes 256 MiB
         torch.cuda.synchronize()
         del src, dst
 
@@ -220,8 +220,8 @@ def main():
                      "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
                      "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
-        "cold": {"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
-                 "flush": "1 GiB write before each step"},
+        "cold": ({"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
+                  "flush": "1 GiB write before each step"} if args.cold_steps > 0 else None),
         "device": pf.device_name(),
     }
     if not args.no_cpu:
