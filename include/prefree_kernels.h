@@ -11,6 +11,7 @@
  *   pfk_spmv_adaptive     no counterpart: CSR-adaptive row blocks found on the fly
  *   pfk_spmv_flat         no counterpart launch: the flat nnz tiling of :407-428 without atomics
  *   pfk_spmv_fixup        no counterpart: replaces the cross-tile atomicAdd (:67,:91,:142)
+ *   pfk_adaptive_owners   no counterpart: the per-pattern split-row table the combine kernel reads
  *   pfk_row_stats         test/statistic.cu:38-98 (per-tile statistics), reduced to row-length stats
  *   pfk_debug_*           expose in-kernel index computations for bit-exact tests
  *   pfk_malloc ... pfk_event_*  CUDA runtime calls of preFreeSpMV.cu:571-661 and CudaTimer
@@ -49,6 +50,9 @@ typedef struct pfk_spmv_args {
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream);
+/* ADAPTIVE planning step: owner_row[t] = the row whose split starts in tile t, else -1, for every
+ * tile (a function of row_ptr and the tiling only; pfk_spmv_adaptive no longer writes it). */
+int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
 /* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count. */
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap);

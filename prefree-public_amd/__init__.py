@@ -129,6 +129,7 @@ def klib() -> ctypes.CDLL:
         lib()
         K = ctypes.CDLL(KLIB_PATH)
         _sig(K.pfk_debug_tile_desc, [_i, _i, ctypes.POINTER(SpmvArgs), _vp, _vp])
+        _sig(K.pfk_adaptive_owners, [_i, ctypes.POINTER(SpmvArgs), _vp])
         _sig(K.pfk_debug_prefree_rows, [_vp, _i, _i, _i, _vp, _vp])
         _sig(K.pfk_adaptive_long_row_min, [_i, _i])
         _sig(K.pfk_supported_tiles, [_i, _i, ctypes.POINTER(_i), _i])
@@ -263,6 +264,15 @@ def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=
                  run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag))
     _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
            "pfk_debug_tile_desc")
+    return ntiles
+
+
+def adaptive_owners(row_ptr, m, nnz, tile, out, err_flag, dtype="f64", guess_spread=0, run_tiles=0, stream=None):
+    """pfk_adaptive_owners: split-row owner of every ADAPTIVE tile into `out` (int32[ntiles])."""
+    ntiles = max(1, -(-(nnz + m) // tile))
+    a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
+                 run_tiles=run_tiles, ntiles=ntiles, owner_row=_p(out), err_flag=_p(err_flag))
+    _check(klib().pfk_adaptive_owners(dtype_code(dtype), ctypes.byref(a), _s(stream)), "pfk_adaptive_owners")
     return ntiles
 
 

@@ -38,6 +38,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 using namespace pfdev;
 
@@ -73,7 +74,14 @@ struct Args {
 // tile's nnz span is at most K + LMAX - 1 plus 3 for 16-byte alignment; the
 // sizes are chosen so that it fits one (fp64) or two (fp32) 4-nnz vectors per
 // lane of a wave64.
-constexpr int adaptive_lmax(int K) { return K <= 188 ? 64 : (K <= 440 ? 64 : K / 2 - 4); }
+// The short-row tiles (238, 494) keep LMAX = 16 and are meant for matrices
+// whose rows all fit one lane's sum: the span then fits 1 or 2 vectors.
+constexpr int adaptive_lmax(int K) { return (K == 238 || K == 494) ? 16 : (K <= 440 ? 64 : K / 2 - 4); }
+
+// ADAPTIVE tile sizes compiled in, per value type: X(type, dtype code, keys per tile).
+#define PF_ADAPTIVE_TILES(X) \
+    X(double, PF_F64, 188) X(double, PF_F64, 238) X(double, PF_F64, 494) X(double, PF_F64, 512) \
+    X(float, PF_F32, 440) X(float, PF_F32, 494) X(float, PF_F32, 1024)
 
 // Logical tile of this workgroup: XCD x (= blockIdx % 8) takes the contiguous
 // tiles [x*g8, (x+1)*g8), so neighbouring rows (and their x entries) share an L2.
@@ -95,10 +103,18 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit elements
 constexpr int kAuxNt = 2;               // cache policy bit 1: non-temporal (streamed once)
 
+// Callers pass wave-uniform base and size.  readfirstlane states that to the
+// compiler, which otherwise may keep the descriptor in VGPRs and wrap every
+// load in a loop over distinct descriptor values.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, long long bytes)
 {
     const long long b = bytes < 0 ? 0 : (bytes > 0x40000000ll ? 0x40000000ll : bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)b, kRsrcWord3);
+    const unsigned long long p = reinterpret_cast<unsigned long long>(base);
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)p);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(p >> 32));
+    const int nb = __builtin_amdgcn_readfirstlane((int)b);
+    void *u = reinterpret_cast<void *>(((unsigned long long)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(u, 0, nb, kRsrcWord3);
 }
 
 // col and val of the 4 consecutive nnz at 16-byte vector `vec` of a resource pair.
@@ -675,8 +691,10 @@ __device__ __forceinline__ void rp_to_lds(const int *__restrict__ rp, const Wave
             s_rpb[j] = rp[d.f - 1 + j];
 }
 
-// DESC_ONLY: write every tile's descriptor to dbg (8 ints per tile) instead of
-// computing y — the index test of this exact code path.
+// DESC_ONLY: instead of computing y, write every tile's descriptor to dbg (8
+// ints per tile; the index test of this exact code path) or, with dbg NULL,
+// the owner of every tile (the row whose split starts in it, else -1) — the
+// per-pattern table the combine kernel reads, built once at planning.
 // Waves per SIMD the register allocation targets: 7 (72 VGPRs) for one
 // 4-nnz vector per lane, fewer for larger tiles.
 template <typename T, int K, int LMAX>
@@ -724,7 +742,6 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     const __amdgpu_buffer_rsrc_t ry = make_rsrc_full(a.y, (long long)a.m * (long long)sizeof(T));
     const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(T));
     const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rowner = make_rsrc_full(a.owner, a.ntiles * 4);
     int err = 0;
 
     uint32_t kb, ke;
@@ -743,9 +760,13 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
 
     for (;;) {
         if (DESC_ONLY && lane == 0) {
-            int *o = dbg + 8 * t;
-            o[0] = d.lo_row; o[1] = d.nr; o[2] = d.A; o[3] = d.B; o[4] = d.head; o[5] = d.tail;
-            o[6] = d.f; o[7] = d.l;
+            if (dbg) {
+                int *o = dbg + 8 * t;
+                o[0] = d.lo_row; o[1] = d.nr; o[2] = d.A; o[3] = d.B; o[4] = d.head; o[5] = d.tail;
+                o[6] = d.f; o[7] = d.l;
+            } else {
+                a.owner[t] = d.tail ? d.lo_row + d.nr - 1 : -1;
+            }
         }
         const int base = d.A & ~3;
         const int nvec = d.B > d.A ? (d.B - base + 3) >> 2 : 0;
@@ -773,16 +794,15 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
 
         if (!DESC_ONLY) {
             const int *s_rpb = s_rpb_all[wave][buf];
-            // Products of tile t (waits for its x gathers only).
+            // Products of tile t (waits for its x gathers only).  Slots
+            // outside [A, B) hold neighbours' products or zeros; no sum reads
+            // them (every row range below is clamped to [A, B)).
 #pragma unroll
             for (int k = 0; k < VPT; ++k) {
                 const int vec = lane + k * kWave;
                 T p[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int e = base + 4 * vec + j;
-                    p[j] = (e >= d.A && e < d.B) ? vt[k][j] * xv[k][j] : T(0);
-                }
+                for (int j = 0; j < 4; ++j) p[j] = vt[k][j] * xv[k][j];
                 store4(s_prod + 4 * vec, p);
             }
             __builtin_amdgcn_wave_barrier();
@@ -859,25 +879,27 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             const int nw = d.nr - d.head - d.tail; // rows written to y
             const __amdgpu_buffer_rsrc_t ryt =
                 make_rsrc(a.y + (d.lo_row + r0), (long long)nw * (long long)sizeof(T));
+            constexpr int P = 16 / (int)sizeof(T);
 #pragma unroll
             for (int q = 0; q < S::kQS; ++q) {
-                constexpr int P = 16 / (int)sizeof(T);
-                const int j = (q * kWave + lane) * P;
-                T w[P];
+                // Slot 0 always issues; later slots only when the tile has the
+                // rows (wave-uniform branch), so most tiles issue one store.
+                if (q == 0 || q * kWave * P < nw) {
+                    const int j = (q * kWave + lane) * P;
+                    T w[P];
 #pragma unroll
-                for (int p = 0; p < P; ++p) w[p] = T(0);
-                if (j < nw) {
+                    for (int p = 0; p < P; ++p) w[p] = T(0);
+                    if (j < nw) {
 #pragma unroll
-                    for (int p = 0; p < P; ++p) w[p] = s_y[r0 + j + p < K + 1 ? r0 + j + p : 0];
+                        for (int p = 0; p < P; ++p) w[p] = s_y[r0 + j + p < K + 1 ? r0 + j + p : 0];
+                    }
+                    buf_store16(ryt, j < nw ? (uint32_t)j * (uint32_t)sizeof(T) : kOob, w);
                 }
-                buf_store16(ryt, j < nw ? (uint32_t)j * (uint32_t)sizeof(T) : kOob, w);
             }
+            // Partials of split rows (rare; owner[] is built once per pattern).
             const uint32_t tslot = (uint32_t)t * (uint32_t)sizeof(T);
-            const T hv = s_y[0];
-            const T tv = s_y[d.nr > 0 ? d.nr - 1 : 0];
-            buf_store(rhead, lane == 0 && d.head ? tslot : kOob, hv);
-            buf_store(rtail, lane == 0 && d.tail ? tslot : kOob, tv);
-            buf_store(rowner, lane == 0 ? (uint32_t)t * 4u : kOob, d.tail ? d.lo_row + d.nr - 1 : -1);
+            if (d.head) buf_store(rhead, lane == 0 ? tslot : kOob, s_y[0]);
+            if (d.tail) buf_store(rtail, lane == 0 ? tslot : kOob, s_y[d.nr > 0 ? d.nr - 1 : 0]);
             __builtin_amdgcn_wave_barrier();
         }
         if (!more)
@@ -1315,17 +1337,10 @@ template <typename T>
 
 int dispatch_adaptive(const pfk_spmv_args *a, void *stream)
 {
-    if constexpr (sizeof(T) == 8) {
-        switch (a->tile) {
-        case 188: return launch_stream<T, 188, adaptive_lmax(188), false>(a, nullptr, stream);
-        case 512: return launch_stream<T, 512, adaptive_lmax(512), false>(a, nullptr, stream);
-        }
-    } else {
-        switch (a->tile) {
-        case 440: return launch_stream<T, 440, adaptive_lmax(440), false>(a, nullptr, stream);
-        case 1024: return launch_stream<T, 1024, adaptive_lmax(1024), false>(a, nullptr, stream);
-        }
-    }
+#define PF_DISPATCH(TT, DT, KK) \
+    if (std::is_same<T, TT>::value && a->tile == KK) return launch_stream<TT, KK, adaptive_lmax(KK), false>(a, nullptr, stream);
+    PF_ADAPTIVE_TILES(PF_DISPATCH)
+#undef PF_DISPATCH
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
     return PF_ERR_UNSUPPORTED;
 }
@@ -1383,11 +1398,23 @@ int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves)
 {
     if (!waves) return PF_ERR_INVALID;
     *waves = 0;
-    if (dtype == PF_F64 && tile == 188) return wave_residency<double, 188>(waves);
-    if (dtype == PF_F64 && tile == 512) return wave_residency<double, 512>(waves);
-    if (dtype == PF_F32 && tile == 440) return wave_residency<float, 440>(waves);
-    if (dtype == PF_F32 && tile == 1024) return wave_residency<float, 1024>(waves);
+#define PF_RESIDENCY(TT, DT, KK) \
+    if (dtype == DT && tile == KK) return wave_residency<TT, KK>(waves);
+    PF_ADAPTIVE_TILES(PF_RESIDENCY)
+#undef PF_RESIDENCY
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", tile);
+    return PF_ERR_UNSUPPORTED;
+}
+
+int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream)
+{
+    if (!a || !a->row_ptr || !a->owner_row || !a->err_flag || a->m <= 0 || a->ntiles < 1) return PF_ERR_INVALID;
+    // The descriptors depend on (K, LMAX) only; the double instantiation serves both value types.
+#define PF_OWNERS(TT, DT, KK) \
+    if (dtype == DT && a->tile == KK) return launch_stream<double, KK, adaptive_lmax(KK), true>(a, nullptr, stream);
+    PF_ADAPTIVE_TILES(PF_OWNERS)
+#undef PF_OWNERS
+    snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
     return PF_ERR_UNSUPPORTED;
 }
 
@@ -1438,16 +1465,16 @@ int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream)
 
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
 {
-    static const int ad64[] = {188, 512};        // k_wave: keys per wave tile
-    static const int ad32[] = {440, 1024};
+    static const int ad64[] = {188, 238, 494, 512};  // k_wave: keys per wave tile
+    static const int ad32[] = {440, 494, 1024};
     static const int fl64[] = {1024, 2048, 4096}; // k_tiles: nnz per workgroup tile
     static const int fl32[] = {2048, 4096};
     static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
     if (variant == PF_PREFREE) { src = pf_tiles; n = 2; }
-    else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 2; }
-    else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 2; }
+    else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 4; }
+    else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 3; }
     else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 3; }
     else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 2; }
     else return 0;
@@ -1457,8 +1484,8 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
 
 int pfk_adaptive_long_row_min(int dtype, int tile)
 {
-    int t[4];
-    const int n = pfk_supported_tiles(PF_ADAPTIVE, dtype, t, 4);
+    int t[8];
+    const int n = pfk_supported_tiles(PF_ADAPTIVE, dtype, t, 8);
     for (int i = 0; i < n; ++i)
         if (t[i] == tile) return adaptive_lmax(tile);
     return -1;
@@ -1487,10 +1514,14 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
 {
     (void)dtype;
     if (!a || !a->row_ptr || !d_out || !a->err_flag || a->m <= 0 || a->ntiles < 1) return PF_ERR_INVALID;
-    if (merged_keys) {  // the descriptors of the k_stream code path itself
+    if (merged_keys) {  // the descriptors of the k_wave code path itself (independent of the value type)
         switch (a->tile) {
         case 188: return launch_stream<double, 188, adaptive_lmax(188), true>(a, d_out, stream);
+        case 238: return launch_stream<double, 238, adaptive_lmax(238), true>(a, d_out, stream);
+        case 440: return launch_stream<double, 440, adaptive_lmax(440), true>(a, d_out, stream);
+        case 494: return launch_stream<double, 494, adaptive_lmax(494), true>(a, d_out, stream);
         case 512: return launch_stream<double, 512, adaptive_lmax(512), true>(a, d_out, stream);
+        case 1024: return launch_stream<double, 1024, adaptive_lmax(1024), true>(a, d_out, stream);
         }
     } else {
         switch (a->tile) {

@@ -49,24 +49,32 @@ int default_tile(int variant, int dtype)
 // Used when no device is queried (pf_select); plans ask the device.
 long long nominal_resident_waves(int dtype, int tile)
 {
-    const int per_simd = dtype == PF_F64 ? (tile == 188 ? 7 : 3) : (tile == 440 ? 5 : 2);
+    int per_simd = 4;
+    if (dtype == PF_F64) per_simd = tile == 188 ? 7 : tile == 238 ? 6 : tile == 494 ? 4 : 3;
+    else per_simd = tile == 440 || tile == 494 ? 5 : 2;
     return 256LL * 4 * per_simd;
 }
 
-// Consecutive tiles per wave: enough that every resident wave gets one run
-// (a single dispatch round, no tail of half-empty rounds), at most 16 so the
-// runs in flight on an XCD stay close together in x.
-int choose_run(long long ntiles, long long resident)
+// The tiles of 494 / 238 keys hold only rows of at most 16 nnz (LMAX 16).
+bool short_row_tile(int tile) { return tile == 494 || tile == 238; }
+
+// Consecutive tiles per wave.  Short-row tiles: at most 3, so that several
+// dispatch rounds keep the tiles in flight on an XCD close together in x
+// (measured best on the banded and very sparse configurations).  Other tiles:
+// enough that every resident wave gets one run, at most 16.
+int choose_run(int tile, long long ntiles, long long resident)
 {
     if (resident <= 0) return 8;
     long long r = (ntiles + resident - 1) / resident;
-    return (int)(r < 1 ? 1 : (r > 16 ? 16 : r));
+    const long long cap = short_row_tile(tile) ? 3 : 16;
+    return (int)(r < 1 ? 1 : (r > cap ? cap : r));
 }
 
 // PF_AUTO: FLAT for very short rows (fewer than 3 nnz per row on average: the
 // merged tiles spend most keys on rows) and for short-row matrices that also
-// hold split rows (power-law); ADAPTIVE otherwise, with the small tile when the
-// matrix is too small to give every resident wave of the large one a tile.
+// hold split rows (power-law).  Otherwise ADAPTIVE: the short-row tile when no
+// row exceeds 16 nnz, the general tile else; a matrix too small to give half
+// the resident waves a tile takes the smallest tile.
 void auto_choice(const pf_row_stats &s, int dtype, int &variant, int &tile)
 {
     const long long m = s.m, nnz = s.nnz;
@@ -79,8 +87,8 @@ void auto_choice(const pf_row_stats &s, int dtype, int &variant, int &tile)
         return;
     }
     variant = PF_ADAPTIVE;
-    tile = big;
-    if (dtype == PF_F64 && (nnz + m) / big < nominal_resident_waves(dtype, big) / 2) tile = 188;
+    tile = s.max_row_len <= 16 ? 494 : big;
+    if (dtype == PF_F64 && (nnz + m) / tile < nominal_resident_waves(dtype, tile) / 2) tile = 188;
 }
 
 bool tile_supported(int variant, int dtype, int tile)
@@ -126,7 +134,7 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
         const long long total = nnz + m;
         r.ntiles = total > 0 ? (total + tile - 1) / tile : 1;
-        r.run_tiles = choose_run(r.ntiles, nominal_resident_waves(dtype, tile));
+        r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
         r.needs_fixup = s.max_row_len > r.long_row_min;
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
     } else if (variant == PF_FLAT) {
@@ -260,7 +268,7 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
     if (info.variant == PF_ADAPTIVE) {
         long long resident = 0;
         if (pfk_adaptive_resident_waves(dtype, info.tile, &resident) == PF_OK && resident > 0) {
-            info.run_tiles = choose_run(info.ntiles, resident);
+            info.run_tiles = choose_run(info.tile, info.ntiles, resident);
             set_grid(info);
         }
     }
@@ -286,6 +294,22 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
         p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
     }
     rc = pfk_fill_zero(p->err, 256, stream);
+    if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
+        // The split-row owner of every tile depends on row_ptr only: build it once.
+        pfk_spmv_args a;
+        std::memset(&a, 0, sizeof a);
+        a.row_ptr = d_row_ptr;
+        a.m = m;
+        a.n = n;
+        a.nnz = nnz;
+        a.tile = info.tile;
+        a.guess_spread = info.guess_spread;
+        a.run_tiles = info.run_tiles;
+        a.ntiles = info.ntiles;
+        a.owner_row = p->owner;
+        a.err_flag = p->err;
+        rc = pfk_adaptive_owners(dtype, &a, stream);
+    }
     if (rc == PF_OK) rc = pfk_stream_sync(stream);
     if (rc != PF_OK) {
         pfk_free(p->ws);

@@ -74,23 +74,26 @@ def make_stats(m, nnz, max_len, empty=0):
     return s
 
 
-def run_for(ntiles, resident):
-    return max(1, min(16, -(-ntiles // resident)))
+def run_for(ntiles, resident, cap=16):
+    return max(1, min(cap, -(-ntiles // resident)))
 
 
-def test_select_auto_banded_is_adaptive_large_tile():
-    """C2 shape: short regular rows -> ADAPTIVE, 512 keys per tile, runs sized to 3072 resident waves."""
+def test_select_auto_banded_is_adaptive_short_row_tile():
+    """C2 shape: rows of <= 16 nnz -> ADAPTIVE 494 keys per tile, runs of at most 3 tiles."""
     s = make_stats(4194304, 20963328, 5)
     i = pf.select(s, "f64", "auto")
-    assert i.variant == pf.ADAPTIVE and i.tile == 512
-    assert i.ntiles == -(-(20963328 + 4194304) // 512)
-    assert i.run_tiles == run_for(i.ntiles, 256 * 4 * 3) == 16
+    assert i.variant == pf.ADAPTIVE and i.tile == 494
+    assert i.ntiles == -(-(20963328 + 4194304) // 494)
+    assert i.run_tiles == run_for(i.ntiles, 256 * 4 * 4, cap=3) == 3
     nruns = -(-i.ntiles // i.run_tiles)
     assert i.grid % 8 == 0 and i.grid * 4 >= nruns and (i.grid - 8) * 4 < nruns
     assert i.needs_fixup == 0 and i.guess_spread == 64
-    assert i.long_row_min == pf.adaptive_long_row_min("f64", 512) == 252
+    assert i.long_row_min == pf.adaptive_long_row_min("f64", 494) == 16
     i32 = pf.select(s, "f32", "auto")
-    assert i32.variant == pf.ADAPTIVE and i32.tile == 440
+    assert i32.variant == pf.ADAPTIVE and i32.tile == 494
+    wide = pf.select(make_stats(4194304, 4194304 * 40, 60), "f64", "auto")   # rows up to 60 nnz
+    assert wide.variant == pf.ADAPTIVE and wide.tile == 512 and wide.long_row_min == 252
+    assert wide.run_tiles == run_for(wide.ntiles, 256 * 4 * 3)
 
 
 def test_select_auto_small_matrix_takes_small_tile():
@@ -134,8 +137,8 @@ def test_select_rejects_bad_arguments():
 
 
 def test_supported_tiles():
-    assert pf.supported_tiles("adaptive", "f64") == [188, 512]
-    assert pf.supported_tiles("adaptive", "f32") == [440, 1024]
+    assert pf.supported_tiles("adaptive", "f64") == [188, 238, 494, 512]
+    assert pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
     assert pf.supported_tiles("flat", "f64") == [1024, 2048, 4096]
     assert pf.supported_tiles("flat", "f32") == [2048, 4096]
     assert pf.supported_tiles("prefree", "f64") == [512, 1024]

@@ -18,7 +18,7 @@ from gpu_util import DEV, dev
 
 pytestmark = pytest.mark.gpu
 
-LMAX = {188: 64, 440: 64, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
+LMAX = {188: 64, 238: 16, 440: 64, 494: 16, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
 
 
 def cases():
@@ -54,6 +54,29 @@ def test_tile_descriptors_match_model(merged, tile, spread, run):
         assert int(err.cpu()[0]) == 0, name
         bad = np.flatnonzero(np.any(got != model, axis=1))
         assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
+
+
+OWNER_TILES = [(dt, t) for dt in ("f64", "f32") for t in pf.supported_tiles("adaptive", dt)]
+
+
+@pytest.mark.parametrize("dtype,tile", OWNER_TILES, ids=[f"{d}-{t}" for d, t in OWNER_TILES])
+def test_adaptive_owner_table_matches_model(dtype, tile):
+    """The per-pattern owner table (row whose split starts in a tile, else -1) the plan builds."""
+    for name, rp in CASES:
+        m, nnz = len(rp) - 1, int(rp[-1])
+        if m == 0:
+            continue
+        model = tile_model(rp, tile, True, LMAX[tile])
+        want = np.where(model[:, 5] == 1, model[:, 0] + model[:, 1] - 1, -1)
+        out = torch.full((len(model),), -7, dtype=torch.int32, device=DEV)
+        err = torch.zeros(64, dtype=torch.int32, device=DEV)
+        nt = pf.adaptive_owners(dev(rp), m, nnz, tile, out, err, dtype=dtype, guess_spread=64, run_tiles=3)
+        torch.cuda.synchronize()
+        assert nt == len(model)
+        assert int(err.cpu()[0]) == 0, name
+        got = out.cpu().numpy().astype(np.int64)
+        bad = np.flatnonzero(got != want)
+        assert bad.size == 0, f"{name}: tile {bad[0]} owner {got[bad[0]]} model {want[bad[0]]}"
 
 
 @pytest.mark.parametrize("tile", [512, 1024])

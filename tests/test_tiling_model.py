@@ -12,7 +12,7 @@ import pytest
 import prefree_amd as pf
 from csr_cases import check_tiling, edge_cases, tile_model
 
-LMAX = {188: 64, 440: 64, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
+LMAX = {188: 64, 238: 16, 440: 64, 494: 16, 512: 252, 1024: 508, 2048: 1020, 4096: 2044}
 
 
 def all_cases():
@@ -23,7 +23,7 @@ def all_cases():
     return cases
 
 
-@pytest.mark.parametrize("tile", [188, 440, 512, 1024, 2048, 4096])
+@pytest.mark.parametrize("tile", [188, 238, 440, 494, 512, 1024, 2048, 4096])
 @pytest.mark.parametrize("merged", [True, False], ids=["adaptive", "flat"])
 def test_model_satisfies_invariants(tile, merged):
     lmax = LMAX[tile] if merged else 0
