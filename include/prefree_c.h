@@ -76,6 +76,8 @@ typedef struct pf_plan_info {
     int guess_spread;     /* row search: spacing of the interpolated first probe round, 0 = none */
     int needs_fixup;      /* 1 when split rows need the combine kernel */
     int run_tiles;        /* ADAPTIVE: consecutive tiles walked by one wave64 */
+    int keep_cached;      /* ADAPTIVE: 1 = col/val read with ordinary loads (the matrix fits the
+                             256 MB MALL and stays cached across calls), 0 = non-temporal loads */
     long long ntiles;     /* logical tiles */
     long long grid;       /* workgroups launched (tiles rounded up to a multiple of the XCD count) */
     size_t workspace_bytes;
@@ -109,6 +111,8 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
 int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out);
 /* Tuning: consecutive tiles per wave64 of the ADAPTIVE kernel (1..256). */
 int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles);
+/* Tuning: cache policy of the ADAPTIVE col/val stream (1 = ordinary loads, 0 = non-temporal). */
+int pf_plan_set_keep_cached(pf_plan *plan, int keep_cached);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).

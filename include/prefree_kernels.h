@@ -40,6 +40,7 @@ typedef struct pfk_spmv_args {
     int tile;          /* keys (ADAPTIVE) or nnz (FLAT, PREFREE) per tile */
     int guess_spread;  /* 0 = plain 64-ary search */
     int run_tiles;     /* ADAPTIVE: consecutive tiles per wave (0 = default 8) */
+    int keep_cached;   /* ADAPTIVE: 1 = ordinary col/val loads (matrix fits the MALL), 0 = non-temporal */
     long long ntiles;
     void *head_slot;   /* [ntiles] partial of the split row entering a tile */
     void *tail_slot;   /* [ntiles] partial of the split row leaving a tile */

@@ -57,7 +57,8 @@ class RowStats(ctypes.Structure):
 class PlanInfo(ctypes.Structure):
     _fields_ = [("variant", ctypes.c_int), ("dtype", ctypes.c_int), ("tile", ctypes.c_int),
                 ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
-                ("run_tiles", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("grid", ctypes.c_longlong),
+                ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
+                ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t)]
 
     def as_dict(self):
@@ -71,7 +72,7 @@ class SpmvArgs(ctypes.Structure):
     _fields_ = [("row_ptr", ctypes.c_void_p), ("col", ctypes.c_void_p), ("val", ctypes.c_void_p),
                 ("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("m", ctypes.c_int), ("n", ctypes.c_int),
                 ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
-                ("run_tiles", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
+                ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p)]
 
 
@@ -104,6 +105,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_create_tuned, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
         _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
         _sig(L.pf_plan_set_run_tiles, [_vp, _i])
+        _sig(L.pf_plan_set_keep_cached, [_vp, _i])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
         _sig(L.pf_plan_execute, [_vp, _vp, _vp, _vp, _vp, _vp, _vp])
         _sig(L.pf_plan_check, [_vp, _vp])
@@ -224,6 +226,9 @@ class Plan:
 
     def set_run_tiles(self, run_tiles):
         _check(lib().pf_plan_set_run_tiles(self._h, int(run_tiles)), "pf_plan_set_run_tiles")
+
+    def set_keep_cached(self, keep_cached):
+        _check(lib().pf_plan_set_keep_cached(self._h, int(bool(keep_cached))), "pf_plan_set_keep_cached")
 
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),

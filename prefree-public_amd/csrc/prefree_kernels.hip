@@ -118,12 +118,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, lo
 }
 
 // col and val of the 4 consecutive nnz at 16-byte vector `vec` of a resource pair.
+template <int AUX = kAuxNt>
 __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
                                       double (&v)[4])
 {
-    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, kAuxNt);
-    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32, 0, kAuxNt);
-    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32 + 16, 0, kAuxNt);
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, AUX);
+    const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32, 0, AUX);
+    const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 32 + 16, 0, AUX);
     c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
     v[0] = __hiloint2double((int)v0.y, (int)v0.x);
     v[1] = __hiloint2double((int)v0.w, (int)v0.z);
@@ -131,11 +132,12 @@ __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer
     v[3] = __hiloint2double((int)v1.w, (int)v1.z);
 }
 
+template <int AUX = kAuxNt>
 __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
                                       float (&v)[4])
 {
-    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, kAuxNt);
-    const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 16, 0, kAuxNt);
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, AUX);
+    const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(rv, vec * 16, 0, AUX);
     c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
     v[0] = __int_as_float((int)vv.x); v[1] = __int_as_float((int)vv.y);
     v[2] = __int_as_float((int)vv.z); v[3] = __int_as_float((int)vv.w);
@@ -649,7 +651,7 @@ __device__ __forceinline__ WaveDesc wave_desc(const int *__restrict__ rp, int m,
 }
 
 // col/val of a tile (an empty descriptor reads nothing).
-template <typename T, int VPT>
+template <typename T, int VPT, int AUX>
 __device__ __forceinline__ void wave_issue_cv(const Args<T> &a, const WaveDesc &d, int (&c)[VPT][4], T (&v)[VPT][4])
 {
     const int base = d.A & ~3;
@@ -659,7 +661,7 @@ __device__ __forceinline__ void wave_issue_cv(const Args<T> &a, const WaveDesc &
     const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
-        load4(rc, rv, lane + k * kWave, c[k], v[k]);
+        load4<AUX>(rc, rv, lane + k * kWave, c[k], v[k]);
 }
 
 template <typename T, int VPT>
@@ -700,7 +702,9 @@ __device__ __forceinline__ void rp_to_lds(const int *__restrict__ rp, const Wave
 template <typename T, int K, int LMAX>
 constexpr int wave_occupancy() { return WaveShape<T, K, LMAX>::kVPT == 1 ? 7 : 4; }
 
-template <typename T, int K, int LMAX, bool DESC_ONLY, int WPE = wave_occupancy<T, K, LMAX>()>
+// NT: col/val loads non-temporal (a matrix larger than the MALL: keep x there);
+// otherwise ordinary loads, so that a matrix that fits stays cached across calls.
+template <typename T, int K, int LMAX, bool DESC_ONLY, bool NT = true, int WPE = wave_occupancy<T, K, LMAX>()>
 __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_wave(Args<T> a, int *__restrict__ dbg)
 {
     using S = WaveShape<T, K, LMAX>;
@@ -756,7 +760,8 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     rp_issue(a.rp, a.m, d.l, t + 1 < t_end, 0, rr);
     int c[VPT][4];
     T v[VPT][4];
-    if (!DESC_ONLY) wave_issue_cv(a, d, c, v);
+    constexpr int CV_AUX = NT ? kAuxNt : 0;
+    if (!DESC_ONLY) wave_issue_cv<T, VPT, CV_AUX>(a, d, c, v);
 
     for (;;) {
         if (DESC_ONLY && lane == 0) {
@@ -790,7 +795,7 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             if (!DESC_ONLY) rp_to_lds<RPL, CAP>(a.rp, dn, rr, s_rpb_all[wave][buf ^ 1]);
         }
         rp_issue(a.rp, a.m, dn.l, t + 2 < t_end, 0, rr);
-        if (!DESC_ONLY) wave_issue_cv(a, dn, c, v);
+        if (!DESC_ONLY) wave_issue_cv<T, VPT, CV_AUX>(a, dn, c, v);
 
         if (!DESC_ONLY) {
             const int *s_rpb = s_rpb_all[wave][buf];
@@ -1311,13 +1316,13 @@ void wave_grid(Args<T> &r, int run, long long &grid)
     grid = ((r.tx + NW - 1) / NW) * kXcds;
 }
 
-template <typename T, int K, int LMAX, bool DESC_ONLY>
+template <typename T, int K, int LMAX, bool DESC_ONLY, bool NT = true>
 int launch_stream(const pfk_spmv_args *a, int *dbg, void *stream)
 {
     Args<T> r = make_args<T>(a);
     long long grid = 0;
     wave_grid<T>(r, a->run_tiles > 0 ? a->run_tiles : 8, grid);
-    hipLaunchKernelGGL((k_wave<T, K, LMAX, DESC_ONLY>), dim3((unsigned)grid), dim3(kWaveWG), 0, S(stream), r, dbg);
+    hipLaunchKernelGGL((k_wave<T, K, LMAX, DESC_ONLY, NT>), dim3((unsigned)grid), dim3(kWaveWG), 0, S(stream), r, dbg);
     PFK_LAUNCHED("k_wave");
     return PF_OK;
 }
@@ -1338,7 +1343,9 @@ template <typename T>
 int dispatch_adaptive(const pfk_spmv_args *a, void *stream)
 {
 #define PF_DISPATCH(TT, DT, KK) \
-    if (std::is_same<T, TT>::value && a->tile == KK) return launch_stream<TT, KK, adaptive_lmax(KK), false>(a, nullptr, stream);
+    if (std::is_same<T, TT>::value && a->tile == KK)                                                      \
+        return a->keep_cached ? launch_stream<TT, KK, adaptive_lmax(KK), false, false>(a, nullptr, stream) \
+                              : launch_stream<TT, KK, adaptive_lmax(KK), false, true>(a, nullptr, stream);
     PF_ADAPTIVE_TILES(PF_DISPATCH)
 #undef PF_DISPATCH
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);

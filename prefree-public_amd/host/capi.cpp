@@ -135,6 +135,9 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         const long long total = nnz + m;
         r.ntiles = total > 0 ? (total + tile - 1) / tile : 1;
         r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
+        // Ordinary loads when col/val + row_ptr fit 1.25x the 256 MB MALL (part of the
+        // stream then survives to the next call); non-temporal beyond, to keep x cached.
+        r.keep_cached = nnz * (4 + vb) + (m + 1) * 4 <= 320LL * 1000 * 1000;
         r.needs_fixup = s.max_row_len > r.long_row_min;
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
     } else if (variant == PF_FLAT) {
@@ -341,6 +344,13 @@ int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles)
     return PF_OK;
 }
 
+int pf_plan_set_keep_cached(pf_plan *plan, int keep_cached)
+{
+    if (!plan || (keep_cached != 0 && keep_cached != 1)) return fail(PF_ERR_INVALID, "keep_cached must be 0 or 1");
+    plan->info.keep_cached = keep_cached;
+    return PF_OK;
+}
+
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out)
 {
     if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
@@ -368,6 +378,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.tile = plan->info.tile;
     a.guess_spread = plan->info.guess_spread;
     a.run_tiles = plan->info.run_tiles;
+    a.keep_cached = plan->info.keep_cached;
     a.ntiles = plan->info.ntiles;
     a.head_slot = plan->head;
     a.tail_slot = plan->tail;

@@ -95,6 +95,28 @@ def test_adaptive_run_lengths(run):
         assert_parity(rp, col, v["f64"], x, ys[1], "f64", what=f"C{cfg} run {run}")
 
 
+def test_adaptive_cache_policy_bit_identical():
+    """Ordinary and non-temporal col/val loads give the same y bit for bit."""
+    import torch
+    from gpu_util import DEV, dev
+    for cfg, scale in ((2, 300), (5, 40000)):
+        rp, col, v = pf.synth_csr(cfg, seed=12, scale_n=scale)
+        m = len(rp) - 1
+        x = pf.synth_x(cfg, m, seed=12)["f64"]
+        d = [dev(rp), dev(col), dev(v["f64"]), dev(x)]
+        ys = []
+        with pf.Plan(d[0], d[1], m, m, len(col), "f64", "adaptive") as p:
+            for keep in (0, 1):
+                p.set_keep_cached(keep)
+                y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+                p.execute(*d, y)
+                torch.cuda.synchronize()
+                ys.append(y.cpu().numpy())
+            p.check()
+        assert np.array_equal(ys[0], ys[1])
+        assert_parity(rp, col, v["f64"], x, ys[0], "f64", what=f"C{cfg} cache policy")
+
+
 def test_adaptive_short_rows_bit_exact():
     """Rows of <= 16 products are summed in nnz order by one lane: the oracle's order exactly."""
     for cfg, scale in ((2, 300), (4, 400000), (1, 0)):
