@@ -34,7 +34,8 @@ enum pf_status {
     PF_ERR_NOMEM = 4,       /* device or host allocation failed */
     PF_ERR_UNSUPPORTED = 5, /* variant / tile combination not compiled in */
     PF_ERR_CSR = 6,         /* malformed CSR: row_ptr[0]!=0, decreasing, row_ptr[m]!=nnz, col out of range */
-    PF_ERR_KERNEL = 7       /* a kernel found an inconsistent tile (corrupted row_ptr after planning) */
+    PF_ERR_KERNEL = 7,      /* a kernel found an inconsistent tile (corrupted row_ptr after planning) */
+    PF_ERR_IO = 8           /* a file could not be read or parsed (pf_mtx_last_error says why) */
 };
 
 /* ---- value types ----------------------------------------------------------- */
@@ -140,6 +141,19 @@ int pf_synth_dims(int cfg, uint64_t seed, int scale_n, int *m, int *n, long long
 int pf_synth_csr(int cfg, uint64_t seed, int scale_n, int vals, int *row_ptr, int *col,
                  double *val_f64, float *val_f32);
 int pf_synth_x(int cfg, uint64_t seed, int n, int vals, double *x_f64, float *x_f32);
+
+/* ---- Matrix Market input (the reference harness's mmio_allinone,
+ * utilities/mmio.cpp:1543-1713) ------------------------------------------------
+ * Reads a coordinate-format file into newly malloc'ed host arrays (free each
+ * with pf_host_free): 1-based indices made 0-based; entries kept in file order,
+ * duplicates included; symmetric and hermitian files get every off-diagonal
+ * entry mirrored right after it (skew-symmetric files are not mirrored, as in
+ * the reference); pattern entries are 1.0, complex entries keep the real part.
+ * Returns PF_ERR_IO with a reason in pf_mtx_last_error() for unreadable files. */
+int pf_mtx_read(const char *path, int *m, int *n, int *nnz, int *is_symmetric, int **row_ptr, int **col,
+                double **val);
+const char *pf_mtx_last_error(void);
+void pf_host_free(void *p);
 
 /* ---- runtime helpers for hosts without HIP headers (thin wrappers) -------- */
 int pf_device_malloc(void **ptr, size_t bytes);

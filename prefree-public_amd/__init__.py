@@ -114,6 +114,13 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_synth_dims, [_i, ctypes.c_uint64, _i, ctypes.POINTER(_i), ctypes.POINTER(_i),
                                ctypes.POINTER(_ll)])
         _sig(L.pf_synth_csr, [_i, ctypes.c_uint64, _i, _i, _vp, _vp, _vp, _vp])
+        _pi = ctypes.POINTER(ctypes.c_int)
+        _sig(L.pf_mtx_read, [ctypes.c_char_p, _pi, _pi, _pi, _pi, ctypes.POINTER(_pi), ctypes.POINTER(_pi),
+                             ctypes.POINTER(ctypes.POINTER(ctypes.c_double))])
+        L.pf_mtx_last_error.restype = ctypes.c_char_p
+        L.pf_mtx_last_error.argtypes = []
+        L.pf_host_free.restype = None
+        L.pf_host_free.argtypes = [_vp]
         _sig(L.pf_synth_x, [_i, ctypes.c_uint64, _i, _i, _vp, _vp])
         _sig(L.pf_device_malloc, [ctypes.POINTER(_vp), ctypes.c_size_t])
         _sig(L.pf_device_free, [_vp])
@@ -314,6 +321,28 @@ def synth_dims(cfg, seed=1, scale_n=0):
     _check(lib().pf_synth_dims(int(cfg), int(seed), int(scale_n), ctypes.byref(m), ctypes.byref(n),
                                ctypes.byref(nnz)), "pf_synth_dims")
     return m.value, n.value, nnz.value
+
+
+def mtx_read(path):
+    """pf_mtx_read: a Matrix Market file as (row_ptr, col, val, m, n, is_symmetric), numpy arrays."""
+    import numpy as np
+    L = lib()
+    m, n, nnz, sym = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rp = ctypes.POINTER(ctypes.c_int)()
+    col = ctypes.POINTER(ctypes.c_int)()
+    val = ctypes.POINTER(ctypes.c_double)()
+    st = L.pf_mtx_read(os.fsencode(path), ctypes.byref(m), ctypes.byref(n), ctypes.byref(nnz), ctypes.byref(sym),
+                       ctypes.byref(rp), ctypes.byref(col), ctypes.byref(val))
+    if st != 0:
+        raise PrefreeError(st, f"pf_mtx_read: {L.pf_mtx_last_error().decode()}")
+    try:
+        r = np.ctypeslib.as_array(rp, shape=(m.value + 1,)).copy()
+        c = np.ctypeslib.as_array(col, shape=(max(nnz.value, 1),))[:nnz.value].copy()
+        v = np.ctypeslib.as_array(val, shape=(max(nnz.value, 1),))[:nnz.value].copy()
+    finally:
+        for ptr in (rp, col, val):
+            L.pf_host_free(ctypes.cast(ptr, ctypes.c_void_p))
+    return r, c, v, m.value, n.value, bool(sym.value)
 
 
 def synth_csr(cfg, seed=1, scale_n=0, vals=0, dtypes=("f64",), out=None):

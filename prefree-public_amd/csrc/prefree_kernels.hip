@@ -700,7 +700,11 @@ __device__ __forceinline__ void rp_to_lds(const int *__restrict__ rp, const Wave
 // Waves per SIMD the register allocation targets: 7 (72 VGPRs) for one
 // 4-nnz vector per lane, fewer for larger tiles.
 template <typename T, int K, int LMAX>
-constexpr int wave_occupancy() { return WaveShape<T, K, LMAX>::kVPT == 1 ? 7 : 4; }
+constexpr int wave_occupancy()
+{
+    constexpr int vpt = WaveShape<T, K, LMAX>::kVPT;
+    return vpt == 1 ? (LMAX == 16 ? 6 : 7) : vpt == 2 ? 4 : vpt == 3 ? 3 : 2;
+}
 
 // NT: col/val loads non-temporal (a matrix larger than the MALL: keep x there);
 // otherwise ordinary loads, so that a matrix that fits stays cached across calls.
@@ -743,7 +747,6 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
         return;
 
     const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc_full(a.y, (long long)a.m * (long long)sizeof(T));
     const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(T));
     const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(T));
     int err = 0;

@@ -188,6 +188,7 @@ const char *pf_status_string(int status)
     case PF_ERR_UNSUPPORTED: return "unsupported variant/tile/dtype";
     case PF_ERR_CSR: return "malformed CSR matrix";
     case PF_ERR_KERNEL: return "kernel found an inconsistent tile";
+    case PF_ERR_IO: return "file could not be read or parsed";
     }
     return "unknown status";
 }
