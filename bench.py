@@ -177,6 +177,20 @@ def main():
     cold_ms /= max(1, args.cold_steps)
     del flush
 
+    # The drop-in boundary (preFreeSpMV) takes host buffers: one SpMV including
+    # the host->device copies of the CSR and x, planning and the copy of y back.
+    torch.cuda.synchronize()
+    h0 = time.perf_counter()
+    h_rp = torch.from_numpy(rp).to(dev)
+    h_col = torch.from_numpy(col).to(dev)
+    h_val = torch.from_numpy(val).to(dev)
+    h_x = torch.from_numpy(x).to(dev)
+    h_y = torch.empty(m, dtype=tdt, device=dev)
+    pf.spmv(h_rp, h_col, h_val, h_x, h_y, m, n, nnz, dt, args.variant, stream=stream)
+    y_host = h_y.cpu()
+    pcie_ms = (time.perf_counter() - h0) * 1e3
+    del h_rp, h_col, h_val, h_x, h_y, y_host
+
     if args.copy_calibration:
         src = torch.ones(1 << 25, dtype=torch.float64, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
@@ -222,6 +236,8 @@ def main():
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
         "cold": ({"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
                   "flush": "1 GiB write before each step"} if args.cold_steps > 0 else None),
+        "host_buffers": {"ms": round(pcie_ms, 3), "gflops": round(2.0 * nnz / (pcie_ms * 1e6), 3),
+                         "what": "one SpMV from pageable host arrays: copies in, plan, execute, copy of y out"},
         "device": pf.device_name(),
     }
     if not args.no_cpu:
