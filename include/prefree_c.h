@@ -126,6 +126,34 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
 int pf_plan_check(pf_plan *plan, void *stream);
 int pf_plan_destroy(pf_plan *plan);
 
+/* ---- tuning ------------------------------------------------------------------
+ * pf_plan_autotune times every compiled configuration for the plan's dtype on
+ * the caller's matrix and vectors (ADAPTIVE tiles x run lengths 1..16, FLAT
+ * tiles; PREFREE and the ordinary-load cache policy when asked by `flags`), each
+ * as the best of two batches of `reps` back-to-back SpMVs, and switches the plan
+ * to the fastest.  d_y holds A·x on return.  Synchronises `stream`; allocates
+ * temporary plans.  The online counterpart of the reference tuner
+ * (scripts/profile_and_generate.py:319-418), which compiled and timed each
+ * candidate as a separate program. */
+enum { PF_TUNE_PREFREE = 1, PF_TUNE_KEEP_CACHED = 2 };
+typedef struct pf_tune_result {
+    int variant, tile, run_tiles, keep_cached;
+    int candidates;     /* configurations timed (including the plan's own) */
+    double us;          /* microseconds per SpMV of the chosen configuration */
+    double default_us;  /* of the configuration the plan had before tuning */
+} pf_tune_result;
+int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x,
+                     void *d_y, int reps, int flags, void *stream, pf_tune_result *result);
+
+/* Size-class table for PF_AUTO, as written by the offline tuner
+ * (prefree-public_amd/tune/autotune.py).  Text, one row per line:
+ *   <class> <nnz_upper | -1> <f64|f32> <adaptive|flat|prefree> <tile> <run_tiles | 0> <keep_cached>
+ * The first row whose dtype matches and whose bound exceeds the matrix's nnz
+ * decides (run 0: the built-in run rule).  NULL clears the table.  Without a
+ * call, $PREFREE_TUNING_TABLE is read once if set.  Plans made before the call
+ * are unaffected. */
+int pf_set_tuning_table(const char *path);
+
 /* One-shot y = A·x: plan, execute, synchronise, destroy. */
 int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
             int m, int n, int nnz, int dtype, int variant, void *stream);

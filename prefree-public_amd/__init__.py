@@ -67,6 +67,22 @@ class PlanInfo(ctypes.Structure):
         return d
 
 
+class TuneResult(ctypes.Structure):
+    """pf_tune_result, include/prefree_c.h."""
+    _fields_ = [("variant", ctypes.c_int), ("tile", ctypes.c_int), ("run_tiles", ctypes.c_int),
+                ("keep_cached", ctypes.c_int), ("candidates", ctypes.c_int), ("us", ctypes.c_double),
+                ("default_us", ctypes.c_double)]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k, _ in self._fields_}
+        d["variant_name"] = VARIANT_NAMES.get(self.variant, "?")
+        return d
+
+
+TUNE_PREFREE = 1
+TUNE_KEEP_CACHED = 2
+
+
 class SpmvArgs(ctypes.Structure):
     """pfk_spmv_args, include/prefree_kernels.h."""
     _fields_ = [("row_ptr", ctypes.c_void_p), ("col", ctypes.c_void_p), ("val", ctypes.c_void_p),
@@ -106,6 +122,8 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
         _sig(L.pf_plan_set_run_tiles, [_vp, _i])
         _sig(L.pf_plan_set_keep_cached, [_vp, _i])
+        _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
+        _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
         _sig(L.pf_plan_execute, [_vp, _vp, _vp, _vp, _vp, _vp, _vp])
         _sig(L.pf_plan_check, [_vp, _vp])
@@ -157,7 +175,8 @@ def _last_error() -> str:
 
 def _check(status: int, what: str):
     if status != 0:
-        raise PrefreeError(status, what)
+        detail = lib().pf_last_error().decode(errors="replace")
+        raise PrefreeError(status, f"{what}: {detail}" if detail else what)
 
 
 def _p(obj):
@@ -233,6 +252,13 @@ class Plan:
 
     def set_run_tiles(self, run_tiles):
         _check(lib().pf_plan_set_run_tiles(self._h, int(run_tiles)), "pf_plan_set_run_tiles")
+
+    def autotune(self, row_ptr, col, val, x, y, reps=20, flags=0, stream=None):
+        """pf_plan_autotune: time the compiled configurations on this matrix, keep the fastest."""
+        r = TuneResult()
+        _check(lib().pf_plan_autotune(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), int(reps), int(flags),
+                                      _s(stream), ctypes.byref(r)), "pf_plan_autotune")
+        return r.as_dict()
 
     def set_keep_cached(self, keep_cached):
         _check(lib().pf_plan_set_keep_cached(self._h, int(bool(keep_cached))), "pf_plan_set_keep_cached")
@@ -321,6 +347,11 @@ def synth_dims(cfg, seed=1, scale_n=0):
     _check(lib().pf_synth_dims(int(cfg), int(seed), int(scale_n), ctypes.byref(m), ctypes.byref(n),
                                ctypes.byref(nnz)), "pf_synth_dims")
     return m.value, n.value, nnz.value
+
+
+def set_tuning_table(path):
+    """pf_set_tuning_table: size-class table for PF_AUTO (None clears it)."""
+    _check(lib().pf_set_tuning_table(None if path is None else os.fsencode(path)), "pf_set_tuning_table")
 
 
 def mtx_read(path):

@@ -4,9 +4,15 @@
 #include "prefree_c.h"
 #include "prefree_kernels.h"
 
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <mutex>
+#include <sstream>
 #include <string>
+#include <vector>
 
 namespace {
 
@@ -70,25 +76,114 @@ int choose_run(int tile, long long ntiles, long long resident)
     return (int)(r < 1 ? 1 : (r > cap ? cap : r));
 }
 
-// PF_AUTO: FLAT for very short rows (fewer than 3 nnz per row on average: the
-// merged tiles spend most keys on rows) and for short-row matrices that also
-// hold split rows (power-law).  Otherwise ADAPTIVE: the short-row tile when no
-// row exceeds 16 nnz, the general tile else; a matrix too small to give half
-// the resident waves a tile takes the smallest tile.
-void auto_choice(const pf_row_stats &s, int dtype, int &variant, int &tile)
+// ---- tuning table (written by the offline tuner, prefree-public_amd/tune) ----
+//
+// One row per (size class, value type): nnz below `nnz_upper` (-1: no bound)
+// selects (variant, tile, run_tiles, keep_cached).  Loaded by
+// pf_set_tuning_table or, once, from $PREFREE_TUNING_TABLE; consulted by
+// PF_AUTO before the built-in rules.  This replaces the reference tuner's
+// generated size-class dispatch (templates/preFreeSpMV_template.cu.j2:845-1003).
+struct TableRow {
+    std::string name;
+    long long nnz_upper;
+    int dtype, variant, tile, run, keep;
+};
+
+std::mutex g_table_mu;
+std::vector<TableRow> g_table;
+bool g_table_env_done = false;
+
+int parse_dtype(const std::string &s) { return s == "f64" ? PF_F64 : s == "f32" ? PF_F32 : -1; }
+int parse_variant(const std::string &s)
 {
+    return s == "adaptive" ? PF_ADAPTIVE : s == "flat" ? PF_FLAT : s == "prefree" ? PF_PREFREE : -1;
+}
+
+int load_table(const char *path, std::vector<TableRow> &out, std::string &why)
+{
+    std::ifstream f(path);
+    if (!f) {
+        why = std::string("cannot open tuning table ") + path;
+        return PF_ERR_IO;
+    }
+    std::string line;
+    int lineno = 0;
+    out.clear();
+    while (std::getline(f, line)) {
+        ++lineno;
+        const size_t hash = line.find('#');
+        if (hash != std::string::npos) line.resize(hash);
+        std::istringstream in(line);
+        TableRow r;
+        std::string dt, var;
+        if (!(in >> r.name)) continue;  // blank or comment
+        if (!(in >> r.nnz_upper >> dt >> var >> r.tile >> r.run >> r.keep)) {
+            why = std::string(path) + ":" + std::to_string(lineno) + ": expected 'class nnz_upper dtype variant tile run keep'";
+            return PF_ERR_IO;
+        }
+        r.dtype = parse_dtype(dt);
+        r.variant = parse_variant(var);
+        if (r.dtype < 0 || r.variant < 0 || r.tile <= 0 || r.run < 0 || r.run > 256 || r.keep < 0 || r.keep > 1) {
+            why = std::string(path) + ":" + std::to_string(lineno) + ": bad value";
+            return PF_ERR_IO;
+        }
+        out.push_back(r);
+    }
+    return PF_OK;
+}
+
+bool tile_supported(int variant, int dtype, int tile);
+
+// Decision of PF_AUTO: variant and tile, plus the run length and cache
+// policy when a tuning-table row fixes them (run 0 / keep -1: not fixed).
+struct Choice {
+    int variant = PF_ADAPTIVE, tile = 0, run = 0, keep = -1;
+};
+
+bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
+{
+    std::lock_guard<std::mutex> lock(g_table_mu);
+    if (!g_table_env_done) {
+        g_table_env_done = true;
+        const char *env = std::getenv("PREFREE_TUNING_TABLE");
+        std::string why;
+        if (env && *env && load_table(env, g_table, why) != PF_OK) g_table.clear();
+    }
+    for (const TableRow &r : g_table) {
+        if (r.dtype != dtype || (r.nnz_upper >= 0 && s.nnz >= r.nnz_upper)) continue;
+        if (!tile_supported(r.variant, dtype, r.tile)) continue;
+        c.variant = r.variant;
+        c.tile = r.tile;
+        c.run = r.run;
+        c.keep = r.keep;
+        return true;
+    }
+    return false;
+}
+
+// PF_AUTO: a tuning-table row if one matches; else FLAT for very short rows
+// (fewer than 3 nnz per row on average: the merged tiles spend most keys on
+// rows) and for short-row matrices that also hold split rows (power-law).
+// Otherwise ADAPTIVE: the short-row tile when no row exceeds 16 nnz, the
+// general tile else; a matrix too small to give half the resident waves a
+// tile takes the smallest tile.
+Choice auto_choice(const pf_row_stats &s, int dtype)
+{
+    Choice c;
+    if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
     const int big = default_tile(PF_ADAPTIVE, dtype);
     const bool very_short = m > 0 && nnz < 3 * m;
     const bool split_rows = s.max_row_len > pfk_adaptive_long_row_min(dtype, big);
     if (very_short || (split_rows && nnz < 16 * m)) {
-        variant = PF_FLAT;
-        tile = default_tile(PF_FLAT, dtype);
-        return;
+        c.variant = PF_FLAT;
+        c.tile = default_tile(PF_FLAT, dtype);
+        return c;
     }
-    variant = PF_ADAPTIVE;
-    tile = s.max_row_len <= 16 ? 494 : big;
-    if (dtype == PF_F64 && (nnz + m) / tile < nominal_resident_waves(dtype, tile) / 2) tile = 188;
+    c.variant = PF_ADAPTIVE;
+    c.tile = s.max_row_len <= 16 ? 494 : big;
+    if (dtype == PF_F64 && (nnz + m) / c.tile < nominal_resident_waves(dtype, c.tile) / 2) c.tile = 188;
+    return c;
 }
 
 bool tile_supported(int variant, int dtype, int tile)
@@ -112,6 +207,17 @@ void set_grid(pf_plan_info &r)
     } else {
         r.grid = ((r.ntiles + kXcds - 1) / kXcds) * kXcds;
     }
+}
+
+// A tuning-table row may fix the run length and cache policy of ADAPTIVE.
+void apply_overrides(const Choice &c, pf_plan_info &info)
+{
+    if (info.variant != PF_ADAPTIVE) return;
+    if (c.run > 0) {
+        info.run_tiles = c.run;
+        set_grid(info);
+    }
+    if (c.keep >= 0) info.keep_cached = c.keep;
 }
 
 // Fills everything in `info` that follows from (stats, dtype, variant, tile).
@@ -173,6 +279,80 @@ struct pf_plan {
     int *err = nullptr;
 };
 
+namespace {
+
+// The plan for a validated matrix with known statistics (shared by plan
+// creation and the tuner's candidates).
+int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
+               void *stream, pf_plan **plan)
+{
+    Choice c;
+    if (variant == PF_AUTO) {  // an explicit tile is kept only if the chosen variant has it
+        c = auto_choice(s, dtype);
+        variant = c.variant;
+        if (tile <= 0 || !tile_supported(variant, dtype, tile)) tile = c.tile;
+    }
+    pf_plan_info info;
+    const int st = finish_info(s, dtype, variant, tile > 0 ? tile : default_tile(variant, dtype), &info);
+    if (st != PF_OK) return st;
+    if (info.variant == PF_ADAPTIVE) {
+        long long resident = 0;
+        if (pfk_adaptive_resident_waves(dtype, info.tile, &resident) == PF_OK && resident > 0) {
+            info.run_tiles = choose_run(info.tile, info.ntiles, resident);
+            set_grid(info);
+        }
+    }
+    if (c.tile == info.tile && c.variant == info.variant) apply_overrides(c, info);
+
+    pf_plan *p = new pf_plan();
+    p->m = m;
+    p->n = n;
+    p->nnz = nnz;
+    p->info = info;
+    p->stats = s;
+    int rc = pfk_malloc(&p->ws, info.workspace_bytes);
+    if (rc != PF_OK) {
+        delete p;
+        return from_kernel_layer(rc, "plan workspace");
+    }
+    char *w = static_cast<char *>(p->ws);
+    p->err = reinterpret_cast<int *>(w);
+    if (info.variant != PF_PREFREE) {
+        const size_t vb = (size_t)value_bytes(dtype);
+        const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
+        p->head = w + 256;
+        p->tail = w + 256 + slots;
+        p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
+    }
+    rc = pfk_fill_zero(p->err, 256, stream);
+    if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
+        // The split-row owner of every tile depends on row_ptr only: build it once.
+        pfk_spmv_args a;
+        std::memset(&a, 0, sizeof a);
+        a.row_ptr = d_row_ptr;
+        a.m = m;
+        a.n = n;
+        a.nnz = nnz;
+        a.tile = info.tile;
+        a.guess_spread = info.guess_spread;
+        a.run_tiles = info.run_tiles;
+        a.ntiles = info.ntiles;
+        a.owner_row = p->owner;
+        a.err_flag = p->err;
+        rc = pfk_adaptive_owners(dtype, &a, stream);
+    }
+    if (rc == PF_OK) rc = pfk_stream_sync(stream);
+    if (rc != PF_OK) {
+        pfk_free(p->ws);
+        delete p;
+        return from_kernel_layer(rc, "plan workspace init");
+    }
+    *plan = p;
+    return PF_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int pf_version(void) { return 100; }  // 0.1.0
@@ -226,12 +406,16 @@ int pf_select(const pf_row_stats *stats, int dtype, int variant, pf_plan_info *o
 {
     if (!stats || !out || value_bytes(dtype) == 0)
         return fail(PF_ERR_INVALID, "pf_select: bad argument");
-    int tile = 0;
-    if (variant == PF_AUTO)
-        auto_choice(*stats, dtype, variant, tile);
-    else
-        tile = default_tile(variant, dtype);
-    return finish_info(*stats, dtype, variant, tile, out);
+    Choice c;
+    if (variant == PF_AUTO) {
+        c = auto_choice(*stats, dtype);
+    } else {
+        c.variant = variant;
+        c.tile = default_tile(variant, dtype);
+    }
+    const int st = finish_info(*stats, dtype, c.variant, c.tile, out);
+    if (st == PF_OK) apply_overrides(c, *out);
+    return st;
 }
 
 int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz,
@@ -263,67 +447,7 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
                                         std::to_string(s.row_ptr_last) + " decreasing=" +
                                         std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
     }
-    pf_plan_info info;
-    if (variant == PF_AUTO) {  // an explicit tile is kept only if the chosen variant has it
-        int t = 0;
-        auto_choice(s, dtype, variant, t);
-        if (tile <= 0 || !tile_supported(variant, dtype, tile)) tile = t;
-    }
-    const int st = finish_info(s, dtype, variant, tile > 0 ? tile : default_tile(variant, dtype), &info);
-    if (st != PF_OK) return st;
-    if (info.variant == PF_ADAPTIVE) {
-        long long resident = 0;
-        if (pfk_adaptive_resident_waves(dtype, info.tile, &resident) == PF_OK && resident > 0) {
-            info.run_tiles = choose_run(info.tile, info.ntiles, resident);
-            set_grid(info);
-        }
-    }
-
-    pf_plan *p = new pf_plan();
-    p->m = m;
-    p->n = n;
-    p->nnz = nnz;
-    p->info = info;
-    p->stats = s;
-    int rc = pfk_malloc(&p->ws, info.workspace_bytes);
-    if (rc != PF_OK) {
-        delete p;
-        return from_kernel_layer(rc, "plan workspace");
-    }
-    char *w = static_cast<char *>(p->ws);
-    p->err = reinterpret_cast<int *>(w);
-    if (info.variant != PF_PREFREE) {
-        const size_t vb = (size_t)value_bytes(dtype);
-        const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
-        p->head = w + 256;
-        p->tail = w + 256 + slots;
-        p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
-    }
-    rc = pfk_fill_zero(p->err, 256, stream);
-    if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
-        // The split-row owner of every tile depends on row_ptr only: build it once.
-        pfk_spmv_args a;
-        std::memset(&a, 0, sizeof a);
-        a.row_ptr = d_row_ptr;
-        a.m = m;
-        a.n = n;
-        a.nnz = nnz;
-        a.tile = info.tile;
-        a.guess_spread = info.guess_spread;
-        a.run_tiles = info.run_tiles;
-        a.ntiles = info.ntiles;
-        a.owner_row = p->owner;
-        a.err_flag = p->err;
-        rc = pfk_adaptive_owners(dtype, &a, stream);
-    }
-    if (rc == PF_OK) rc = pfk_stream_sync(stream);
-    if (rc != PF_OK) {
-        pfk_free(p->ws);
-        delete p;
-        return from_kernel_layer(rc, "plan workspace init");
-    }
-    *plan = p;
-    return PF_OK;
+    return plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan);
 }
 
 int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz, int dtype,
@@ -435,6 +559,147 @@ int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const voi
     if (st == PF_OK) st = pf_plan_check(p, stream);
     const int st2 = pf_plan_destroy(p);
     return st != PF_OK ? st : st2;
+}
+
+int pf_set_tuning_table(const char *path)
+{
+    std::vector<TableRow> rows;
+    if (path) {
+        std::string why;
+        const int st = load_table(path, rows, why);
+        if (st != PF_OK) return fail(st, why);
+    }
+    std::lock_guard<std::mutex> lock(g_table_mu);
+    g_table.swap(rows);
+    g_table_env_done = true;  // an explicit table (or none) overrides the environment
+    return PF_OK;
+}
+
+// Times `reps` back-to-back executions (after two warm-up launches) and
+// returns the mean microseconds per SpMV; the best of two trials.
+static int time_plan(pf_plan *p, const int *rp, const int *col, const void *val, const void *x, void *y, int reps,
+                     void *stream, double *us)
+{
+    void *e0 = nullptr, *e1 = nullptr;
+    PF_TRY(pfk_event_create(&e0), "event");
+    int st = pfk_event_create(&e1);
+    double best = 1e300;
+    for (int trial = 0; st == PF_OK && trial < 2; ++trial) {
+        for (int w = 0; st == PF_OK && w < 2; ++w) st = pf_plan_execute(p, rp, col, val, x, y, stream);
+        if (st == PF_OK) st = pfk_event_record(e0, stream);
+        for (int r = 0; st == PF_OK && r < reps; ++r) st = pf_plan_execute(p, rp, col, val, x, y, stream);
+        if (st == PF_OK) st = pfk_event_record(e1, stream);
+        if (st == PF_OK) st = pfk_event_sync(e1);
+        float ms = 0;
+        if (st == PF_OK) st = pfk_event_elapsed_ms(&ms, e0, e1);
+        if (st == PF_OK) best = std::min(best, 1e3 * ms / reps);
+    }
+    pfk_event_destroy(e0);
+    if (e1) pfk_event_destroy(e1);
+    if (st != PF_OK) return from_kernel_layer(st, "autotune timing");
+    *us = best;
+    return PF_OK;
+}
+
+int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x,
+                     void *d_y, int reps, int flags, void *stream, pf_tune_result *result)
+{
+    if (!plan || reps < 1 || reps > 100000) return fail(PF_ERR_INVALID, "pf_plan_autotune: bad plan or reps");
+    if (plan->m == 0 || plan->nnz == 0) {
+        if (result) {
+            std::memset(result, 0, sizeof *result);
+            result->variant = plan->info.variant;
+            result->tile = plan->info.tile;
+            result->run_tiles = plan->info.run_tiles;
+        }
+        return PF_OK;
+    }
+    const int dtype = plan->info.dtype;
+    double base_us = 0;
+    int st = time_plan(plan, d_row_ptr, d_col, d_val, d_x, d_y, reps, stream, &base_us);
+    if (st != PF_OK) return st;
+    pf_tune_result best;
+    std::memset(&best, 0, sizeof best);
+    best.variant = plan->info.variant;
+    best.tile = plan->info.tile;
+    best.run_tiles = plan->info.run_tiles;
+    best.keep_cached = plan->info.keep_cached;
+    best.us = base_us;
+    best.default_us = base_us;
+    best.candidates = 1;
+    pf_plan *best_plan = nullptr;
+
+    static const int kRuns[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    const int variants[] = {PF_ADAPTIVE, PF_FLAT, PF_PREFREE};
+    for (int variant : variants) {
+        if (variant == PF_PREFREE && !(flags & PF_TUNE_PREFREE)) continue;
+        int tiles[8];
+        const int nt = pfk_supported_tiles(variant, dtype, tiles, 8);
+        for (int ti = 0; ti < nt; ++ti) {
+            pf_plan *cand = nullptr;
+            st = plan_build(plan->stats, d_row_ptr, plan->m, plan->n, plan->nnz, dtype, variant, tiles[ti], stream,
+                            &cand);
+            if (st != PF_OK) {
+                if (best_plan) pf_plan_destroy(best_plan);
+                return st;
+            }
+            bool keep_cand = false;
+            const int nruns = variant == PF_ADAPTIVE ? (int)(sizeof kRuns / sizeof kRuns[0]) : 1;
+            const int nkeep = variant == PF_ADAPTIVE && (flags & PF_TUNE_KEEP_CACHED) ? 2 : 1;
+            int cand_run = cand->info.run_tiles, cand_keep = cand->info.keep_cached;
+            double cand_us = 1e300;
+            for (int ri = 0; ri < nruns; ++ri) {
+                for (int k = 0; k < nkeep; ++k) {
+                    if (variant == PF_ADAPTIVE) {
+                        cand->info.run_tiles = kRuns[ri];
+                        cand->info.keep_cached = k;
+                        set_grid(cand->info);
+                    }
+                    double us = 0;
+                    st = time_plan(cand, d_row_ptr, d_col, d_val, d_x, d_y, reps, stream, &us);
+                    if (st != PF_OK) {
+                        pf_plan_destroy(cand);
+                        if (best_plan) pf_plan_destroy(best_plan);
+                        return st;
+                    }
+                    ++best.candidates;
+                    if (us < cand_us) {
+                        cand_us = us;
+                        cand_run = cand->info.run_tiles;
+                        cand_keep = cand->info.keep_cached;
+                    }
+                }
+            }
+            if (cand_us < best.us) {
+                cand->info.run_tiles = cand_run;
+                cand->info.keep_cached = cand_keep;
+                set_grid(cand->info);
+                best.variant = cand->info.variant;
+                best.tile = cand->info.tile;
+                best.run_tiles = cand->info.run_tiles;
+                best.keep_cached = cand->info.keep_cached;
+                best.us = cand_us;
+                if (best_plan) pf_plan_destroy(best_plan);
+                best_plan = cand;
+                keep_cand = true;
+            }
+            if (!keep_cand) pf_plan_destroy(cand);
+        }
+    }
+    if (best_plan) {  // move the winner into the caller's plan
+        std::swap(plan->info, best_plan->info);
+        std::swap(plan->ws, best_plan->ws);
+        std::swap(plan->head, best_plan->head);
+        std::swap(plan->tail, best_plan->tail);
+        std::swap(plan->owner, best_plan->owner);
+        std::swap(plan->err, best_plan->err);
+        pf_plan_destroy(best_plan);
+    }
+    // y = A x with the chosen configuration, so that the caller's y is defined.
+    st = pf_plan_execute(plan, d_row_ptr, d_col, d_val, d_x, d_y, stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream) == PF_OK ? PF_OK : from_kernel_layer(PF_ERR_HIP, "autotune sync");
+    if (st == PF_OK && result) *result = best;
+    return st;
 }
 
 int pf_device_malloc(void **ptr, size_t bytes) { return from_kernel_layer(pfk_malloc(ptr, bytes), "device malloc"); }
