@@ -172,6 +172,7 @@ def write_table(best_by_dtype, thresholds, path):
 def measure(args):
     """One profiled process: 20 SpMVs of one candidate, then 3 copies of 256 MiB for the counter scale."""
     import torch
+    torch.cuda.init()  # before this library's first HIP call (see main)
     pf = load_pkg()
     matrix, dtype, variant, tile, run = args
     rp, col, val, x, m, n = load_matrix(matrix, dtype, "initvec")
@@ -231,6 +232,11 @@ def main():
     import yaml
     with open(args.config) as f:
         cfg = yaml.safe_load(f)
+    # torch's bundled HIP runtime must initialise before this library's first
+    # HIP call in the process (two runtimes share the device; the later one to
+    # start otherwise finds no GPU).
+    import torch
+    torch.cuda.init()
     out_dir = args.out or os.path.dirname(os.path.abspath(args.config))
     os.makedirs(out_dir, exist_ok=True)
     thresholds = cfg["size_thresholds"]
