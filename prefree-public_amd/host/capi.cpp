@@ -47,7 +47,7 @@ int default_tile(int variant, int dtype)
 {
     if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
     if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 512 : 440;
-    return 4096;
+    return dtype == PF_F64 ? 2048 : 4096;  // FLAT: the measured best per value type on C2-C5
 }
 
 // Wave64s of the ADAPTIVE kernel resident at once on an MI355X (256 CUs x 4

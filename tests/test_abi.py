@@ -105,11 +105,11 @@ def test_select_auto_small_matrix_takes_small_tile():
 
 
 def test_select_auto_very_short_rows_is_flat():
-    """C4 shape: 2.5 nnz per row -> FLAT 4096."""
+    """C4 shape: 2.5 nnz per row -> FLAT (2048 nnz per tile for fp64, 4096 for fp32)."""
     s = make_stats(20000000, 50000000, 14, empty=1640000)
-    for dt in ("f64", "f32"):
+    for dt, tile in (("f64", 2048), ("f32", 4096)):
         i = pf.select(s, dt, "auto")
-        assert i.variant == pf.FLAT and i.tile == 4096 and i.needs_fixup == 1
+        assert i.variant == pf.FLAT and i.tile == tile and i.needs_fixup == 1
 
 
 def test_select_auto_power_law_is_flat_dense_rows_adaptive():
@@ -125,7 +125,7 @@ def test_select_long_rows_need_the_combine_kernel():
     i = pf.select(s, "f64", "adaptive")
     assert i.needs_fixup == 1 and i.guess_spread == 0 and i.tile == 512
     f = pf.select(s, "f64", "flat")
-    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 4096) and f.needs_fixup == 1
+    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 2048) and f.needs_fixup == 1
     p = pf.select(s, "f64", "prefree")
     assert p.variant == pf.PREFREE and p.tile == 512 and p.ntiles == -(-15000000 // 512)
 
