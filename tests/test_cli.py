@@ -68,3 +68,45 @@ def test_cli_symmetric_power_law(tmp_path):
     r = run([f])
     assert r.returncode == 0, r.stdout + r.stderr
     assert "Success!" in r.stdout and "our_total:" in r.stdout
+
+
+PFSTAT = os.path.join(os.path.dirname(CLI), "pfstat")
+
+
+def test_pfstat_usage_and_bad_file():
+    r = subprocess.run([PFSTAT], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and "usage: pfstat" in r.stdout
+    r = subprocess.run([PFSTAT, "/nonexistent/x.mtx"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", ["prefree", "adaptive", "flat"])
+def test_pfstat_tile_statistics(tmp_path, variant):
+    """Per-tile spans and row-piece lengths: pieces partition the nnz, spans cover the rows in order."""
+    import csv
+    import oracle
+    rp, col, _ = pf.synth_csr(3, seed=4, scale_n=20000, dtypes=())
+    f = str(tmp_path / "pl.mtx")
+    write_mtx(f, rp, col)
+    out = tmp_path / "stat"
+    r = subprocess.run([PFSTAT, f, "--variant", variant, "--out", str(out)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    name = "pl.csv" if variant == "prefree" else f"pl_{variant}.csv"
+    rows = list(csv.DictReader(open(out / name)))
+    nnz = int(rp[-1])
+    tile = int(re.search(r"tiling: \w+, (\d+)", r.stdout).group(1))
+    m = len(rp) - 1
+    pieces = 0.0
+    for t in rows:
+        s, e = int(t["start_row"]), int(t["end_row"])
+        assert 0 <= s <= e <= m
+        assert int(t["max_row_length"]) <= (tile if variant != "adaptive" else tile + 252)
+        pieces += float(t["avg_row_length"]) * (e - s)
+    assert abs(pieces - nnz) <= 0.005 * len(rows) + 1e-6 * nnz    # averages are printed to 2 decimals
+    if variant == "prefree":
+        ref = oracle.pre_start_row(rp, tile)
+        assert [int(t["start_row"]) for t in rows] == [int(v) for v in ref[:len(rows)]]
+        assert len(rows) == -(-nnz // tile)
+    assert "PF_AUTO:" in r.stdout
