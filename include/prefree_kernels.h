@@ -10,6 +10,7 @@
  *                         with pre_start_rowPerTile (:3-28, launched :599) folded into the kernel
  *   pfk_spmv_adaptive     no counterpart: CSR-adaptive row blocks found on the fly
  *   pfk_spmv_flat         no counterpart launch: the flat nnz tiling of :407-428 without atomics
+ *                         (tile 256: runs of tiles with carried row sums, combine included)
  *   pfk_spmv_fixup        no counterpart: replaces the cross-tile atomicAdd (:67,:91,:142)
  *   pfk_adaptive_owners   no counterpart: the per-pattern split-row table the combine kernel reads
  *   pfk_row_stats         test/statistic.cu:38-98 (per-tile statistics), reduced to row-length stats
@@ -39,7 +40,7 @@ typedef struct pfk_spmv_args {
     int nnz;
     int tile;          /* keys (ADAPTIVE) or nnz (FLAT, PREFREE) per tile */
     int guess_spread;  /* 0 = plain 64-ary search */
-    int run_tiles;     /* ADAPTIVE: consecutive tiles per wave (0 = default 8) */
+    int run_tiles;     /* ADAPTIVE, FLAT 256: consecutive tiles per wave (0 = default 8) */
     int keep_cached;   /* ADAPTIVE: 1 = ordinary col/val loads (matrix fits the MALL), 0 = non-temporal */
     long long ntiles;
     void *head_slot;   /* [ntiles] partial of the split row entering a tile */
@@ -62,6 +63,8 @@ int pfk_adaptive_long_row_min(int dtype, int tile);
 /* Wave64s of the ADAPTIVE kernel for (dtype, tile) resident on the current device at once
  * (occupancy per CU x CUs); sizes the tile runs so that one dispatch round covers the matrix. */
 int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves);
+/* The same for the FLAT kernel of 256-nnz tiles (k_flow). */
+int pfk_flow_resident_waves(int dtype, long long *waves);
 
 /* Row statistics.  d_out: 44 unsigned long long (layout in prefree_kernels.hip). */
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,
@@ -81,6 +84,7 @@ int pfk_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
 int pfk_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
 int pfk_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream);
 int pfk_fill_zero(void *p, size_t bytes, void *stream);  /* a fill kernel, not hipMemsetAsync */
+int pfk_fill_u32(void *p, size_t nwords, unsigned value, void *stream);  /* fill kernel, 32-bit words */
 int pfk_stream_create(void **s);
 int pfk_stream_destroy(void *s);
 int pfk_stream_sync(void *s);

@@ -401,6 +401,16 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     uint32_t kb, ke;
     bool last;
     tile_keys<MERGE>(t, a.ntiles, K, a.m, a.nnz, kb, ke, last);
+    int c[S::kVPT][4];
+    T v[S::kVPT][4], xv[S::kVPT][4];
+    if constexpr (!MERGE) {
+        // FLAT: the nnz range [kb, min(ke, nnz)) is known before any row is
+        // found, so the col/val stream starts first and the row search
+        // overlaps its latency.
+        const int A0 = (int)kb, B0 = (int)min(ke, (uint32_t)a.nnz);
+        const int base0 = A0 & ~3;
+        issue_cv(a, base0, B0, B0 > A0 ? (B0 - base0 + 3) >> 2 : 0, c, v);
+    }
     search_tile_rows<MERGE>(a.rp, a.m, a.nnz, a.guess_spread, kb, ke, last, s_rows);
     __syncthreads();
     if (tid == 0) {
@@ -418,9 +428,7 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     const int base = A & ~3;
     const int nvec = B > A ? (B - base + 3) >> 2 : 0;
 
-    int c[S::kVPT][4];
-    T v[S::kVPT][4], xv[S::kVPT][4];
-    issue_cv(a, base, B, nvec, c, v);
+    if constexpr (MERGE) issue_cv(a, base, B, nvec, c, v);
     gather_x(a, nvec, c, xv);
     products_to_lds(s_prod, base, nvec, A, B, v, xv);
     __syncthreads();
@@ -919,6 +927,234 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     if (err && lane == 0) atomicOr(a.err, 1);
 }
 
+// ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
+//
+// Every wave64 walks a run of consecutive 256-nnz tiles (one 4-nnz vector per
+// lane).  A row that crosses a tile edge carries its partial sum in a register
+// into the next tile, continuing the sum in nnz order (rows of <= 16 nnz stay
+// bit-identical to the serial sum); only rows crossing a run edge leave
+// partials in head / tail slots for k_fixup (runs of R tiles = R*256 nnz).
+// Rows belong to the tile holding their first nnz (empty rows: the tile
+// holding nnz row_ptr[r]; trailing empty rows: the last tile).  Only a run's
+// first tile searches row_ptr; later tiles scan forward from the previous end.
+// Pipelining as in k_wave: while tile t is reduced, col/val of t+1 and the
+// row_ptr block of t+1 are in flight.
+
+constexpr int kFlowT = 256;                            // nnz per tile
+constexpr int kFlowRB = 3 * kWave;                     // row_ptr entries per block
+constexpr int kFlowLC = kFlowT / (kThreadMax + 1) + 2; // long pieces per tile
+
+// Row r's piece goes to y[r]; kFlowCarry: the row continuing into the next tile.
+constexpr int kFlowCarry = -1;
+
+template <typename T>
+__global__ __launch_bounds__(kWaveWG) void k_flow(Args<T> a)
+{
+    constexpr int NW = kWaveWG / kWave;
+    __shared__ __attribute__((aligned(16))) T s_prod_all[NW][kFlowT];
+    __shared__ int s_rp_all[NW][kFlowRB];
+    __shared__ int s_la_all[NW][kFlowLC], s_lb_all[NW][kFlowLC], s_ld_all[NW][kFlowLC];
+    __shared__ T s_cout_all[NW][1];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    T *s_prod = s_prod_all[wave];
+    int *s_rp = s_rp_all[wave];
+    int *s_la = s_la_all[wave], *s_lb = s_lb_all[wave], *s_ld = s_ld_all[wave];
+    T *s_cout = s_cout_all[wave];
+
+    const long long xcd = blockIdx.x % kXcds;
+    const long long wx = (blockIdx.x / kXcds) * NW + wave;  // run index inside its XCD
+    if (wx >= a.tx)
+        return;
+    const long long u = xcd * a.tx + wx;  // run
+    const long long t_begin = u * a.tpw;
+    long long t_end = t_begin + a.tpw;
+    if (t_end > a.ntiles) t_end = a.ntiles;
+    if (t_begin >= t_end)
+        return;
+
+    const int m = a.m, nnz = a.nnz;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc_full(a.y, (long long)m * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rrp = make_rsrc_full(a.rp, ((long long)m + 1) * 4);
+    const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rowner = make_rsrc_full(a.owner, a.ntiles * 4);
+
+    // row_ptr block: lane holds entries F + lane + 64 q (entries past m read 0 and are never used).
+    auto load_block = [&](int F, int (&rr)[3]) {
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+            rr[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rrp, (F + q * kWave + lane) * 4, 0, 0);
+    };
+    // col/val of tile t (16-byte loads; lanes past the tile read zeros).
+    int c[4];
+    T v[4];
+    auto issue_cv = [&](long long t) {
+        const int A = (int)(t * kFlowT);
+        const int B = min(A + kFlowT, nnz);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + A, (long long)(B - A) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + A, (long long)(B - A) * (long long)sizeof(T));
+        load4(rc, rv, lane, c, v);
+    };
+
+    // First row of the run's first tile: rows [0, F) start before its nnz A0.
+    const int A0 = (int)(t_begin * kFlowT);
+    int F = wave_search_lt<false>(a.rp, m, (uint32_t)A0, key_guess<false>((uint32_t)A0, m, nnz), a.guess_spread,
+                                  lane) + 1;
+    int rr[3];
+    load_block(F, rr);
+    issue_cv(t_begin);
+    // A row started before A0 and ending after it continues into the run.
+    int c_row = -1;
+    bool c_in_run = false;
+    T c_sum = T(0);
+    {
+        const int rpF = rlane(rr[0], 0);
+        if (F > 0 && rpF > A0) c_row = F - 1;
+    }
+
+    for (long long t = t_begin;; ++t) {
+        const int A = (int)(t * kFlowT);
+        const int B = min(A + kFlowT, nnz);
+        const bool last = t == a.ntiles - 1;
+        const int len_t = B - A;
+
+        // Rows starting in this tile: [F, Fn).
+#pragma unroll
+        for (int q = 0; q < 3; ++q) s_rp[q * kWave + lane] = rr[q];
+        int Fn;
+        if (last) {
+            Fn = m;
+        } else {
+            int j = -1;
+#pragma unroll
+            for (int q = 2; q >= 0; --q) {
+                const int idx = q * kWave + lane;
+                const uint64_t mask = __ballot(F + idx > m || rr[q] >= B);
+                if (mask) j = q * kWave + __ffsll((long long)mask) - 1;
+            }
+            Fn = j >= 0 ? F + j
+                        : wave_search_lt<false>(a.rp, m, (uint32_t)B, key_guess<false>((uint32_t)B, m, nnz), 0, lane) + 1;
+        }
+        const int nr = Fn - F;
+        const int rpF = rlane(rr[0], 0);  // row_ptr[F] (== nnz when F == m)
+
+        // x gathers of this tile, then the next tile's loads.
+        T xv[4];
+        T vt[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool in = lane * 4 + j < len_t;
+            xv[j] = buf_load(rx, in ? (uint32_t)c[j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+            vt[j] = v[j];
+        }
+        const bool more = t + 1 < t_end;
+        if (more) {
+            load_block(Fn, rr);
+            issue_cv(t + 1);
+        }
+        {
+            T p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = vt[j] * xv[j];
+            store4(s_prod + 4 * lane, p);
+        }
+        __builtin_amdgcn_wave_barrier();
+
+        int nl = 0;
+        // The row carried in from the previous tile: piece [A, min(row_ptr[F], B)).
+        if (c_row >= 0) {
+            const int cend = min(rpF, B);
+            const int clen = cend - A;
+            if (clen <= kThreadMax) {
+                T s = c_sum;
+                for (int q = 0; q < clen; ++q) s += s_prod[q];
+                c_sum = s;  // every lane computes the same sum (uniform loop)
+            } else {
+                T s = T(0);
+                for (int q = lane; q < clen; q += kWave) s += s_prod[q];
+                c_sum = c_sum + wave_sum(s);
+            }
+            if (rpF <= B) {  // the row ends in this tile
+                if (c_in_run) buf_store(ry, lane == 0 ? (uint32_t)c_row * (uint32_t)sizeof(T) : kOob, c_sum);
+                else buf_store(rhead, lane == 0 ? (uint32_t)u * (uint32_t)sizeof(T) : kOob, c_sum);
+                c_row = -1;
+            }
+        }
+        // Rows starting here, one lane each; pieces of more than 16 products are listed.
+        const int rpFn = nr < kFlowRB ? s_rp[nr] : a.rp[Fn];  // row_ptr[Fn]: end of the last row starting here
+        const bool cont = nr > 0 && !last && rpFn > B;
+        for (int q0 = 0; q0 < nr; q0 += kWave) {
+            const int i = q0 + lane;
+            const bool valid = i < nr;
+            int ra = 0, rbf = 0;
+            if (valid) {
+                ra = i < kFlowRB ? s_rp[i] : a.rp[F + i];
+                rbf = i + 1 < kFlowRB ? s_rp[i + 1] : a.rp[F + i + 1];
+            }
+            const int rb = min(rbf, B);
+            const int len = rb - ra;
+            const bool is_cont = cont && i == nr - 1;
+            T s = T(0);
+            bool lng = false;
+            if (valid) {
+                if (len <= kThreadMax) {
+                    for (int q = ra - A; q < rb - A; ++q) s += s_prod[q];
+                    if (is_cont) s_cout[0] = s;
+                } else {
+                    lng = true;
+                }
+            }
+            const uint64_t mask = __ballot(lng);
+            if (mask) {
+                const int pos = nl + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(mask >> 32),
+                                                                     __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
+                if (lng && pos < kFlowLC) {
+                    s_la[pos] = ra - A;
+                    s_lb[pos] = rb - A;
+                    s_ld[pos] = is_cont ? kFlowCarry : F + i;
+                }
+                nl += __popcll(mask);
+            }
+            buf_store(ry, valid && !lng && !is_cont ? (uint32_t)(F + i) * (uint32_t)sizeof(T) : kOob, s);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (nl > kFlowLC) {
+            nl = kFlowLC;  // cannot happen: at most 256/17 pieces exceed 16 products
+            atomicOr(a.err, 1);
+        }
+        for (int j = 0; j < nl; ++j) {
+            T s = T(0);
+            const int e1 = s_lb[j];
+            for (int q = s_la[j] + lane; q < e1; q += kWave) s += s_prod[q];
+            s = wave_sum(s);
+            const int dst = s_ld[j];
+            if (dst == kFlowCarry) {
+                if (lane == 0) s_cout[0] = s;
+            } else {
+                buf_store(ry, lane == 0 ? (uint32_t)dst * (uint32_t)sizeof(T) : kOob, s);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (cont) {  // the last row starting here continues into the next tile
+            c_row = F + nr - 1;
+            c_sum = s_cout[0];
+            c_in_run = true;
+        }
+        if (!more)
+            break;
+        F = Fn;
+    }
+    // Run end: the row leaving the run (if any) and its partial.
+    const uint32_t uslot = (uint32_t)u * (uint32_t)sizeof(T);
+    const bool leaving = c_row >= 0;
+    buf_store(rtail, lane == 0 && leaving && c_in_run ? uslot : kOob, c_sum);
+    buf_store(rhead, lane == 0 && leaving && !c_in_run ? uslot : kOob, c_sum);
+    buf_store(rowner, lane == 0 ? (uint32_t)u * 4u : kOob, leaving && c_in_run ? c_row : -1);
+}
+
 // Debug: the descriptor every tile of k_tiles computes.
 template <bool MERGE, int K, int LMAX, int SPAN_MAX>
 __global__ __launch_bounds__(kBS) void k_tile_desc(Args<double> a, int *__restrict__ out)
@@ -961,10 +1197,15 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
     __syncthreads();
     const long long t0 = (long long)blockIdx.x * kBS;
     const long long t = t0 + tid;
-    const int r = t < a.ntiles ? a.owner[t] : -1;
+    int r = t < a.ntiles ? a.owner[t] : -1;
+    if (r >= a.m) {  // an owner outside the matrix: report, never dereference
+        atomicOr(a.err, 1);
+        r = -1;
+    }
     if (r >= 0) {
         const long long last_key = (long long)a.rp[r + 1] - 1 + (MERGE ? r : 0);
-        const long long tb = last_key / K;  // last tile holding a piece of row r
+        long long tb = last_key / K;  // last tile holding a piece of row r
+        if (tb >= a.ntiles) { atomicOr(a.err, 1); tb = a.ntiles - 1; }
         if (tb - t <= kFixSerial) {
             T s = T(0);
             for (long long u = t + 1; u <= tb; ++u)
@@ -978,8 +1219,9 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
     const int n = s_n;
     for (int j = wave; j < n; j += kWaves) {
         const long long tl = t0 + s_list[j];
-        const int rl = a.owner[tl];
-        const long long tb = ((long long)a.rp[rl + 1] - 1 + (MERGE ? rl : 0)) / K;
+        const int rl = a.owner[tl];  // validated above (listed only when 0 <= rl < m)
+        long long tb = ((long long)a.rp[rl + 1] - 1 + (MERGE ? rl : 0)) / K;
+        if (tb >= a.ntiles) tb = a.ntiles - 1;
         T s = T(0);
         for (long long u = tl + 1 + lane; u <= tb; u += kWave)
             s += a.head[u];
@@ -1211,6 +1453,12 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
     }
 }
 
+__global__ __launch_bounds__(kBS) void k_fill_u32(uint32_t *__restrict__ p, size_t nwords, uint32_t value)
+{
+    for (size_t i = (size_t)blockIdx.x * kBS + threadIdx.x; i < nwords; i += (size_t)gridDim.x * kBS)
+        p[i] = value;
+}
+
 __global__ __launch_bounds__(kBS) void k_fill_zero(uint32_t *__restrict__ p, size_t nwords)
 {
     for (size_t i = (size_t)blockIdx.x * kBS + threadIdx.x; i < nwords; i += (size_t)gridDim.x * kBS)
@@ -1355,9 +1603,33 @@ int dispatch_adaptive(const pfk_spmv_args *a, void *stream)
     return PF_ERR_UNSUPPORTED;
 }
 
+// k_flow over runs of run_tiles tiles, then the combine of rows crossing run
+// edges (k_fixup over runs: "tile" = one run of run_tiles * 256 nnz).
+template <typename T>
+int launch_flow(const pfk_spmv_args *a, void *stream)
+{
+    Args<T> r = make_args<T>(a);
+    const long long run = a->run_tiles > 0 ? a->run_tiles : 8;
+    const long long nruns = (r.ntiles + run - 1) / run;
+    r.tpw = run;
+    r.tx = (nruns + kXcds - 1) / kXcds;
+    const long long grid = ((r.tx + 3) / 4) * kXcds;
+    hipLaunchKernelGGL((k_flow<T>), dim3((unsigned)grid), dim3(kWaveWG), 0, S(stream), r);
+    PFK_LAUNCHED("k_flow");
+    if (nruns > 1) {
+        Args<T> f = r;
+        f.ntiles = nruns;
+        const unsigned fgrid = (unsigned)((nruns + kBS - 1) / kBS);
+        hipLaunchKernelGGL((k_fixup<T, false>), dim3(fgrid), dim3(kBS), 0, S(stream), f, (int)(run * kFlowT));
+        PFK_LAUNCHED("k_fixup");
+    }
+    return PF_OK;
+}
+
 template <typename T>
 int dispatch_flat(const pfk_spmv_args *a, void *stream)
 {
+    if (a->tile == kFlowT) return launch_flow<T>(a, stream);
     if constexpr (sizeof(T) == 8) {
         switch (a->tile) {
         case 1024: return launch_tiles<T, false, 1024, 0>(a, stream);
@@ -1402,6 +1674,22 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     if (!args_ok(a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream) : PF_ERR_INVALID;
+}
+
+int pfk_flow_resident_waves(int dtype, long long *waves)
+{
+    if (!waves) return PF_ERR_INVALID;
+    int per_cu = 0;
+    if (dtype == PF_F64)
+        PFK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_flow<double>),
+                                                              kWaveWG, 0));
+    else if (dtype == PF_F32)
+        PFK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_flow<float>),
+                                                              kWaveWG, 0));
+    else
+        return PF_ERR_INVALID;
+    *waves = (long long)per_cu * (kWaveWG / kWave) * device_cus();
+    return PF_OK;
 }
 
 int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves)
@@ -1477,16 +1765,16 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
 {
     static const int ad64[] = {188, 238, 494, 512};  // k_wave: keys per wave tile
     static const int ad32[] = {440, 494, 1024};
-    static const int fl64[] = {1024, 2048, 4096}; // k_tiles: nnz per workgroup tile
-    static const int fl32[] = {2048, 4096};
+    static const int fl64[] = {256, 1024, 2048, 4096}; // k_flow (256), k_tiles: nnz per tile
+    static const int fl32[] = {256, 2048, 4096};
     static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
     if (variant == PF_PREFREE) { src = pf_tiles; n = 2; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 4; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 3; }
-    else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 3; }
-    else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 2; }
+    else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 4; }
+    else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 3; }
     else return 0;
     for (int i = 0; i < n && i < cap; ++i) tiles[i] = src[i];
     return n;
@@ -1595,6 +1883,17 @@ int pfk_fill_zero(void *p, size_t bytes, void *stream)
     const unsigned grid = grid_for((long long)words, kBS, 8192);
     hipLaunchKernelGGL(k_fill_zero, dim3(grid), dim3(kBS), 0, S(stream), static_cast<uint32_t *>(p), words);
     PFK_LAUNCHED("k_fill_zero");
+    return PF_OK;
+}
+
+int pfk_fill_u32(void *p, size_t nwords, unsigned value, void *stream)
+{
+    if (!p) return PF_ERR_INVALID;
+    if (!nwords) return PF_OK;
+    const unsigned grid = grid_for((long long)nwords, kBS, 8192);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid), dim3(kBS), 0, S(stream), static_cast<uint32_t *>(p), nwords,
+                       (uint32_t)value);
+    PFK_LAUNCHED("k_fill_u32");
     return PF_OK;
 }
 

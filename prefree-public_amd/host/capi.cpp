@@ -39,6 +39,9 @@ int from_kernel_layer(int status, const char *what)
 
 constexpr int kXcds = 8;
 
+// FLAT tiles of 256 nnz are walked in runs by k_flow (rows carried between tiles).
+constexpr int kFlowTile = 256;
+
 int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : 0; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -56,7 +59,8 @@ int default_tile(int variant, int dtype)
 long long nominal_resident_waves(int dtype, int tile)
 {
     int per_simd = 4;
-    if (dtype == PF_F64) per_simd = tile == 188 ? 7 : tile == 238 ? 6 : tile == 494 ? 4 : 3;
+    if (tile == kFlowTile) per_simd = dtype == PF_F64 ? 7 : 8;
+    else if (dtype == PF_F64) per_simd = tile == 188 ? 7 : tile == 238 ? 6 : tile == 494 ? 4 : 3;
     else per_simd = tile == 440 || tile == 494 ? 5 : 2;
     return 256LL * 4 * per_simd;
 }
@@ -199,7 +203,7 @@ bool tile_supported(int variant, int dtype, int tile)
 // workgroup, runs dealt evenly to the XCDs; one tile per workgroup otherwise.
 void set_grid(pf_plan_info &r)
 {
-    if (r.variant == PF_ADAPTIVE) {
+    if (r.variant == PF_ADAPTIVE || (r.variant == PF_FLAT && r.tile == kFlowTile)) {
         const long long run = r.run_tiles > 0 ? r.run_tiles : 1;
         const long long nruns = (r.ntiles + run - 1) / run;
         const long long tx = (nruns + kXcds - 1) / kXcds;
@@ -252,6 +256,10 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.long_row_min = 0;
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
         r.needs_fixup = r.ntiles > 1;
+        if (tile == kFlowTile) {  // runs of tiles, rows carried across tile edges inside a run
+            r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
+            r.needs_fixup = r.ntiles > r.run_tiles;
+        }
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
     } else if (variant == PF_PREFREE) {
         r.long_row_min = 0;
@@ -295,10 +303,13 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     pf_plan_info info;
     const int st = finish_info(s, dtype, variant, tile > 0 ? tile : default_tile(variant, dtype), &info);
     if (st != PF_OK) return st;
-    if (info.variant == PF_ADAPTIVE) {
+    if (info.variant == PF_ADAPTIVE || (info.variant == PF_FLAT && info.tile == kFlowTile)) {
         long long resident = 0;
-        if (pfk_adaptive_resident_waves(dtype, info.tile, &resident) == PF_OK && resident > 0) {
+        const int rs = info.variant == PF_ADAPTIVE ? pfk_adaptive_resident_waves(dtype, info.tile, &resident)
+                                                   : pfk_flow_resident_waves(dtype, &resident);
+        if (rs == PF_OK && resident > 0) {
             info.run_tiles = choose_run(info.tile, info.ntiles, resident);
+            if (info.variant == PF_FLAT) info.needs_fixup = info.ntiles > info.run_tiles;
             set_grid(info);
         }
     }
@@ -325,6 +336,8 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
         p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
     }
     rc = pfk_fill_zero(p->err, 256, stream);
+    // Every owner slot starts as "no split row": a combine kernel never reads an unset slot.
+    if (rc == PF_OK && p->owner) rc = pfk_fill_u32(p->owner, (size_t)info.ntiles, 0xFFFFFFFFu, stream);
     if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
         // The split-row owner of every tile depends on row_ptr only: build it once.
         pfk_spmv_args a;
@@ -467,6 +480,8 @@ int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles)
 {
     if (!plan || run_tiles < 1 || run_tiles > 256) return fail(PF_ERR_INVALID, "run_tiles must be in 1..256");
     plan->info.run_tiles = run_tiles;
+    if (plan->info.variant == PF_FLAT && plan->info.tile == kFlowTile)
+        plan->info.needs_fixup = plan->info.ntiles > run_tiles;
     set_grid(plan->info);
     return PF_OK;
 }
@@ -518,8 +533,9 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         if (plan->info.needs_fixup) PF_TRY(pfk_spmv_fixup(dt, 1, &a, stream), "split-row combine");
         return PF_OK;
     case PF_FLAT:
-        PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");
-        if (plan->info.needs_fixup) PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
+        PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");  // tile 256 launches its own combine
+        if (plan->info.needs_fixup && plan->info.tile != kFlowTile)
+            PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
         return PF_OK;
     case PF_PREFREE:
         PF_TRY(pfk_spmv_prefree(dt, &a, stream), "prefree kernel");
@@ -644,15 +660,17 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
                 return st;
             }
             bool keep_cand = false;
-            const int nruns = variant == PF_ADAPTIVE ? (int)(sizeof kRuns / sizeof kRuns[0]) : 1;
+            const bool walks_runs = variant == PF_ADAPTIVE || (variant == PF_FLAT && tiles[ti] == kFlowTile);
+            const int nruns = walks_runs ? (int)(sizeof kRuns / sizeof kRuns[0]) : 1;
             const int nkeep = variant == PF_ADAPTIVE && (flags & PF_TUNE_KEEP_CACHED) ? 2 : 1;
             int cand_run = cand->info.run_tiles, cand_keep = cand->info.keep_cached;
             double cand_us = 1e300;
             for (int ri = 0; ri < nruns; ++ri) {
                 for (int k = 0; k < nkeep; ++k) {
-                    if (variant == PF_ADAPTIVE) {
+                    if (walks_runs) {
                         cand->info.run_tiles = kRuns[ri];
-                        cand->info.keep_cached = k;
+                        if (variant == PF_ADAPTIVE) cand->info.keep_cached = k;
+                        else cand->info.needs_fixup = cand->info.ntiles > kRuns[ri];
                         set_grid(cand->info);
                     }
                     double us = 0;
@@ -673,6 +691,8 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
             if (cand_us < best.us) {
                 cand->info.run_tiles = cand_run;
                 cand->info.keep_cached = cand_keep;
+                if (cand->info.variant == PF_FLAT && cand->info.tile == kFlowTile)
+                    cand->info.needs_fixup = cand->info.ntiles > cand_run;
                 set_grid(cand->info);
                 best.variant = cand->info.variant;
                 best.tile = cand->info.tile;

@@ -139,8 +139,8 @@ def test_select_rejects_bad_arguments():
 def test_supported_tiles():
     assert pf.supported_tiles("adaptive", "f64") == [188, 238, 494, 512]
     assert pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
-    assert pf.supported_tiles("flat", "f64") == [1024, 2048, 4096]
-    assert pf.supported_tiles("flat", "f32") == [2048, 4096]
+    assert pf.supported_tiles("flat", "f64") == [256, 1024, 2048, 4096]
+    assert pf.supported_tiles("flat", "f32") == [256, 2048, 4096]
     assert pf.supported_tiles("prefree", "f64") == [512, 1024]
 
 

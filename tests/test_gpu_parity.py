@@ -95,6 +95,48 @@ def test_adaptive_run_lengths(run):
         assert_parity(rp, col, v["f64"], x, ys[1], "f64", what=f"C{cfg} run {run}")
 
 
+@pytest.mark.parametrize("run", [1, 2, 3, 8, 64])
+def test_flow_run_lengths(run):
+    """FLAT 256 (rows carried across tile edges): any run length, KAT exact, U[-1,1] within tolerance."""
+    import torch
+    from gpu_util import DEV, dev
+    for cfg, scale in ((2, 300), (3, 60000), (5, 40000), (4, 400000), (1, 0)):
+        rp, col, v = pf.synth_csr(cfg, seed=13, scale_n=scale)
+        m = len(rp) - 1
+        x = pf.synth_x(cfg, m, seed=13)["f64"]
+        d = [dev(rp), dev(col), dev(v["f64"]), dev(x)]
+        kv, kx = oracle.initvec(len(col), np.float64), oracle.initvec(m, np.float64)
+        with pf.Plan(d[0], d[1], m, m, len(col), "f64", "flat", 256) as p:
+            p.set_run_tiles(run)
+            for vals, xs, exact in ((v["f64"], x, False), (kv, kx, kat_exact_possible(rp, "f64"))):
+                y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+                p.execute(d[0], d[1], dev(vals), dev(xs), y)
+                torch.cuda.synchronize()
+                assert_parity(rp, col, vals, xs, y.cpu().numpy(), "f64", exact=exact, what=f"C{cfg} flow run {run}")
+            p.check()
+
+
+def test_flow_short_rows_bit_exact_within_runs():
+    """Rows of <= 16 nnz that do not cross a run edge are summed in nnz order, even across tile edges."""
+    import torch
+    from gpu_util import DEV, dev
+    rp, col, v = pf.synth_csr(2, seed=14, scale_n=300)
+    m = len(rp) - 1
+    x = pf.synth_x(2, m, seed=14)["f64"]
+    d = [dev(rp), dev(col), dev(v["f64"]), dev(x)]
+    with pf.Plan(d[0], d[1], m, m, len(col), "f64", "flat", 256) as p:
+        p.set_run_tiles(1 << 8)   # runs of 256 tiles: 65536 nnz, so the matrix spans few runs
+        y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+        p.execute(*d, y)
+        torch.cuda.synchronize()
+    ref = oracle.spmv_serial(rp, col, v["f64"], x)
+    got = y.cpu().numpy()
+    run_nnz = 256 * 256
+    crossing = (rp[:-1] // run_nnz) != ((np.maximum(rp[1:], rp[:-1] + 1) - 1) // run_nnz)
+    assert np.array_equal(got[~crossing], ref[~crossing])
+    assert_parity(rp, col, v["f64"], x, got, "f64", what="flow C2")
+
+
 def test_adaptive_cache_policy_bit_identical():
     """Ordinary and non-temporal col/val loads give the same y bit for bit."""
     import torch
