@@ -47,6 +47,8 @@ typedef struct pfk_spmv_args {
     void *tail_slot;   /* [ntiles] partial of the split row leaving a tile */
     int *owner_row;    /* [ntiles] row whose split starts in the tile, or -1 */
     int *err_flag;     /* [1] set non-zero by a kernel that finds an inconsistent tile */
+    int *row_map;      /* FLAT 1024/2048: [2*(ntiles+1)] (first row, row_ptr there) of each tile, or NULL */
+    int map_ready;     /* 1: row_map holds the rows an earlier call found; 0: search (and record them) */
 } pfk_spmv_args;
 
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream);

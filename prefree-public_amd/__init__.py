@@ -89,7 +89,8 @@ class SpmvArgs(ctypes.Structure):
                 ("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("m", ctypes.c_int), ("n", ctypes.c_int),
                 ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
-                ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p)]
+                ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p), ("row_map", ctypes.c_void_p),
+                ("map_ready", ctypes.c_int)]
 
 
 _lib = None

@@ -927,6 +927,148 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     if (err && lane == 0) atomicOr(a.err, 1);
 }
 
+// ---- k_flat: FLAT tiles with the row search remembered across calls ---------
+//
+// One workgroup (4 wave64s) per tile of K nnz, XCD-interleaved.  A FLAT tile's
+// nnz range [kb, min(kb + K, nnz)) is known before any row is, so every wave
+// starts streaming col/val at once (16-byte non-temporal loads, K/1024
+// vectors per lane).  The tile's rows are [f, l): f = the first row starting
+// at or after kb, l = the first at or after the next tile's start.
+//   MODE kFlatSearch: waves 2 and 3 find f and l by a wave-cooperative search
+//     of row_ptr and record (f, row_ptr[f]) in the plan's row map;
+//   MODE kFlatMemo: the row map written by an earlier search is read instead
+//     (one load), so later calls of a plan skip the search latency;
+//   MODE kFlatDesc: search only, the descriptors written to dbg (index test).
+// From f, l, row_ptr[f] and row_ptr[l] every lane derives the tile
+// descriptor with no further memory access; the row bounds are staged in LDS
+// while x is gathered.
+
+constexpr int kFlatSearch = 0, kFlatMemo = 1, kFlatDesc = 2;
+
+template <typename T, int K>
+struct FlatShape {
+    static constexpr int kVPT = K / (4 * kBS);                   // 4-nnz vectors per lane
+    static constexpr int kRpCap = K + 2;                         // row bounds staged in LDS
+    static constexpr int kWaveCap = K / (kThreadMax + 1) + 1;
+    static constexpr int kBlockCap = K / (kWaveMax + 1) + 1;
+    static_assert(kVPT * 4 * kBS == K, "K must be a multiple of 1024");
+};
+
+template <typename T, int K, int MODE>
+__global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, int *__restrict__ dbg)
+{
+    using S = FlatShape<T, K>;
+    constexpr int VPT = S::kVPT;
+    constexpr bool DESC = MODE == kFlatDesc;
+    __shared__ __attribute__((aligned(16))) T s_prod[DESC ? 4 : K];
+    __shared__ int s_rp[DESC ? 4 : S::kRpCap];
+    __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l]
+    __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const long long t = xcd_tile(a.g8);
+    if (t >= a.ntiles)
+        return;  // whole workgroup: padding of the XCD mapping
+    const int m = a.m, nnz = a.nnz;
+    const bool last = t == a.ntiles - 1;
+    const int kb = (int)(t * K);
+    const int B = last ? nnz : kb + K;                 // nnz range [kb, B)
+    const uint32_t ke = last ? (uint32_t)nnz + 1u : (uint32_t)(kb + K);
+
+    int c[VPT][4];
+    T v[VPT][4];
+    if (!DESC) {
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B - kb) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, (long long)(B - kb) * (long long)sizeof(T));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k)
+            load4(rc, rv, tid + k * kBS, c[k], v[k]);
+    }
+    if (MODE == kFlatMemo) {
+        if (tid == 0) {
+            const int2 e0 = reinterpret_cast<const int2 *>(map)[t];
+            const int2 e1 = reinterpret_cast<const int2 *>(map)[t + 1];
+            s_info[0] = e0.x; s_info[1] = e0.y; s_info[2] = e1.x; s_info[3] = e1.y;
+        }
+    } else if (wave == 2) {  // f: first row with row_ptr >= kb
+        const int f = wave_search_lt<false>(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
+                                            a.guess_spread, lane) + 1;
+        if (lane == 0) {
+            const int rpf = a.rp[f];
+            s_info[0] = f; s_info[1] = rpf;
+            if (MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(f, rpf);
+        }
+    } else if (wave == 3) {  // l: first row with row_ptr >= ke (m for the last tile)
+        const int l = last ? m
+                           : wave_search_lt<false>(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane) + 1;
+        if (lane == 0) {
+            const int rpl = a.rp[l];
+            s_info[2] = l; s_info[3] = rpl;
+            if (MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(l, rpl);
+        }
+    }
+    if (tid == 0) { L.nw = 0; L.nb = 0; }
+    __syncthreads();
+
+    // Descriptor (the FLAT case of make_desc, from the four values).
+    const int f = s_info[0], rpf = s_info[1], l = s_info[2], rpl = s_info[3];
+    const int head = (f > 0 && rpf > kb) ? 1 : 0;  // row f-1 started before kb and reaches into the tile
+    int lo_row = head ? f - 1 : f;
+    int nr = l - lo_row;
+    int tail = (!last && f < l && rpl > (int)ke) ? 1 : 0;
+    const bool ok = f >= 0 && l >= f && l <= m && lo_row >= 0 && rpf >= kb && rpf <= nnz && rpl <= nnz &&
+                    (last || rpl >= (int)ke);
+    if (!ok) {  // row_ptr (or the row map) changed after planning
+        if (tid == 0) atomicOr(a.err, 1);
+        lo_row = 0; nr = 0; tail = 0;
+    }
+    if (DESC) {
+        if (tid == 0) {
+            int *o = dbg + 8 * t;
+            o[0] = lo_row; o[1] = nr;
+            o[2] = nr > 0 ? kb : 0; o[3] = nr > 0 ? (f < l ? (tail ? (int)ke : rpl) : min(rpf, B)) : 0;
+            o[4] = ok ? head : 0; o[5] = tail; o[6] = f; o[7] = l;
+        }
+        return;
+    }
+
+    // Row bounds into LDS (global row_ptr is read directly beyond kRpCap).
+    for (int i = tid; i <= nr && i < S::kRpCap; i += kBS)
+        s_rp[i] = a.rp[lo_row + i];
+    {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int vec = tid + k * kBS;
+            const bool in = 4 * vec < B - kb;
+            T p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const T xv = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+                p[j] = v[k][j] * xv;  // slots past the tile are never read
+            }
+            store4(s_prod + 4 * vec, p);
+        }
+    }
+    __syncthreads();
+
+    const int *__restrict__ rp = a.rp;
+    reduce_tile(
+        s_prod, L, kb, kb, B, nr,
+        [&](int i, int &ra, int &rb) {
+            ra = i < S::kRpCap ? s_rp[i] : rp[lo_row + i];
+            rb = i + 1 < S::kRpCap ? s_rp[i + 1] : rp[lo_row + i + 1];
+        },
+        [&](int i, T s) {
+            if (head && i == 0) a.head[t] = s;
+            else if (tail && i == nr - 1) a.tail[t] = s;
+            else a.y[lo_row + i] = s;
+        });
+    if (tid == 0) a.owner[t] = tail ? lo_row + nr - 1 : -1;
+}
+
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
 //
 // Every wave64 walks a run of consecutive 256-nnz tiles (one 4-nnz vector per
@@ -1626,21 +1768,33 @@ int launch_flow(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
+// k_flat: search (and record the row map when the plan has one) or, once the
+// map is recorded, read it.
+template <typename T, int K>
+int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
+{
+    Args<T> r = make_args<T>(a);
+    const long long grid = r.g8 * kXcds;
+    if (dbg)
+        hipLaunchKernelGGL((k_flat<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr, dbg);
+    else if (a->row_map && a->map_ready)
+        hipLaunchKernelGGL((k_flat<T, K, kFlatMemo>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, a->row_map,
+                           nullptr);
+    else
+        hipLaunchKernelGGL((k_flat<T, K, kFlatSearch>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
+                           a->row_map, nullptr);
+    PFK_LAUNCHED("k_flat");
+    return PF_OK;
+}
+
 template <typename T>
 int dispatch_flat(const pfk_spmv_args *a, void *stream)
 {
     if (a->tile == kFlowT) return launch_flow<T>(a, stream);
-    if constexpr (sizeof(T) == 8) {
-        switch (a->tile) {
-        case 1024: return launch_tiles<T, false, 1024, 0>(a, stream);
-        case 2048: return launch_tiles<T, false, 2048, 0>(a, stream);
-        case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
-        }
-    } else {
-        switch (a->tile) {
-        case 2048: return launch_tiles<T, false, 2048, 0>(a, stream);
-        case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
-        }
+    switch (a->tile) {
+    case 1024: return launch_flat<T, 1024>(a, nullptr, stream);
+    case 2048: return launch_flat<T, 2048>(a, nullptr, stream);
+    case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
     }
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
     return PF_ERR_UNSUPPORTED;
@@ -1765,8 +1919,8 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
 {
     static const int ad64[] = {188, 238, 494, 512};  // k_wave: keys per wave tile
     static const int ad32[] = {440, 494, 1024};
-    static const int fl64[] = {256, 1024, 2048, 4096}; // k_flow (256), k_tiles: nnz per tile
-    static const int fl32[] = {256, 2048, 4096};
+    static const int fl64[] = {256, 1024, 2048, 4096}; // nnz per tile: k_flow, k_flat, k_flat, k_tiles
+    static const int fl32[] = {256, 1024, 2048, 4096};
     static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
@@ -1774,7 +1928,7 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
     else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 4; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 3; }
     else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 4; }
-    else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 3; }
+    else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 4; }
     else return 0;
     for (int i = 0; i < n && i < cap; ++i) tiles[i] = src[i];
     return n;
@@ -1822,9 +1976,9 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
         case 1024: return launch_stream<double, 1024, adaptive_lmax(1024), true>(a, d_out, stream);
         }
     } else {
-        switch (a->tile) {
-        case 1024: return launch_flat_desc<1024>(a, d_out, stream);
-        case 2048: return launch_flat_desc<2048>(a, d_out, stream);
+        switch (a->tile) {  // the descriptors of the kernel each FLAT tile size runs
+        case 1024: return launch_flat<double, 1024>(a, d_out, stream);
+        case 2048: return launch_flat<double, 2048>(a, d_out, stream);
         case 4096: return launch_flat_desc<4096>(a, d_out, stream);
         }
     }

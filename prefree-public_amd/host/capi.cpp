@@ -42,6 +42,9 @@ constexpr int kXcds = 8;
 // FLAT tiles of 256 nnz are walked in runs by k_flow (rows carried between tiles).
 constexpr int kFlowTile = 256;
 
+// FLAT tiles of 1024 and 2048 nnz (k_flat) remember the rows their search found.
+bool uses_row_map(int variant, int tile) { return variant == PF_FLAT && (tile == 1024 || tile == 2048); }
+
 int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : 0; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -50,7 +53,7 @@ int default_tile(int variant, int dtype)
 {
     if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
     if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 512 : 440;
-    return dtype == PF_F64 ? 2048 : 4096;  // FLAT: the measured best per value type on C2-C5
+    return dtype == PF_F64 ? 1024 : 2048;  // FLAT: the measured best per value type on C2-C5
 }
 
 // Wave64s of the ADAPTIVE kernel resident at once on an MI355X (256 CUs x 4
@@ -165,28 +168,35 @@ bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
     return false;
 }
 
-// PF_AUTO: a tuning-table row if one matches; else FLAT for very short rows
-// (fewer than 3 nnz per row on average: the merged tiles spend most keys on
-// rows) and for short-row matrices that also hold split rows (power-law).
-// Otherwise ADAPTIVE: the short-row tile when no row exceeds 16 nnz, the
-// general tile else; a matrix too small to give half the resident waves a
-// tile takes the smallest tile.
+// PF_AUTO: a tuning-table row if one matches; else
+//   * a matrix too small to give half the resident waves a 512-key tile:
+//     ADAPTIVE with the smallest tile (one wave per tile, launch-bound anyway);
+//   * long rows carrying most of the nnz (mean >= 16 and rows beyond ADAPTIVE's
+//     long-row threshold, e.g. a few dense rows): ADAPTIVE 512, whose runs
+//     keep a long row's pieces on one wave;
+//   * otherwise FLAT (1024 nnz per tile for fp64, 2048 for fp32), whose rows
+//     are found once and remembered by the plan.
+// (Measured on MI355X: C2 FLAT 61.6 us vs ADAPTIVE 75.0; C4 FLAT 366 vs 400;
+// C3 FLAT 222 vs 230; C5 ADAPTIVE 1489 vs FLAT 1582.)
 Choice auto_choice(const pf_row_stats &s, int dtype)
 {
     Choice c;
     if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
     const int big = default_tile(PF_ADAPTIVE, dtype);
-    const bool very_short = m > 0 && nnz < 3 * m;
-    const bool split_rows = s.max_row_len > pfk_adaptive_long_row_min(dtype, big);
-    if (very_short || (split_rows && nnz < 16 * m)) {
-        c.variant = PF_FLAT;
-        c.tile = default_tile(PF_FLAT, dtype);
+    if (dtype == PF_F64 && (nnz + m) / big < nominal_resident_waves(dtype, big) / 2) {
+        c.variant = PF_ADAPTIVE;
+        c.tile = 188;
         return c;
     }
-    c.variant = PF_ADAPTIVE;
-    c.tile = s.max_row_len <= 16 ? 494 : big;
-    if (dtype == PF_F64 && (nnz + m) / c.tile < nominal_resident_waves(dtype, c.tile) / 2) c.tile = 188;
+    const bool long_rows = s.max_row_len > pfk_adaptive_long_row_min(dtype, big);
+    if (long_rows && nnz >= 16 * m) {
+        c.variant = PF_ADAPTIVE;
+        c.tile = big;
+        return c;
+    }
+    c.variant = PF_FLAT;
+    c.tile = default_tile(PF_FLAT, dtype);
     return c;
 }
 
@@ -256,11 +266,12 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.long_row_min = 0;
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
         r.needs_fixup = r.ntiles > 1;
+        r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
+        if (uses_row_map(PF_FLAT, tile)) r.workspace_bytes += (size_t)(r.ntiles + 1) * 8 + 256;
         if (tile == kFlowTile) {  // runs of tiles, rows carried across tile edges inside a run
             r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
             r.needs_fixup = r.ntiles > r.run_tiles;
         }
-        r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
     } else if (variant == PF_PREFREE) {
         r.long_row_min = 0;
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
@@ -285,6 +296,8 @@ struct pf_plan {
     void *tail = nullptr;
     int *owner = nullptr;
     int *err = nullptr;
+    int *row_map = nullptr;  // FLAT 1024/2048: tile -> (first row, row_ptr there), found by the first call
+    bool map_ready = false;  // set once a call that records the map has been issued
 };
 
 namespace {
@@ -334,6 +347,10 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
         p->head = w + 256;
         p->tail = w + 256 + slots;
         p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
+        if (uses_row_map(info.variant, info.tile)) {
+            const size_t owners = ((size_t)info.ntiles * 4 + 255) & ~(size_t)255;
+            p->row_map = reinterpret_cast<int *>(w + 256 + 2 * slots + owners);
+        }
     }
     rc = pfk_fill_zero(p->err, 256, stream);
     // Every owner slot starts as "no split row": a combine kernel never reads an unset slot.
@@ -526,6 +543,8 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.tail_slot = plan->tail;
     a.owner_row = plan->owner;
     a.err_flag = plan->err;
+    a.row_map = plan->row_map;
+    a.map_ready = plan->map_ready ? 1 : 0;
     const int dt = plan->info.dtype;
     switch (plan->info.variant) {
     case PF_ADAPTIVE:
@@ -534,6 +553,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         return PF_OK;
     case PF_FLAT:
         PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");  // tile 256 launches its own combine
+        if (plan->row_map) plan->map_ready = true;  // later calls on this stream read the recorded rows
         if (plan->info.needs_fixup && plan->info.tile != kFlowTile)
             PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
         return PF_OK;
@@ -713,6 +733,8 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
         std::swap(plan->tail, best_plan->tail);
         std::swap(plan->owner, best_plan->owner);
         std::swap(plan->err, best_plan->err);
+        std::swap(plan->row_map, best_plan->row_map);
+        std::swap(plan->map_ready, best_plan->map_ready);
         pf_plan_destroy(best_plan);
     }
     // y = A x with the chosen configuration, so that the caller's y is defined.

@@ -20,19 +20,33 @@ def dev(a, min_len=4):
     return torch.from_numpy(a).to(DEV)
 
 
-def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=1):
-    """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info)."""
+def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2):
+    """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info).
+
+    The plan executes `repeat` times, y refilled with `fill` before each call,
+    and the last call's y is returned.  A plan's first call may differ in
+    kind from later ones (FLAT records the rows its search found and later
+    calls read them), so the first and the last y must agree bit for bit
+    (up to atomic ordering for the reference's PREFREE algorithm)."""
     m, n, nnz = len(rp) - 1, len(x), len(col)
     d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
     y = torch.full((max(m, 1),), fill, dtype=TORCH[dtype], device=DEV)
     stream = torch.cuda.current_stream()
+    first = None
     with pf.Plan(d_rp, d_col, m, n, nnz, dtype, variant, tile, stream=stream) as p:
-        for _ in range(repeat):
+        for k in range(repeat):
+            y.fill_(fill)
             p.execute(d_rp, d_col, d_val, d_x, y, stream=stream)
+            if k == 0:
+                torch.cuda.synchronize()
+                first = y[:m].cpu().numpy()
         torch.cuda.synchronize()
         p.check(stream=stream)
         info = p.info.as_dict()
-    return y[:m].cpu().numpy(), info
+    out = y[:m].cpu().numpy()
+    if info["variant_name"] != "prefree":
+        assert np.array_equal(first, out, equal_nan=True), "first and repeated calls of one plan differ"
+    return out, info
 
 
 def kat_exact_possible(rp, dtype):

@@ -78,26 +78,22 @@ def run_for(ntiles, resident, cap=16):
     return max(1, min(cap, -(-ntiles // resident)))
 
 
-def test_select_auto_banded_is_adaptive_short_row_tile():
-    """C2 shape: rows of <= 16 nnz -> ADAPTIVE 494 keys per tile, runs of at most 3 tiles."""
+def test_select_auto_banded_is_flat():
+    """C2 shape: short regular rows -> FLAT, 1024 nnz per tile (fp64) / 2048 (fp32)."""
     s = make_stats(4194304, 20963328, 5)
     i = pf.select(s, "f64", "auto")
-    assert i.variant == pf.ADAPTIVE and i.tile == 494
-    assert i.ntiles == -(-(20963328 + 4194304) // 494)
-    assert i.run_tiles == run_for(i.ntiles, 256 * 4 * 4, cap=3) == 3
-    nruns = -(-i.ntiles // i.run_tiles)
-    assert i.grid % 8 == 0 and i.grid * 4 >= nruns and (i.grid - 8) * 4 < nruns
-    assert i.needs_fixup == 0 and i.guess_spread == 64
-    assert i.long_row_min == pf.adaptive_long_row_min("f64", 494) == 16
+    assert i.variant == pf.FLAT and i.tile == 1024
+    assert i.ntiles == -(-20963328 // 1024) and i.needs_fixup == 1
+    assert i.grid % 8 == 0 and i.grid >= i.ntiles and i.grid - 8 < i.ntiles
+    assert i.guess_spread == 64
     i32 = pf.select(s, "f32", "auto")
-    assert i32.variant == pf.ADAPTIVE and i32.tile == 494
-    wide = pf.select(make_stats(4194304, 4194304 * 40, 60), "f64", "auto")   # rows up to 60 nnz
-    assert wide.variant == pf.ADAPTIVE and wide.tile == 512 and wide.long_row_min == 252
-    assert wide.run_tiles == run_for(wide.ntiles, 256 * 4 * 3)
+    assert i32.variant == pf.FLAT and i32.tile == 2048
+    wide = pf.select(make_stats(4194304, 4194304 * 40, 60), "f64", "auto")   # rows up to 60 nnz: still FLAT
+    assert wide.variant == pf.FLAT and wide.tile == 1024
 
 
 def test_select_auto_small_matrix_takes_small_tile():
-    """C1 shape: too few 512-key tiles for the device -> 188-key tiles, one per run."""
+    """C1 shape: too few 512-key tiles for the device -> ADAPTIVE, 188-key tiles, one per run."""
     s = make_stats(4096, 65536, 16)
     i = pf.select(s, "f64", "auto")
     assert i.variant == pf.ADAPTIVE and i.tile == 188 and i.run_tiles == 1
@@ -105,19 +101,20 @@ def test_select_auto_small_matrix_takes_small_tile():
 
 
 def test_select_auto_very_short_rows_is_flat():
-    """C4 shape: 2.5 nnz per row -> FLAT (2048 nnz per tile for fp64, 4096 for fp32)."""
+    """C4 shape: 2.5 nnz per row -> FLAT."""
     s = make_stats(20000000, 50000000, 14, empty=1640000)
-    for dt, tile in (("f64", 2048), ("f32", 4096)):
+    for dt, tile in (("f64", 1024), ("f32", 2048)):
         i = pf.select(s, dt, "auto")
         assert i.variant == pf.FLAT and i.tile == tile and i.needs_fixup == 1
 
 
 def test_select_auto_power_law_is_flat_dense_rows_adaptive():
-    """C3 shape (short rows plus split rows) -> FLAT; C5 shape (long mean row) -> ADAPTIVE with the combine kernel."""
+    """C3 shape (short rows plus a few long ones) -> FLAT; C5 shape (dense rows hold most nnz) -> ADAPTIVE 512."""
     c3 = pf.select(make_stats(2000000, 15200000, 200000), "f64", "auto")
-    assert c3.variant == pf.FLAT
+    assert c3.variant == pf.FLAT and c3.tile == 1024
     c5 = pf.select(make_stats(1000000, 315647995, 499000), "f64", "auto")
     assert c5.variant == pf.ADAPTIVE and c5.tile == 512 and c5.needs_fixup == 1 and c5.run_tiles == 16
+    assert c5.run_tiles == run_for(c5.ntiles, 256 * 4 * 3)
 
 
 def test_select_long_rows_need_the_combine_kernel():
@@ -125,7 +122,7 @@ def test_select_long_rows_need_the_combine_kernel():
     i = pf.select(s, "f64", "adaptive")
     assert i.needs_fixup == 1 and i.guess_spread == 0 and i.tile == 512
     f = pf.select(s, "f64", "flat")
-    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 2048) and f.needs_fixup == 1
+    assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 1024) and f.needs_fixup == 1
     p = pf.select(s, "f64", "prefree")
     assert p.variant == pf.PREFREE and p.tile == 512 and p.ntiles == -(-15000000 // 512)
 
@@ -140,7 +137,7 @@ def test_supported_tiles():
     assert pf.supported_tiles("adaptive", "f64") == [188, 238, 494, 512]
     assert pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
     assert pf.supported_tiles("flat", "f64") == [256, 1024, 2048, 4096]
-    assert pf.supported_tiles("flat", "f32") == [256, 2048, 4096]
+    assert pf.supported_tiles("flat", "f32") == [256, 1024, 2048, 4096]
     assert pf.supported_tiles("prefree", "f64") == [512, 1024]
 
 

@@ -36,15 +36,18 @@ def test_table_rows_drive_auto(table):
 def test_table_rows_with_unsupported_tiles_are_skipped(table):
     table.write_text("x -1 f64 adaptive 777 0 0\n")
     pf.set_tuning_table(str(table))
-    assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").tile == 494   # built-in rule
+    assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").tile == 1024   # built-in rule
 
 
 def test_clearing_the_table_restores_the_rules(table):
     table.write_text("x -1 f64 flat 1024 0 0\n")
     pf.set_tuning_table(str(table))
-    assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").variant == pf.FLAT
-    pf.set_tuning_table(None)
+    assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").tile == 1024
+    table.write_text("x -1 f64 adaptive 494 3 0\n")
+    pf.set_tuning_table(str(table))
     assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").variant == pf.ADAPTIVE
+    pf.set_tuning_table(None)
+    assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").variant == pf.FLAT
 
 
 @pytest.mark.parametrize("text", ["x 10 f64 adaptive\n", "x 10 f16 flat 4096 0 0\n", "x 10 f64 dense 4096 0 0\n",
