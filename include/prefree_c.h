@@ -82,6 +82,8 @@ typedef struct pf_plan_info {
     long long ntiles;     /* logical tiles */
     long long grid;       /* workgroups launched (tiles rounded up to a multiple of the XCD count) */
     size_t workspace_bytes;
+    int row_aligned;      /* FLAT 1024/2048: 1 = each tile owns the rows starting in it (all rows hold at
+                             most 256 nnz); no row is split and no combine kernel runs */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -114,6 +116,10 @@ int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out);
 int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles);
 /* Tuning: cache policy of the ADAPTIVE col/val stream (1 = ordinary loads, 0 = non-temporal). */
 int pf_plan_set_keep_cached(pf_plan *plan, int keep_cached);
+/* FLAT 1024/2048 only: 1 = row-aligned tiles (chosen at planning when every
+ * row holds at most 256 nnz), 0 = nnz tiles with split rows combined by a
+ * second kernel.  Both give the same y. */
+int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).

@@ -49,7 +49,12 @@ typedef struct pfk_spmv_args {
     int *err_flag;     /* [1] set non-zero by a kernel that finds an inconsistent tile */
     int *row_map;      /* FLAT 1024/2048: [2*(ntiles+1)] (first row, row_ptr there) of each tile, or NULL */
     int map_ready;     /* 1: row_map holds the rows an earlier call found; 0: search (and record them) */
+    int row_aligned;   /* FLAT 1024/2048: 1 = each tile owns the rows starting in it (every row must hold
+                          at most PFK_ALIGN_ROW_MAX nnz); no split rows, no pfk_spmv_fixup */
 } pfk_spmv_args;
+
+/* Longest row a row-aligned FLAT plan accepts. */
+#define PFK_ALIGN_ROW_MAX 256
 
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream);

@@ -59,7 +59,7 @@ class PlanInfo(ctypes.Structure):
                 ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
                 ("grid", ctypes.c_longlong),
-                ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -90,7 +90,7 @@ class SpmvArgs(ctypes.Structure):
                 ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p), ("row_map", ctypes.c_void_p),
-                ("map_ready", ctypes.c_int)]
+                ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int)]
 
 
 _lib = None
@@ -123,6 +123,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
         _sig(L.pf_plan_set_run_tiles, [_vp, _i])
         _sig(L.pf_plan_set_keep_cached, [_vp, _i])
+        _sig(L.pf_plan_set_row_aligned, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -264,6 +265,9 @@ class Plan:
     def set_keep_cached(self, keep_cached):
         _check(lib().pf_plan_set_keep_cached(self._h, int(bool(keep_cached))), "pf_plan_set_keep_cached")
 
+    def set_row_aligned(self, row_aligned):
+        _check(lib().pf_plan_set_row_aligned(self._h, int(bool(row_aligned))), "pf_plan_set_row_aligned")
+
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),
                "pf_plan_execute")
@@ -295,12 +299,14 @@ def spmv(row_ptr, col, val, x, y, m, n, nnz, dtype="f64", variant="auto", stream
                          dtype_code(dtype), variant_code(variant), _s(stream)), "pf_spmv")
 
 
-def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, run_tiles=0, stream=None):
-    """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT into `out` (int32[8*ntiles])."""
+def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, run_tiles=0, stream=None,
+                     row_aligned=False):
+    """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT (split or row-aligned
+    tiles) into `out` (int32[8*ntiles])."""
     total = nnz + m if merged else nnz
     ntiles = max(1, -(-total // tile))
     a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
-                 run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag))
+                 run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag), row_aligned=int(bool(row_aligned)))
     _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
            "pfk_debug_tile_desc")
     return ntiles

@@ -49,6 +49,17 @@ constexpr int kWaves = kBS / kWave;
 constexpr int kThreadMax = 16;         // rows up to this length: one lane each
 constexpr int kWaveMax = 512;          // rows up to this length: one wave each
 
+// Workgroup barrier for LDS traffic only.  __syncthreads() also orders global
+// memory, which on gfx950 means waiting for every outstanding vector memory
+// operation (loads in flight for the next tile, y stores not yet acknowledged);
+// the tile kernels exchange data between threads only through LDS.
+__device__ __forceinline__ void lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <typename T>
 struct Args {
     const int *__restrict__ rp;
@@ -347,7 +358,7 @@ __device__ __forceinline__ void reduce_tile(const T *s_prod, ReduceLds<T, WCAP, 
             if (j < BCAP) { L.bl[j] = i; L.ba[j] = a0; L.bb[j] = a0 + len; }
         }
     }
-    __syncthreads();
+    lds_sync();
     const int nw = min(L.nw, WCAP);
     for (int j = wave; j < nw; j += kWaves) {
         T s = T(0);
@@ -365,7 +376,7 @@ __device__ __forceinline__ void reduce_tile(const T *s_prod, ReduceLds<T, WCAP, 
         s = wave_sum(s);
         if (lane == 0)
             L.red[wave] = s;
-        __syncthreads();
+        lds_sync();
         if (tid == 0) {
             T tot = L.red[0];
 #pragma unroll
@@ -373,9 +384,9 @@ __device__ __forceinline__ void reduce_tile(const T *s_prod, ReduceLds<T, WCAP, 
                 tot += L.red[w];
             put(L.bl[j], tot);
         }
-        __syncthreads();
+        lds_sync();
     }
-    __syncthreads();
+    lds_sync();
     if (tid == 0) {
         L.nw = 0;
         L.nb = 0;
@@ -412,7 +423,7 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
         issue_cv(a, base0, B0, B0 > A0 ? (B0 - base0 + 3) >> 2 : 0, c, v);
     }
     search_tile_rows<MERGE>(a.rp, a.m, a.nnz, a.guess_spread, kb, ke, last, s_rows);
-    __syncthreads();
+    lds_sync();
     if (tid == 0) {
         const TileDesc d = make_desc<MERGE, LMAX, S::kSpanMax>(a.rp, a.m, a.nnz, kb, ke, s_rows[0],
                                                                 s_rows[1], a.err);
@@ -422,7 +433,7 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
         L.nb = 0;
         a.owner[t] = d.tail ? d.lo_row + d.nr - 1 : -1;
     }
-    __syncthreads();
+    lds_sync();
     const int lo_row = s_desc[0], nr = s_desc[1], A = s_desc[2], B = s_desc[3];
     const int head = s_desc[4], tail = s_desc[5];
     const int base = A & ~3;
@@ -431,7 +442,7 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     if constexpr (MERGE) issue_cv(a, base, B, nvec, c, v);
     gather_x(a, nvec, c, xv);
     products_to_lds(s_prod, base, nvec, A, B, v, xv);
-    __syncthreads();
+    lds_sync();
 
     const int *__restrict__ rp = a.rp;
     reduce_tile(
@@ -508,6 +519,18 @@ __device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t of
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// One value, non-temporal (the row-aligned kernels' y stores).
+__device__ __forceinline__ void buf_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, double v)
+{
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)off, 0, kAuxNt);
+}
+
+__device__ __forceinline__ void buf_store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, (int)off, 0, kAuxNt);
 }
 
 // A resource over a whole array addressed with 32-bit byte offsets (the plan
@@ -1010,7 +1033,7 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
         }
     }
     if (tid == 0) { L.nw = 0; L.nb = 0; }
-    __syncthreads();
+    lds_sync();
 
     // Descriptor (the FLAT case of make_desc, from the four values).
     const int f = s_info[0], rpf = s_info[1], l = s_info[2], rpl = s_info[3];
@@ -1052,7 +1075,7 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
             store4(s_prod + 4 * vec, p);
         }
     }
-    __syncthreads();
+    lds_sync();
 
     const int *__restrict__ rp = a.rp;
     reduce_tile(
@@ -1067,6 +1090,231 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
             else a.y[lo_row + i] = s;
         });
     if (tid == 0) a.owner[t] = tail ? lo_row + nr - 1 : -1;
+}
+
+// ---- k_rows: FLAT tiles that own whole rows --------------------------------
+//
+// For matrices whose rows all hold at most kAlignRowMax nnz (checked at
+// planning).  Tile t owns the rows that start in its nnz range [kb, kb + K):
+// rows [f, l), with f and l as in k_flat (the row map is the same).  No row is
+// split, so a step is this one launch, with no head / tail partials and no
+// combine kernel.  The tile's products are the nnz [row_ptr[f], row_ptr[l]),
+// which start at or after kb and end before kb + K + kAlignRowMax:
+//   * the nominal range [kb, kb + K) is streamed before the rows are known;
+//     its nnz before row_ptr[f] belong to the previous tile's last row and
+//     are not gathered;
+//   * the overflow [kb + K, row_ptr[l]) of the tile's last row (fewer than
+//     kAlignRowMax nnz, one per lane) is read once l is known.
+//   MODE kFlatMemo: every wave reads (f, row_ptr[f]) of tiles t and t + 1 from
+//     the row map itself (a uniform load, no barrier), so its row_ptr,
+//     overflow and gather loads follow its col/val loads at once;
+//   MODE kFlatSearch: waves 2 and 3 search and record the map, as in k_flat;
+//   MODE kFlatDesc: descriptors only (index test).
+
+constexpr int kAlignRowMax = PFK_ALIGN_ROW_MAX;
+
+template <typename T, int K>
+struct RowsShape {
+    static constexpr int kVPT = K / (4 * kBS);                   // 4-nnz vectors per lane
+    static constexpr int kProd = K + kAlignRowMax;               // products: nominal range + overflow
+    static constexpr int kRpCap = K + 2;                         // row bounds staged in LDS
+    static constexpr int kRpPer = (kRpCap + kBS - 1) / kBS;      // row_ptr loads per lane
+    static constexpr int kWaveCap = kProd / (kThreadMax + 1) + 1;
+    static constexpr int kBlockCap = kProd / (kWaveMax + 1) + 1;
+    static_assert(kVPT * 4 * kBS == K, "K must be a multiple of 1024");
+    static_assert(kAlignRowMax <= kBS, "one overflow nnz per lane");
+};
+
+// A row-aligned tile once its rows are known (see k_rows): rows [f0, f0 + nr),
+// products of nnz [A, B), nov overflow nnz past kb + K, cnt row bounds staged.
+struct RowsDesc {
+    int kb, B0, f0, nr, nov, A, B, cnt;
+};
+
+// The tile's loads after its col / val: the overflow col / val, the x gathers
+// of the nominal range and of the overflow, then row_ptr[f0 .. f0 + cnt).  The
+// overflow loads and gathers are issued by every lane (an empty range or an
+// out-of-range offset reads nothing), so the compiler's wait counts in front
+// of the gathers are exact; the row_ptr loads skip whole waves past cnt and
+// come last, where a wait for all of them costs nothing.
+template <typename T, int K>
+__device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, const int (&c)[RowsShape<T, K>::kVPT][4],
+                                           T (&xv)[RowsShape<T, K>::kVPT][4], T &ov, T &xo,
+                                           int (&rr)[RowsShape<T, K>::kRpPer])
+{
+    using S = RowsShape<T, K>;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int ob = d.nov > 0 ? d.kb + K : 0;
+    const __amdgpu_buffer_rsrc_t rco = make_rsrc(a.col + ob, (long long)d.nov * 4);
+    const __amdgpu_buffer_rsrc_t rvo = make_rsrc(a.val + ob, (long long)d.nov * (long long)sizeof(T));
+    const int oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
+    ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+#pragma unroll
+    for (int k = 0; k < S::kVPT; ++k) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int g = d.kb + 4 * (tid + k * kBS) + j;
+            const bool use = g >= d.A && g < d.B && g < d.B0;  // slots outside [A, B) are never read
+            xv[k][j] = buf_load(rx, use ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+        }
+    }
+    xo = buf_load(rx, tid < d.nov ? (uint32_t)oc * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    const __amdgpu_buffer_rsrc_t rrp = make_rsrc(a.rp + d.f0, (long long)d.cnt * 4);
+#pragma unroll
+    for (int q = 0; q < S::kRpPer; ++q) {
+        rr[q] = 0;
+        if (q * kBS + wave * kWave < d.cnt)
+            rr[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rrp, (tid + q * kBS) * 4, 0, 0);
+    }
+}
+
+// Products and row bounds of a row-aligned tile into LDS.
+template <typename T, int K>
+__device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsShape<T, K>::kVPT][4],
+                                           const T (&xv)[RowsShape<T, K>::kVPT][4], T ov, T xo,
+                                           const int (&rr)[RowsShape<T, K>::kRpPer], T *s_prod, int *s_rp)
+{
+    using S = RowsShape<T, K>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < S::kVPT; ++k) {
+        T p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            p[j] = v[k][j] * xv[k][j];
+        store4(s_prod + 4 * (tid + k * kBS), p);
+    }
+    if (tid < d.nov) s_prod[K + tid] = ov * xo;
+#pragma unroll
+    for (int q = 0; q < S::kRpPer; ++q)
+        if (tid + q * kBS < d.cnt) s_rp[tid + q * kBS] = rr[q];
+}
+
+// Row sums of a staged row-aligned tile into y.  Bounds come from LDS; a tile
+// with more rows than LDS holds (long runs of empty rows) reads the rest from
+// row_ptr in a separate branch, so the common path waits on LDS only and
+// leaves the y stores and any loads already issued for the next tile in flight.
+template <typename T, int K>
+__device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, const T *s_prod, const int *s_rp,
+                                            ReduceLds<T, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
+{
+    using S = RowsShape<T, K>;
+    if (d.nr < S::kRpCap) {
+        // y[f0 .. f0 + nr) through a resource over exactly those rows, written
+        // non-temporally: y is not read again here, and keeping it out of L2
+        // leaves room for x (C4: 355 instead of 377 us per call).
+        const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f0, (long long)d.nr * (long long)sizeof(T));
+        reduce_tile(
+            s_prod, L, d.kb, d.A, d.B, d.nr,
+            [&](int i, int &ra, int &rb) {
+                ra = s_rp[i];
+                rb = s_rp[i + 1];
+            },
+            [&](int i, T s) { buf_store_nt(ry, (uint32_t)i * (uint32_t)sizeof(T), s); });
+    } else {  // more rows than LDS holds: any number, up to m
+        const int *__restrict__ rp = a.rp + d.f0;
+        T *__restrict__ y = a.y + d.f0;
+        reduce_tile(
+            s_prod, L, d.kb, d.A, d.B, d.nr,
+            [&](int i, int &ra, int &rb) {
+                ra = i < S::kRpCap ? s_rp[i] : rp[i];
+                rb = i + 1 < S::kRpCap ? s_rp[i + 1] : rp[i + 1];
+            },
+            [&](int i, T s) { y[i] = s; });
+    }
+}
+
+template <typename T, int K, int MODE>
+__global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, int *__restrict__ dbg)
+{
+    using S = RowsShape<T, K>;
+    constexpr int VPT = S::kVPT;
+    constexpr bool DESC = MODE == kFlatDesc;
+    __shared__ __attribute__((aligned(16))) T s_prod[DESC ? 4 : S::kProd];
+    __shared__ int s_rp[DESC ? 4 : S::kRpCap];
+    __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l] (search modes)
+    __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const long long t = xcd_tile(a.g8);
+    if (t >= a.ntiles)
+        return;  // whole workgroup: padding of the XCD mapping
+    const int m = a.m, nnz = a.nnz;
+    const bool last = t == a.ntiles - 1;
+    const int kb = (int)(t * K);
+    const int B0 = last ? nnz : kb + K;                // nominal nnz range [kb, B0)
+    const uint32_t ke = last ? (uint32_t)nnz + 1u : (uint32_t)(kb + K);
+
+    int f = 0, rpf = 0, l = 0, rpl = 0;
+    if (MODE == kFlatMemo) {
+        const int2 *mp = reinterpret_cast<const int2 *>(map);
+        const int2 e0 = mp[t], e1 = mp[t + 1];
+        f = e0.x; rpf = e0.y; l = e1.x; rpl = e1.y;
+    }
+    int c[VPT][4];
+    T v[VPT][4];
+    if (!DESC) {
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B0 - kb) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, (long long)(B0 - kb) * (long long)sizeof(T));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k)
+            load4(rc, rv, tid + k * kBS, c[k], v[k]);
+    }
+    if (MODE != kFlatMemo) {
+        if (wave == 2) {  // f: first row with row_ptr >= kb
+            const int ff = wave_search_lt<false>(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
+                                                 a.guess_spread, lane) + 1;
+            if (lane == 0) {
+                const int r = a.rp[ff];
+                s_info[0] = ff; s_info[1] = r;
+                if (MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
+            }
+        } else if (wave == 3) {  // l: first row with row_ptr >= ke (m for the last tile)
+            const int ll = last ? m
+                                : wave_search_lt<false>(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread,
+                                                        lane) + 1;
+            if (lane == 0) {
+                const int r = a.rp[ll];
+                s_info[2] = ll; s_info[3] = r;
+                if (MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
+            }
+        }
+        lds_sync();
+        f = s_info[0]; rpf = s_info[1]; l = s_info[2]; rpl = s_info[3];
+    }
+    if (tid == 0) { L.nw = 0; L.nb = 0; }
+
+    // The tile's rows [f, l) and nnz [rpf, rpl); everything read below is
+    // bounded by these checks even if row_ptr changed after planning.
+    const int ovf = last ? 0 : rpl - (int)ke;  // nnz of the last row past the nominal range
+    const bool ok = f >= 0 && l >= f && l <= m && rpf >= kb && rpf <= rpl && rpl <= nnz &&
+                    (last ? (l == m && rpl == nnz) : (ovf >= 0 && ovf < kAlignRowMax));
+    if (!ok && tid == 0) atomicOr(a.err, 1);
+    const int f0 = ok ? f : 0;
+    const int nr = ok ? l - f : 0;
+    const int nov = ok ? ovf : 0;
+    const int A = ok ? rpf : kb, B = ok ? rpl : kb;
+    if (DESC) {
+        if (tid == 0) {
+            int *o = dbg + 8 * t;
+            o[0] = f0; o[1] = nr; o[2] = A; o[3] = B;
+            o[4] = 0; o[5] = 0; o[6] = f; o[7] = l;
+        }
+        return;
+    }
+
+    const RowsDesc d{kb, B0, f0, nr, nov, A, B, min(nr + 1, S::kRpCap)};
+    T xv[VPT][4], ov, xo;
+    int rr[S::kRpPer];
+    rows_loads<T, K>(a, d, c, xv, ov, xo, rr);
+    rows_stage<T, K>(d, v, xv, ov, xo, rr, s_prod, s_rp);
+    lds_sync();
+
+    rows_reduce<T, K>(a, d, s_prod, s_rp, L);
 }
 
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
@@ -1768,13 +2016,26 @@ int launch_flow(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
-// k_flat: search (and record the row map when the plan has one) or, once the
-// map is recorded, read it.
+// k_flat (split rows) or k_rows (row-aligned tiles): search (and record the
+// row map when the plan has one) or, once the map is recorded, read it.
 template <typename T, int K>
 int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
 {
     Args<T> r = make_args<T>(a);
     const long long grid = r.g8 * kXcds;
+    if (a->row_aligned) {
+        if (dbg)
+            hipLaunchKernelGGL((k_rows<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr,
+                               dbg);
+        else if (a->row_map && a->map_ready)
+            hipLaunchKernelGGL((k_rows<T, K, kFlatMemo>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
+                               a->row_map, nullptr);
+        else
+            hipLaunchKernelGGL((k_rows<T, K, kFlatSearch>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
+                               a->row_map, nullptr);
+        PFK_LAUNCHED("k_rows");
+        return PF_OK;
+    }
     if (dbg)
         hipLaunchKernelGGL((k_flat<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr, dbg);
     else if (a->row_map && a->map_ready)
@@ -1790,6 +2051,10 @@ int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
 template <typename T>
 int dispatch_flat(const pfk_spmv_args *a, void *stream)
 {
+    if (a->row_aligned && a->tile != 1024 && a->tile != 2048) {
+        snprintf(g_err, sizeof g_err, "row-aligned FLAT tiles are 1024 or 2048 nnz, not %d", a->tile);
+        return PF_ERR_INVALID;
+    }
     if (a->tile == kFlowT) return launch_flow<T>(a, stream);
     switch (a->tile) {
     case 1024: return launch_flat<T, 1024>(a, nullptr, stream);

@@ -267,7 +267,13 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
         r.needs_fixup = r.ntiles > 1;
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
-        if (uses_row_map(PF_FLAT, tile)) r.workspace_bytes += (size_t)(r.ntiles + 1) * 8 + 256;
+        if (uses_row_map(PF_FLAT, tile)) {
+            r.workspace_bytes += (size_t)(r.ntiles + 1) * 8 + 256;
+            // Short rows only: each tile owns the rows starting in it, nothing
+            // is split and a step is one launch.
+            r.row_aligned = s.max_row_len <= PFK_ALIGN_ROW_MAX ? 1 : 0;
+            if (r.row_aligned) r.needs_fixup = 0;
+        }
         if (tile == kFlowTile) {  // runs of tiles, rows carried across tile edges inside a run
             r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
             r.needs_fixup = r.ntiles > r.run_tiles;
@@ -510,6 +516,18 @@ int pf_plan_set_keep_cached(pf_plan *plan, int keep_cached)
     return PF_OK;
 }
 
+int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned)
+{
+    if (!plan || (row_aligned != 0 && row_aligned != 1)) return fail(PF_ERR_INVALID, "row_aligned must be 0 or 1");
+    if (!uses_row_map(plan->info.variant, plan->info.tile))
+        return fail(PF_ERR_UNSUPPORTED, "row-aligned tiles are FLAT 1024 or 2048");
+    if (row_aligned && plan->stats.max_row_len > PFK_ALIGN_ROW_MAX)
+        return fail(PF_ERR_INVALID, "a row holds more than " + std::to_string(PFK_ALIGN_ROW_MAX) + " nnz");
+    plan->info.row_aligned = row_aligned;
+    plan->info.needs_fixup = row_aligned ? 0 : (plan->info.ntiles > 1);
+    return PF_OK;
+}
+
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out)
 {
     if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
@@ -545,6 +563,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.err_flag = plan->err;
     a.row_map = plan->row_map;
     a.map_ready = plan->map_ready ? 1 : 0;
+    a.row_aligned = plan->info.row_aligned;
     const int dt = plan->info.dtype;
     switch (plan->info.variant) {
     case PF_ADAPTIVE:

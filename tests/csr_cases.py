@@ -68,7 +68,13 @@ def edge_cases(seed=7):
 
 # ---- tiling model of k_tiles (ADAPTIVE: merged keys; FLAT: nnz keys) ----------
 
-def tile_model(rp, K, merged, lmax):
+def tile_model(rp, K, merged, lmax, aligned=False):
+    """Per-tile (lo_row, n_rows, A, B, head, tail): rows [lo, lo+n) and nnz [A, B).
+
+    aligned (FLAT only): every tile owns the rows starting in its nnz range
+    [kb, kb+K) (the last tile also the rows starting at nnz), whole, with the
+    nnz [row_ptr[f], row_ptr[l]); no row is split.
+    """
     rp = np.asarray(rp, dtype=np.int64)
     m = len(rp) - 1
     nnz = int(rp[-1])
@@ -82,6 +88,9 @@ def tile_model(rp, K, merged, lmax):
         ke = (total if merged else total + 1) if last else kb + K
         f = int(np.searchsorted(keys, kb, side="left"))
         l = m if last else int(np.searchsorted(keys, ke, side="left"))
+        if aligned:
+            desc[t] = (f, l - f, rp[f], rp[l], 0, 0)
+            continue
         head = tail = 0
         A = B = 0
         h = f - 1

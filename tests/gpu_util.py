@@ -20,20 +20,23 @@ def dev(a, min_len=4):
     return torch.from_numpy(a).to(DEV)
 
 
-def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2):
+def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2, row_aligned=None):
     """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info).
 
     The plan executes `repeat` times, y refilled with `fill` before each call,
     and the last call's y is returned.  A plan's first call may differ in
     kind from later ones (FLAT records the rows its search found and later
     calls read them), so the first and the last y must agree bit for bit
-    (up to atomic ordering for the reference's PREFREE algorithm)."""
+    (up to atomic ordering for the reference's PREFREE algorithm).
+    row_aligned (FLAT 1024/2048): force row-aligned (1) or split-row (0) tiles."""
     m, n, nnz = len(rp) - 1, len(x), len(col)
     d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
     y = torch.full((max(m, 1),), fill, dtype=TORCH[dtype], device=DEV)
     stream = torch.cuda.current_stream()
     first = None
     with pf.Plan(d_rp, d_col, m, n, nnz, dtype, variant, tile, stream=stream) as p:
+        if row_aligned is not None:
+            p.set_row_aligned(row_aligned)
         for k in range(repeat):
             y.fill_(fill)
             p.execute(d_rp, d_col, d_val, d_x, y, stream=stream)

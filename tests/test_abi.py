@@ -83,7 +83,8 @@ def test_select_auto_banded_is_flat():
     s = make_stats(4194304, 20963328, 5)
     i = pf.select(s, "f64", "auto")
     assert i.variant == pf.FLAT and i.tile == 1024
-    assert i.ntiles == -(-20963328 // 1024) and i.needs_fixup == 1
+    assert i.ntiles == -(-20963328 // 1024)
+    assert i.row_aligned == 1 and i.needs_fixup == 0     # rows <= 256 nnz: tiles own whole rows
     assert i.grid % 8 == 0 and i.grid >= i.ntiles and i.grid - 8 < i.ntiles
     assert i.guess_spread == 64
     i32 = pf.select(s, "f32", "auto")
@@ -105,13 +106,13 @@ def test_select_auto_very_short_rows_is_flat():
     s = make_stats(20000000, 50000000, 14, empty=1640000)
     for dt, tile in (("f64", 1024), ("f32", 2048)):
         i = pf.select(s, dt, "auto")
-        assert i.variant == pf.FLAT and i.tile == tile and i.needs_fixup == 1
+        assert i.variant == pf.FLAT and i.tile == tile and i.row_aligned == 1 and i.needs_fixup == 0
 
 
 def test_select_auto_power_law_is_flat_dense_rows_adaptive():
     """C3 shape (short rows plus a few long ones) -> FLAT; C5 shape (dense rows hold most nnz) -> ADAPTIVE 512."""
     c3 = pf.select(make_stats(2000000, 15200000, 200000), "f64", "auto")
-    assert c3.variant == pf.FLAT and c3.tile == 1024
+    assert c3.variant == pf.FLAT and c3.tile == 1024 and c3.row_aligned == 0 and c3.needs_fixup == 1
     c5 = pf.select(make_stats(1000000, 315647995, 499000), "f64", "auto")
     assert c5.variant == pf.ADAPTIVE and c5.tile == 512 and c5.needs_fixup == 1 and c5.run_tiles == 16
     assert c5.run_tiles == run_for(c5.ntiles, 256 * 4 * 3)
@@ -125,6 +126,16 @@ def test_select_long_rows_need_the_combine_kernel():
     assert f.variant == pf.FLAT and f.ntiles == -(-15000000 // 1024) and f.needs_fixup == 1
     p = pf.select(s, "f64", "prefree")
     assert p.variant == pf.PREFREE and p.tile == 512 and p.ntiles == -(-15000000 // 512)
+
+
+def test_select_row_aligned_threshold():
+    """FLAT 1024/2048 tiles own whole rows when no row exceeds PFK_ALIGN_ROW_MAX (256) nnz."""
+    for max_len, aligned in ((256, 1), (257, 0)):
+        for dt, tile in (("f64", 1024), ("f32", 2048)):
+            i = pf.select(make_stats(1000000, 20000000, max_len), dt, "flat")
+            assert i.tile == tile and i.row_aligned == aligned and i.needs_fixup == 1 - aligned
+    for variant in ("adaptive", "prefree"):
+        assert pf.select(make_stats(1000000, 20000000, 5), "f64", variant).row_aligned == 0
 
 
 def test_select_rejects_bad_arguments():

@@ -57,6 +57,35 @@ def test_tile_descriptors_match_model(merged, tile, spread, run):
         assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
 
 
+@pytest.mark.parametrize("spread", [0, 64, 1000])
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_row_aligned_descriptors_match_model(tile, spread):
+    """Row-aligned FLAT tiles (rows starting in the tile, whole): exact descriptors wherever no
+    tile's last row reaches 256 or more nnz past the tile's nominal end (always so when rows hold at
+    most 256 nnz, the planning rule); otherwise the kernel refuses (error flag), since its product
+    buffer holds K + 255 nnz."""
+    for name, rp in CASES:
+        m, nnz = len(rp) - 1, int(rp[-1])
+        if m == 0:
+            continue
+        model = tile_model(rp, tile, False, 0, aligned=True)
+        ntiles = len(model)
+        out = torch.full((8 * ntiles,), -7, dtype=torch.int32, device=DEV)
+        err = torch.zeros(64, dtype=torch.int32, device=DEV)
+        got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, False, out, err, guess_spread=spread,
+                                        row_aligned=True)
+        torch.cuda.synchronize()
+        assert got_tiles == ntiles
+        kb = np.arange(ntiles - 1, dtype=np.int64) * tile
+        if np.any(model[:-1, 3] - (kb + tile) >= 256):
+            assert int(err.cpu()[0]) != 0, name
+            continue
+        assert int(err.cpu()[0]) == 0, name
+        got = out.cpu().numpy().reshape(ntiles, 8)[:, :6].astype(np.int64)
+        bad = np.flatnonzero(np.any(got != model, axis=1))
+        assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
+
+
 OWNER_TILES = [(dt, t) for dt in ("f64", "f32") for t in pf.supported_tiles("adaptive", dt)]
 
 

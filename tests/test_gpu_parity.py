@@ -169,6 +169,62 @@ def test_adaptive_short_rows_bit_exact():
         assert_parity(rp, col, v["f64"], x, y, "f64", exact=True, what=f"C{cfg}")
 
 
+ALIGN_MAX = 256   # PFK_ALIGN_ROW_MAX
+
+
+def short_row_cases():
+    out = [(name, rp, col, n) for name, rp, col, n in CASES if len(rp) > 1 and np.diff(rp).max() <= ALIGN_MAX]
+    for cfg, scale in ((1, 0), (2, 300), (4, 400000)):
+        rp, col, _ = pf.synth_csr(cfg, seed=21, scale_n=scale, dtypes=())
+        out.append((f"C{cfg}", rp, col, len(rp) - 1))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_flat_row_aligned_and_split_tiles(tile, dtype):
+    """Short-row matrices: FLAT plans pick row-aligned tiles (one launch, no split row); forcing
+    split-row tiles gives the same y.  KAT inputs are bit-exact both ways; with U[-1,1] inputs the
+    row-aligned y of rows <= 16 nnz is bit-exact too, each row being summed whole by one lane."""
+    for name, rp, col, n in short_row_cases():
+        ys = {}
+        for ra in (None, 0):
+            kv = oracle.initvec(len(col), NP[dtype])
+            kx = oracle.initvec(n, NP[dtype])
+            y, info = gpu_spmv(rp, col, kv, kx, "flat", tile=tile, dtype=dtype, row_aligned=ra)
+            assert info["tile"] == tile
+            if ra is None:
+                assert info["row_aligned"] == 1 and info["needs_fixup"] == 0, name
+            else:
+                assert info["row_aligned"] == 0 and info["needs_fixup"] == int(info["ntiles"] > 1), name
+            if kat_exact_possible(rp, dtype):
+                assert_parity(rp, col, kv, kx, y, dtype, exact=True, what=f"{name}/kat/ra={ra}")
+            rng = np.random.default_rng(tile + len(col))
+            val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+            x = rng.uniform(-1, 1, n).astype(NP[dtype])
+            y, _ = gpu_spmv(rp, col, val, x, "flat", tile=tile, dtype=dtype, row_aligned=ra)
+            assert_parity(rp, col, val, x, y, dtype, what=f"{name}/random/ra={ra}")
+            ys[ra] = y
+        ref = oracle.spmv_serial(rp, col, val, x)
+        short = np.diff(rp) <= 16
+        assert np.array_equal(ys[None][short], ref[short]), name
+
+
+def test_row_aligned_refused_for_long_rows():
+    import torch
+    from gpu_util import dev
+    for name, rp, col, n in CASES:
+        if len(rp) < 2 or np.diff(rp).max() <= ALIGN_MAX or len(col) < 2048:
+            continue
+        d_rp, d_col = dev(rp), dev(col)
+        with pf.Plan(d_rp, d_col, len(rp) - 1, n, len(col), "f64", "flat", 1024) as p:
+            assert p.info.row_aligned == 0, name
+            with pytest.raises(pf.PrefreeError):
+                p.set_row_aligned(1)
+            p.set_row_aligned(0)
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("variant", ["adaptive", "flat"])
 def test_deterministic(variant):
     rp, col, v = pf.synth_csr(5, seed=4, scale_n=40000)

@@ -32,6 +32,30 @@ def test_model_satisfies_invariants(tile, merged):
         check_tiling(rp, desc, tile, lmax, merged)
 
 
+ALIGN_MAX = 256   # PFK_ALIGN_ROW_MAX: longest row of a row-aligned FLAT plan
+
+
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_row_aligned_model_satisfies_invariants(tile):
+    """Row-aligned FLAT tiles: every nnz and row exactly once, no split, and
+    the span the kernel's product buffer holds (K + 255 nnz past kb)."""
+    n = 0
+    for name, rp in all_cases():
+        if len(rp) < 2 or np.diff(rp).max() > ALIGN_MAX:
+            continue
+        n += 1
+        desc = tile_model(rp, tile, False, 0, aligned=True)
+        check_tiling(rp, desc, tile, ALIGN_MAX, False)
+        kb = np.arange(len(desc)) * tile
+        assert np.all(desc[:, 2] >= kb), name
+        assert np.all(desc[:, 3] - kb < tile + ALIGN_MAX), name
+        # same row map (first row of each tile) as the split tiling
+        split = tile_model(rp, tile, False, 0)
+        rows_split = np.where(split[:, 4] == 1, split[:, 0] + 1, split[:, 0])
+        assert np.array_equal(desc[:, 0], rows_split), name
+    assert n >= 10
+
+
 def test_adaptive_tiles_are_balanced():
     for name, rp in all_cases():
         desc = tile_model(rp, 188, True, 64)
