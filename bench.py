@@ -39,7 +39,14 @@ WORKLOADS = {
 }
 
 
-KERNELS = {"adaptive": "k_wave", "flat": "k_tiles", "prefree": "k_prefree"}
+def kernel_name(info):
+    """The dominant kernel of a plan's step (prefree-public_amd/csrc/prefree_kernels.hip)."""
+    v = info["variant_name"]
+    if v == "adaptive":
+        return "k_wave"
+    if v == "prefree":
+        return "k_prefree"
+    return {256: "k_flow", 4096: "k_tiles"}.get(info["tile"], "k_rows" if info["row_aligned"] else "k_flat")
 
 
 def load_pkg():
@@ -98,6 +105,10 @@ def main():
     ap.add_argument("--cold-steps", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--launch", default="auto", choices=["auto", "graph", "eager"],
+                    help="timed steps as one captured HIP graph or launched one by one from Python; auto: graph "
+                         "when an eager warm-up step takes under 20 us (launch-bound), eager otherwise (a graph "
+                         "adds about 0.5 us per kernel on MI355X)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the measurement, run a plain copy kernel over 256 MiB 3 times (known bytes, "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -142,10 +153,34 @@ def main():
     def step():
         plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=stream)
 
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
     for _ in range(args.warmup):
         step()
+    w1.record(stream)
     torch.cuda.synchronize()
+    warm_us = w0.elapsed_time(w1) * 1e3 / max(1, args.warmup)
     plan.check(stream=stream)
+    y_eager = d_y.clone()
+    use_graph = args.launch == "graph" or (args.launch == "auto" and warm_us < 20.0)
+
+    # The timed steps as one HIP graph of exactly --steps SpMV launches (the
+    # plan's kernels only: no memset, no host synchronisation), so that the
+    # launch-bound small configurations measure the GPU rather than the rate
+    # at which Python can launch (--launch chooses; see its help).
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cs = torch.cuda.current_stream()
+            for _ in range(args.steps):
+                plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=cs)
+        torch.cuda.synchronize()
+        d_y.fill_(float("nan"))
+        graph.replay()                       # untimed replay, checked against the eager y below
+        torch.cuda.synchronize()
+        graph_same = bool(torch.equal(d_y, y_eager)) if info["variant_name"] != "prefree" else None
 
     # Timed region: exactly --steps steps, device-synchronised on both sides.
     e0 = torch.cuda.Event(enable_timing=True)
@@ -153,8 +188,11 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     e0.record(stream)
-    for _ in range(args.steps):
-        step()
+    if graph is not None:
+        graph.replay()
+    else:
+        for _ in range(args.steps):
+            step()
     e1.record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -204,7 +242,8 @@ def main():
     bytes_gather = (2 * nnz + m) * vb + nnz * 4 + (m + 1) * 4       # test/test_cdspmv.cpp:306
     gbs = bytes_eff / (ms_kernel * 1e-3) / 1e9
     key = f"C{args.config}-{dt}-{info['variant_name']}-{info['tile']}" + (
-        f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "")
+        f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
+        "-rows" if info["row_aligned"] else "")
 
     result = {
         "metric": METRIC,
@@ -223,6 +262,7 @@ def main():
                    "cfg": f"C{args.config}", "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
                    "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
                    "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
+                   "row_aligned": bool(info["row_aligned"]),
                    "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3)},
         "gbps_effective": round(gbs, 1),
         "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
@@ -230,12 +270,16 @@ def main():
                         "source": "test/test_cdspmv.cpp:305-306"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profiles(key),
-                     "kernel": KERNELS[info["variant_name"]],
+                     "kernel": kernel_name(info),
                      "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
                      "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
         "cold": ({"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
                   "flush": "1 GiB write before each step"} if args.cold_steps > 0 else None),
+        "launch": ("one captured HIP graph of the timed steps (y checked bit for bit against an eager step: "
+                   f"{'equal' if graph_same else ('n/a' if graph_same is None else 'DIFFERENT')})"
+                   if graph is not None else "eager launches from Python")
+                  + f"; eager warm-up step {warm_us:.1f} us",
         "host_buffers": {"ms": round(pcie_ms, 3), "gflops": round(2.0 * nnz / (pcie_ms * 1e6), 3),
                          "what": "one SpMV from pageable host arrays: copies in, plan, execute, copy of y out"},
         "device": pf.device_name(),

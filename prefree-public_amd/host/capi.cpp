@@ -169,20 +169,27 @@ bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
 }
 
 // PF_AUTO: a tuning-table row if one matches; else
+//   * no row longer than PFK_ALIGN_ROW_MAX: FLAT (1024 nnz per tile for fp64,
+//     2048 for fp32) with row-aligned tiles, one launch per call;
 //   * a matrix too small to give half the resident waves a 512-key tile:
 //     ADAPTIVE with the smallest tile (one wave per tile, launch-bound anyway);
 //   * long rows carrying most of the nnz (mean >= 16 and rows beyond ADAPTIVE's
 //     long-row threshold, e.g. a few dense rows): ADAPTIVE 512, whose runs
 //     keep a long row's pieces on one wave;
-//   * otherwise FLAT (1024 nnz per tile for fp64, 2048 for fp32), whose rows
-//     are found once and remembered by the plan.
-// (Measured on MI355X: C2 FLAT 61.6 us vs ADAPTIVE 75.0; C4 FLAT 366 vs 400;
-// C3 FLAT 222 vs 230; C5 ADAPTIVE 1489 vs FLAT 1582.)
+//   * otherwise FLAT with split rows.
+// (Measured on MI355X: C2 row-aligned FLAT 58.4 us vs ADAPTIVE 75.0; C4 346 vs
+// 400; C1 3.3 vs ADAPTIVE-188 4.5; C3 split FLAT 222 vs ADAPTIVE 230; C5
+// ADAPTIVE 1489 vs FLAT 1582.)
 Choice auto_choice(const pf_row_stats &s, int dtype)
 {
     Choice c;
     if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
+    if (s.max_row_len <= PFK_ALIGN_ROW_MAX) {
+        c.variant = PF_FLAT;
+        c.tile = default_tile(PF_FLAT, dtype);
+        return c;
+    }
     const int big = default_tile(PF_ADAPTIVE, dtype);
     if (dtype == PF_F64 && (nnz + m) / big < nominal_resident_waves(dtype, big) / 2) {
         c.variant = PF_ADAPTIVE;

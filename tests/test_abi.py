@@ -93,10 +93,12 @@ def test_select_auto_banded_is_flat():
     assert wide.variant == pf.FLAT and wide.tile == 1024
 
 
-def test_select_auto_small_matrix_takes_small_tile():
-    """C1 shape: too few 512-key tiles for the device -> ADAPTIVE, 188-key tiles, one per run."""
-    s = make_stats(4096, 65536, 16)
-    i = pf.select(s, "f64", "auto")
+def test_select_auto_small_matrix():
+    """C1 shape (rows of 16): row-aligned FLAT.  With a row beyond 256 nnz, too few 512-key tiles
+    for the device -> ADAPTIVE, 188-key tiles, one per run."""
+    i = pf.select(make_stats(4096, 65536, 16), "f64", "auto")
+    assert i.variant == pf.FLAT and i.tile == 1024 and i.row_aligned == 1 and i.needs_fixup == 0
+    i = pf.select(make_stats(4096, 65536, 300), "f64", "auto")
     assert i.variant == pf.ADAPTIVE and i.tile == 188 and i.run_tiles == 1
     assert i.long_row_min == 64
 
