@@ -75,6 +75,9 @@ def cpu_baseline(rp, col, val, x, seconds, nnz):
     import oracle
 
     threads = oracle.omp_max_threads()
+    f16 = val.dtype == np.float16
+    if f16:  # the fp16 values widened to fp64: the sums this library's fp16 result is rounded from
+        val, x = val.astype(np.float64), x.astype(np.float64)
     y = np.zeros(len(rp) - 1, dtype=val.dtype)
     oracle.spmv_omp(rp, col, val, x, y=y)  # warm-up (page-in)
     reps, t0 = 0, time.perf_counter()
@@ -89,7 +92,8 @@ def cpu_baseline(rp, col, val, x, seconds, nnz):
     return {"value": round(2.0 * nnz / (ms * 1e6), 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
             "ms_per_spmv": round(ms, 4),
             "sample": f"full matrix, {reps} SpMVs in {el:.1f} s (OpenMP restatement of spmv_serial, "
-                      f"test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads)"}, y
+                      f"test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads"
+                      + (", on the fp16 values widened to fp64" if f16 else "") + ")"}, y
 
 
 def main():
@@ -98,7 +102,7 @@ def main():
     ap.add_argument("--steps", type=int, default=4000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
-    ap.add_argument("--dtype", default="f64", choices=["f64", "f32"])
+    ap.add_argument("--dtype", default="f64", choices=["f64", "f32", "f16"])
     ap.add_argument("--variant", default="auto", choices=["auto", "adaptive", "flat", "prefree"])
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1)
@@ -127,8 +131,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     dt = args.dtype
-    vb = 8 if dt == "f64" else 4
-    tdt = torch.float64 if dt == "f64" else torch.float32
+    vb = {"f64": 8, "f32": 4, "f16": 2}[dt]
+    tdt = {"f64": torch.float64, "f32": torch.float32, "f16": torch.float16}[dt]
 
     rp, col, vals = pf.synth_csr(args.config, seed=args.seed, dtypes=(dt,))
     val = vals[dt]
@@ -258,7 +262,7 @@ def main():
         "vs_baseline": None,
         "dtype": dt,
         "data": "synthetic (seeded generator prefree-public_amd/host/synth.cpp, U[-1,1] values)",
-        "config": {"workload": WORKLOADS[args.config] + ("" if dt == "f64" else " (fp32)"),
+        "config": {"workload": WORKLOADS[args.config] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
                    "cfg": f"C{args.config}", "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
                    "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
                    "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
@@ -287,10 +291,18 @@ def main():
     if not args.no_cpu:
         cpu, y_cpu = cpu_baseline(rp, col, val, x, args.cpu_seconds, nnz)
         import oracle
-        err, zero_bad, _ = oracle.rownorm_maxerr(rp, col, val, x, y_cpu, y_gpu)
+        if dt == "f16":  # against the fp64 sums of the same fp16 data: one binary16 rounding per row,
+            # 2^-11 relative or, for a subnormal result, 2^-25 absolute (allowed for as 2^-24)
+            den = oracle.spmv_serial(rp, col, np.abs(val.astype(np.float64)), np.abs(x.astype(np.float64)))
+            dev_ = np.abs(y_gpu.astype(np.float64) - y_cpu)
+            zero_bad = int(np.count_nonzero((den == 0) & (y_gpu != 0)))
+            nz = den > 0
+            err = float((np.maximum(dev_[nz] - 2.0 ** -24, 0) / den[nz]).max()) if nz.any() else 0.0
+        else:
+            err, zero_bad, _ = oracle.rownorm_maxerr(rp, col, val, x, y_cpu, y_gpu)
         result["cpu_baseline"] = cpu
         result["parity"] = {"max_rownorm_err_vs_cpu": err, "zero_rows_bad": zero_bad,
-                            "tol": 1e-12 if dt == "f64" else 1e-5}
+                            "tol": {"f64": 1e-12, "f32": 1e-5, "f16": 1e-3}[dt]}
         result["speedup_vs_cpu"] = round(cpu["ms_per_spmv"] / ms_step, 1)
     else:
         result["cpu_baseline"] = None

@@ -20,14 +20,25 @@
  * PREFREE_TILE=<keys per tile>, PREFREE_WARMUP=<n> (200), PREFREE_ITERS=<n> (4000).
  *
  * valT is double (the reference's default -Dfp64 build).  Defining
- * PREFREE_VALT_FLOAT before including this header selects the float overload.
+ * PREFREE_VALT_FLOAT before including this header selects the float overload,
+ * PREFREE_VALT_HALF the fp16 one: the reference's non-fp64 build stores half
+ * values (include/common.h:43-46); pf_half holds the same 16 IEEE binary16
+ * bits, so a half* converts with a reinterpret_cast.  The fp16 overload forms
+ * products and row sums in fp32 and rounds each row sum to half once.
  */
 #ifndef PREFREE_DROPIN_H
 #define PREFREE_DROPIN_H
 
+/* IEEE binary16 value, bit for bit. */
+typedef struct pf_half {
+    unsigned short bits;
+} pf_half;
+
 #ifndef valT
-#ifdef PREFREE_VALT_FLOAT
+#if defined(PREFREE_VALT_FLOAT)
 #define valT float
+#elif defined(PREFREE_VALT_HALF)
+#define valT pf_half
 #else
 #define valT double
 #endif
@@ -37,5 +48,7 @@ void preFreeSpMV(double *csrVal, int *csrRowPtr, int *csrColInd, double *X_val, 
                  int nnzA, double *cdTime, double *cdPre);
 void preFreeSpMV(float *csrVal, int *csrRowPtr, int *csrColInd, float *X_val, float *Y_val, int rowA, int colA,
                  int nnzA, double *cdTime, double *cdPre);
+void preFreeSpMV(pf_half *csrVal, int *csrRowPtr, int *csrColInd, pf_half *X_val, pf_half *Y_val, int rowA,
+                 int colA, int nnzA, double *cdTime, double *cdPre);
 
 #endif

@@ -39,7 +39,9 @@ enum pf_status {
 };
 
 /* ---- value types ----------------------------------------------------------- */
-enum pf_dtype { PF_F64 = 0, PF_F32 = 1 };
+/* PF_F16: val, x and y hold IEEE binary16 values (2 bytes each); products and row sums are formed in
+ * fp32 and each row sum is rounded to half once.  FLAT tiles (1024, 2048) only. */
+enum pf_dtype { PF_F64 = 0, PF_F32 = 1, PF_F16 = 2 };
 
 /* ---- kernel variants (all compute y = A·x, y overwritten) ------------------
  * PF_AUTO      pick from row-length statistics (pf_select)

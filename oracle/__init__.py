@@ -161,10 +161,48 @@ def bytes_gather(rows, cols, nnz, val_bytes):
 
 
 def initvec(n, dtype=np.float64):
-    """initVec, include/common.h:126-133."""
+    """initVec, include/common.h:126-133 (fp16: the reference's valT = half cast of (float)(i % 15))."""
+    if np.dtype(dtype) == np.float16:
+        return initvec(n, np.float32).astype(np.float16)
     v = np.empty(n, dtype=dtype)
     if dtype == np.float64:
         lib().oracle_initvec_f64(_ptr(v, ctypes.c_double), n)
     else:
         lib().oracle_initvec_f32(_ptr(v, ctypes.c_float), n)
     return v
+
+
+# ---- fp16 (the reference's non-fp64 build: valT = half, include/common.h:43-46) ----------
+#
+# numpy's binary16 arithmetic converts both operands to float, operates, and
+# rounds the result to the nearest binary16 (ties to even): for a product or a
+# sum of two binary16 values this is the correctly rounded binary16 result.
+
+
+def spmv_serial_f16(row_ptr, col, val, x):
+    """spmv_serial, test/test_cdspmv.cpp:4-20, in the reference's fp16 build: the accumulator t and
+    every product are binary16, each product and each addition rounded to binary16, in nnz order.
+    Vectorised over rows (position k of every row at step k); returns float16[m]."""
+    _check_csr(row_ptr, col)
+    val = np.asarray(val, dtype=np.float16)
+    x = np.asarray(x, dtype=np.float16)
+    m = len(row_ptr) - 1
+    lens = np.diff(row_ptr).astype(np.int64)
+    t = np.zeros(m, dtype=np.float16)
+    for k in range(int(lens.max()) if m else 0):
+        with np.errstate(over="ignore"):
+            rows = np.flatnonzero(lens > k)
+            j = row_ptr[rows].astype(np.int64) + k
+            prod = val[j] * x[col[j]]          # binary16 product
+            t[rows] = t[rows] + prod           # binary16 sum
+    return t
+
+
+def spmv_f16_rounded(row_ptr, col, val, x):
+    """This library's fp16 result model: exact products of the binary16 inputs, summed in fp64 in nnz
+    order (spmv_serial, test/test_cdspmv.cpp:4-20, on the values widened to double), each row
+    sum rounded once to binary16.  Returns float16[m]."""
+    v64 = np.asarray(val, dtype=np.float16).astype(np.float64)
+    x64 = np.asarray(x, dtype=np.float16).astype(np.float64)
+    with np.errstate(over="ignore"):       # sums beyond 65504 round to +-inf, as intended
+        return spmv_serial(row_ptr, col, v64, x64).astype(np.float16)

@@ -26,11 +26,11 @@ LIB_DIR = os.path.join(_HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libprefree.so")
 KLIB_PATH = os.path.join(LIB_DIR, "libprefree_kernels.so")
 
-F64, F32 = 0, 1
+F64, F32, F16 = 0, 1, 2
 AUTO, PREFREE, ADAPTIVE, FLAT = 0, 1, 2, 3
 VARIANTS = {"auto": AUTO, "prefree": PREFREE, "adaptive": ADAPTIVE, "flat": FLAT}
 VARIANT_NAMES = {v: k for k, v in VARIANTS.items()}
-DTYPES = {"f64": F64, "f32": F32}
+DTYPES = {"f64": F64, "f32": F32, "f16": F16}
 STATUS = {0: "PF_OK", 1: "PF_ERR_INVALID", 2: "PF_ERR_ALIGN", 3: "PF_ERR_HIP", 4: "PF_ERR_NOMEM",
           5: "PF_ERR_UNSUPPORTED", 6: "PF_ERR_CSR", 7: "PF_ERR_KERNEL"}
 
@@ -206,6 +206,8 @@ def dtype_code(d) -> int:
         return F64
     if "float32" in name or name == "float":
         return F32
+    if "float16" in name or name == "half":
+        return F16
     raise ValueError(f"unsupported dtype {d}")
 
 
@@ -387,7 +389,8 @@ def synth_csr(cfg, seed=1, scale_n=0, vals=0, dtypes=("f64",), out=None):
     """(row_ptr, col, {dtype: val}) of configuration `cfg` as numpy arrays.
 
     `out` may supply preallocated arrays (dict with keys row_ptr, col, f64, f32),
-    e.g. pinned host memory."""
+    e.g. pinned host memory.  "f16" values are the f64 draws rounded to the
+    nearest IEEE binary16 (ties to even)."""
     m, n, nnz = synth_dims(cfg, seed, scale_n)
     out = dict(out or {})
     rp = out.get("row_ptr")
@@ -395,20 +398,30 @@ def synth_csr(cfg, seed=1, scale_n=0, vals=0, dtypes=("f64",), out=None):
     col = out.get("col")
     col = np.empty(nnz, dtype=np.int32) if col is None else col
     vals_out = {}
-    for d in dtypes:
+    gen = [d for d in dtypes if d != "f16"] + (["f64"] if "f16" in dtypes and "f64" not in dtypes else [])
+    for d in gen:
         a = out.get(d)
         vals_out[d] = np.empty(nnz, dtype=np.float64 if d == "f64" else np.float32) if a is None else a
     _check(lib().pf_synth_csr(int(cfg), int(seed), int(scale_n), int(vals), rp.ctypes.data, col.ctypes.data,
                               vals_out["f64"].ctypes.data if "f64" in vals_out else None,
                               vals_out["f32"].ctypes.data if "f32" in vals_out else None), "pf_synth_csr")
+    if "f16" in dtypes:
+        vals_out["f16"] = vals_out["f64"].astype(np.float16)
+        if "f64" not in dtypes:
+            del vals_out["f64"]
     return rp, col, vals_out
 
 
 def synth_x(cfg, n, seed=1, vals=0, dtypes=("f64",)):
-    xs = {d: np.empty(n, dtype=np.float64 if d == "f64" else np.float32) for d in dtypes}
+    gen = [d for d in dtypes if d != "f16"] + (["f64"] if "f16" in dtypes and "f64" not in dtypes else [])
+    xs = {d: np.empty(n, dtype=np.float64 if d == "f64" else np.float32) for d in gen}
     _check(lib().pf_synth_x(int(cfg), int(seed), int(n), int(vals),
                             xs["f64"].ctypes.data if "f64" in xs else None,
                             xs["f32"].ctypes.data if "f32" in xs else None), "pf_synth_x")
+    if "f16" in dtypes:
+        xs["f16"] = xs["f64"].astype(np.float16)
+        if "f64" not in dtypes:
+            del xs["f64"]
     return xs
 
 

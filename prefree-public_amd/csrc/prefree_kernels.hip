@@ -60,6 +60,14 @@ __device__ __forceinline__ void lds_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// fp16 mode: values, x and y stored as IEEE binary16; products and row sums
+// are formed in fp32 (a product of two halves is exact in fp32) and each row
+// sum is rounded to half once, when y is stored.
+typedef _Float16 half_t;
+template <typename T> struct AccOf { using type = T; };
+template <> struct AccOf<half_t> { using type = float; };
+template <typename T> using acc_t = typename AccOf<T>::type;
+
 template <typename T>
 struct Args {
     const int *__restrict__ rp;
@@ -75,8 +83,8 @@ struct Args {
     long long g8;        // k_tiles: tiles per XCD (ceil(ntiles / 8))
     long long tx;        // k_stream: tiles per XCD
     long long tpw;       // k_stream: tiles per workgroup
-    T *__restrict__ head;
-    T *__restrict__ tail;
+    acc_t<T> *__restrict__ head;  // split-row partial sums (fp32 in the fp16 mode)
+    acc_t<T> *__restrict__ tail;
     int *__restrict__ owner;
     int *__restrict__ err;
 };
@@ -128,6 +136,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, lo
     return __builtin_amdgcn_make_buffer_rsrc(u, 0, nb, kRsrcWord3);
 }
 
+// Bytes of a val resource over `count` values starting at an even index.  The
+// range check of a multi-dword load drops every dword that ends past the
+// resource, so an fp16 range is rounded up to whole dwords: with val 16-byte
+// aligned the extra two bytes share the last value's dword (never another
+// page), and the lane slot they fill is never gathered or summed.
+template <typename T>
+__device__ __forceinline__ long long val_range_bytes(int count)
+{
+    return (((long long)count * (long long)sizeof(T)) + 3) & ~3ll;
+}
+
 // col and val of the 4 consecutive nnz at 16-byte vector `vec` of a resource pair.
 template <int AUX = kAuxNt>
 __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
@@ -152,6 +171,20 @@ __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer
     c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
     v[0] = __int_as_float((int)vv.x); v[1] = __int_as_float((int)vv.y);
     v[2] = __int_as_float((int)vv.z); v[3] = __int_as_float((int)vv.w);
+}
+
+template <int AUX = kAuxNt>
+__device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
+                                      half_t (&v)[4])
+{
+    typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(rc, vec * 16, 0, AUX);
+    const u32x2v vv = __builtin_amdgcn_raw_buffer_load_b64(rv, vec * 8, 0, AUX);
+    c[0] = (int)cc.x; c[1] = (int)cc.y; c[2] = (int)cc.z; c[3] = (int)cc.w;
+    v[0] = __builtin_bit_cast(half_t, (unsigned short)(vv.x & 0xFFFFu));
+    v[1] = __builtin_bit_cast(half_t, (unsigned short)(vv.x >> 16));
+    v[2] = __builtin_bit_cast(half_t, (unsigned short)(vv.y & 0xFFFFu));
+    v[3] = __builtin_bit_cast(half_t, (unsigned short)(vv.y >> 16));
 }
 
 __device__ __forceinline__ void store4(double *s, const double (&p)[4])
@@ -519,6 +552,11 @@ __device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t of
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ half_t buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, half_t *)
+{
+    return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0));
 }
 
 
@@ -972,10 +1010,11 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     using S = FlatShape<T, K>;
     constexpr int VPT = S::kVPT;
     constexpr bool DESC = MODE == kFlatDesc;
-    __shared__ __attribute__((aligned(16))) T s_prod[DESC ? 4 : K];
+    using P = acc_t<T>;
+    __shared__ __attribute__((aligned(16))) P s_prod[DESC ? 4 : K];
     __shared__ int s_rp[DESC ? 4 : S::kRpCap];
     __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l]
-    __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
+    __shared__ ReduceLds<P, S::kWaveCap, S::kBlockCap> L;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -993,7 +1032,7 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     T v[VPT][4];
     if (!DESC) {
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B - kb) * 4);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, (long long)(B - kb) * (long long)sizeof(T));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B - kb));
 #pragma unroll
         for (int k = 0; k < VPT; ++k)
             load4(rc, rv, tid + k * kBS, c[k], v[k]);
@@ -1055,11 +1094,11 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
         for (int k = 0; k < VPT; ++k) {
             const int vec = tid + k * kBS;
             const bool in = 4 * vec < B - kb;
-            T p[4];
+            P p[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const T xv = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
-                p[j] = v[k][j] * xv;  // slots past the tile are never read
+                p[j] = P(v[k][j]) * P(xv);  // slots past the tile are never read
             }
             store4(s_prod + 4 * vec, p);
         }
@@ -1073,10 +1112,10 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
             ra = i < S::kRpCap ? s_rp[i] : rp[lo_row + i];
             rb = i + 1 < S::kRpCap ? s_rp[i + 1] : rp[lo_row + i + 1];
         },
-        [&](int i, T s) {
+        [&](int i, P s) {
             if (head && i == 0) a.head[t] = s;
             else if (tail && i == nr - 1) a.tail[t] = s;
-            else a.y[lo_row + i] = s;
+            else a.y[lo_row + i] = T(s);
         });
     if (tid == 0) a.owner[t] = tail ? lo_row + nr - 1 : -1;
 }
@@ -1163,19 +1202,20 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
 template <typename T, int K>
 __device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsShape<T, K>::kVPT][4],
                                            const T (&xv)[RowsShape<T, K>::kVPT][4], T ov, T xo,
-                                           const int (&rr)[RowsShape<T, K>::kRpPer], T *s_prod, int *s_rp)
+                                           const int (&rr)[RowsShape<T, K>::kRpPer], acc_t<T> *s_prod, int *s_rp)
 {
     using S = RowsShape<T, K>;
+    using P = acc_t<T>;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int k = 0; k < S::kVPT; ++k) {
-        T p[4];
+        P p[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            p[j] = v[k][j] * xv[k][j];
+            p[j] = P(v[k][j]) * P(xv[k][j]);
         store4(s_prod + 4 * (tid + k * kBS), p);
     }
-    if (tid < d.nov) s_prod[K + tid] = ov * xo;
+    if (tid < d.nov) s_prod[K + tid] = P(ov) * P(xo);
 #pragma unroll
     for (int q = 0; q < S::kRpPer; ++q)
         if (tid + q * kBS < d.cnt) s_rp[tid + q * kBS] = rr[q];
@@ -1186,30 +1226,39 @@ __device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsS
 // row_ptr in a separate branch, so the common path waits on LDS only and
 // leaves the y stores and any loads already issued for the next tile in flight.
 template <typename T, int K>
-__device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, const T *s_prod, const int *s_rp,
-                                            ReduceLds<T, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
+__device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, const acc_t<T> *s_prod,
+                                            const int *s_rp,
+                                            ReduceLds<acc_t<T>, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
 {
     using S = RowsShape<T, K>;
+    using P = acc_t<T>;
     if (d.nr < S::kRpCap) {
-        // Row sums staged in LDS, then y[f0 .. f0 + nr) written as 16-byte
-        // non-temporal stores through a resource over exactly those rows (the
-        // range check drops the bytes past the last row).  y is not read again
-        // here; keeping it out of L2 leaves room for x (C4: 345 instead of 377 us
-        // per call with 8-byte stores through L2).
-        __shared__ __attribute__((aligned(16))) T s_y[S::kRpCap + 4];
-        reduce_tile(
-            s_prod, L, d.kb, d.A, d.B, d.nr,
-            [&](int i, int &ra, int &rb) {
-                ra = s_rp[i];
-                rb = s_rp[i + 1];
-            },
-            [&](int i, T s) { s_y[i] = s; });
+        // fp64 / fp32: row sums staged in LDS, then y[f0 .. f0 + nr) written as
+        // 16-byte non-temporal stores through a resource over exactly those rows
+        // (the range check drops the whole dwords past the last row).  y is not
+        // read again here; keeping it out of L2 leaves room for x (C4: 345
+        // instead of 377 us per call with 8-byte stores through L2).
         const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f0, (long long)d.nr * (long long)sizeof(T));
-        constexpr int kPer = 16 / (int)sizeof(T);
-        const int n16 = (d.nr + kPer - 1) / kPer;
-        for (int j = (int)threadIdx.x; j < n16; j += kBS)
-            __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16, 0,
-                                                   kAuxNt);
+        const auto bounds = [&](int i, int &ra, int &rb) {
+            ra = s_rp[i];
+            rb = s_rp[i + 1];
+        };
+        if constexpr (sizeof(T) >= 4) {
+            __shared__ __attribute__((aligned(16))) T s_y[S::kRpCap + 4];
+            reduce_tile(s_prod, L, d.kb, d.A, d.B, d.nr, bounds, [&](int i, P s) { s_y[i] = T(s); });
+            constexpr int kPer = 16 / (int)sizeof(T);
+            const int n16 = (d.nr + kPer - 1) / kPer;
+            for (int j = (int)threadIdx.x; j < n16; j += kBS)
+                __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16,
+                                                       0, kAuxNt);
+        } else {
+            // fp16: one 2-byte store per row.  The range check works on whole
+            // dwords, so a 16-byte store ending in a half-covered dword would
+            // drop the tile's last row.
+            reduce_tile(s_prod, L, d.kb, d.A, d.B, d.nr, bounds, [&](int i, P s) {
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, T(s)), ry, i * 2, 0, kAuxNt);
+            });
+        }
     } else {  // more rows than LDS holds: any number, up to m
         const int *__restrict__ rp = a.rp + d.f0;
         T *__restrict__ y = a.y + d.f0;
@@ -1219,7 +1268,7 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
                 ra = i < S::kRpCap ? s_rp[i] : rp[i];
                 rb = i + 1 < S::kRpCap ? s_rp[i + 1] : rp[i + 1];
             },
-            [&](int i, T s) { y[i] = s; });
+            [&](int i, P s) { y[i] = T(s); });
     }
 }
 
@@ -1229,10 +1278,10 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     using S = RowsShape<T, K>;
     constexpr int VPT = S::kVPT;
     constexpr bool DESC = MODE == kFlatDesc;
-    __shared__ __attribute__((aligned(16))) T s_prod[DESC ? 4 : S::kProd];
+    __shared__ __attribute__((aligned(16))) acc_t<T> s_prod[DESC ? 4 : S::kProd];
     __shared__ int s_rp[DESC ? 4 : S::kRpCap];
     __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l] (search modes)
-    __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
+    __shared__ ReduceLds<acc_t<T>, S::kWaveCap, S::kBlockCap> L;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -1256,7 +1305,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     T v[VPT][4];
     if (!DESC) {
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B0 - kb) * 4);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, (long long)(B0 - kb) * (long long)sizeof(T));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B0 - kb));
 #pragma unroll
         for (int k = 0; k < VPT; ++k)
             load4(rc, rv, tid + k * kBS, c[k], v[k]);
@@ -1594,10 +1643,10 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
         long long tb = last_key / K;  // last tile holding a piece of row r
         if (tb >= a.ntiles) { atomicOr(a.err, 1); tb = a.ntiles - 1; }
         if (tb - t <= kFixSerial) {
-            T s = T(0);
+            acc_t<T> s = 0;
             for (long long u = t + 1; u <= tb; ++u)
                 s += a.head[u];
-            a.y[r] = a.tail[t] + s;
+            a.y[r] = T(a.tail[t] + s);
         } else {
             s_list[atomicAdd(&s_n, 1)] = tid;
         }
@@ -1609,12 +1658,12 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
         const int rl = a.owner[tl];  // validated above (listed only when 0 <= rl < m)
         long long tb = ((long long)a.rp[rl + 1] - 1 + (MERGE ? rl : 0)) / K;
         if (tb >= a.ntiles) tb = a.ntiles - 1;
-        T s = T(0);
+        acc_t<T> s = 0;
         for (long long u = tl + 1 + lane; u <= tb; u += kWave)
             s += a.head[u];
         s = wave_sum(s);
         if (lane == 0)
-            a.y[rl] = a.tail[tl] + s;
+            a.y[rl] = T(a.tail[tl] + s);
     }
 }
 
@@ -1900,11 +1949,17 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.g8 = (a->ntiles + kXcds - 1) / kXcds;
     r.tx = r.g8;
     r.tpw = 1;
-    r.head = static_cast<T *>(a->head_slot);
-    r.tail = static_cast<T *>(a->tail_slot);
+    r.head = static_cast<acc_t<T> *>(a->head_slot);
+    r.tail = static_cast<acc_t<T> *>(a->tail_slot);
     r.owner = a->owner_row;
     r.err = a->err_flag;
     return r;
+}
+
+int unsupported_f16(const char *variant)
+{
+    snprintf(g_err, sizeof g_err, "%s has no fp16 kernel (fp16 runs on FLAT tiles of 1024 or 2048 nnz)", variant);
+    return PF_ERR_UNSUPPORTED;
 }
 
 bool args_ok(const pfk_spmv_args *a, bool need_ws)
@@ -2052,11 +2107,18 @@ int dispatch_flat(const pfk_spmv_args *a, void *stream)
         snprintf(g_err, sizeof g_err, "row-aligned FLAT tiles are 1024 or 2048 nnz, not %d", a->tile);
         return PF_ERR_INVALID;
     }
-    if (a->tile == kFlowT) return launch_flow<T>(a, stream);
-    switch (a->tile) {
-    case 1024: return launch_flat<T, 1024>(a, nullptr, stream);
-    case 2048: return launch_flat<T, 2048>(a, nullptr, stream);
-    case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
+    if constexpr (__is_same(T, half_t)) {  // fp16: the 1024 / 2048 kernels only
+        switch (a->tile) {
+        case 1024: return launch_flat<T, 1024>(a, nullptr, stream);
+        case 2048: return launch_flat<T, 2048>(a, nullptr, stream);
+        }
+    } else {
+        if (a->tile == kFlowT) return launch_flow<T>(a, stream);
+        switch (a->tile) {
+        case 1024: return launch_flat<T, 1024>(a, nullptr, stream);
+        case 2048: return launch_flat<T, 2048>(a, nullptr, stream);
+        case 4096: return launch_tiles<T, false, 4096, 0>(a, stream);
+        }
     }
     snprintf(g_err, sizeof g_err, "tile %d not compiled for this value type", a->tile);
     return PF_ERR_UNSUPPORTED;
@@ -2078,6 +2140,7 @@ extern "C" {
 
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream)
 {
+    if (dtype == PF_F16) return unsupported_f16("ADAPTIVE");
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_adaptive<double>(a, stream)
@@ -2089,7 +2152,8 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
-         : dtype == PF_F32 ? dispatch_flat<float>(a, stream) : PF_ERR_INVALID;
+         : dtype == PF_F32 ? dispatch_flat<float>(a, stream)
+         : dtype == PF_F16 ? dispatch_flat<half_t>(a, stream) : PF_ERR_INVALID;
 }
 
 int pfk_flow_resident_waves(int dtype, long long *waves)
@@ -2145,6 +2209,9 @@ int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *str
         Args<float> r = make_args<float>(a);
         if (merged_keys) hipLaunchKernelGGL((k_fixup<float, true>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
         else hipLaunchKernelGGL((k_fixup<float, false>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
+    } else if (dtype == PF_F16 && !merged_keys) {
+        Args<half_t> r = make_args<half_t>(a);
+        hipLaunchKernelGGL((k_fixup<half_t, false>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
     } else {
         return PF_ERR_INVALID;
     }
@@ -2154,6 +2221,8 @@ int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *str
 
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream)
 {
+    if (dtype == PF_F16) return unsupported_f16("PREFREE");
+    if (dtype != PF_F64 && dtype != PF_F32) return PF_ERR_INVALID;  // before y is sized from it
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, false)) return PF_ERR_INVALID;
     const size_t ybytes = (size_t)a->m * (dtype == PF_F64 ? 8 : 4);
@@ -2183,14 +2252,16 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
     static const int ad32[] = {440, 494, 1024};
     static const int fl64[] = {256, 1024, 2048, 4096}; // nnz per tile: k_flow, k_flat, k_flat, k_tiles
     static const int fl32[] = {256, 1024, 2048, 4096};
+    static const int fl16[] = {1024, 2048};            // fp16: k_flat / k_rows only
     static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
-    if (variant == PF_PREFREE) { src = pf_tiles; n = 2; }
+    if (variant == PF_PREFREE && dtype != PF_F16) { src = pf_tiles; n = 2; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 4; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 3; }
     else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 4; }
     else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 4; }
+    else if (variant == PF_FLAT && dtype == PF_F16) { src = fl16; n = 2; }
     else return 0;
     for (int i = 0; i < n && i < cap; ++i) tiles[i] = src[i];
     return n;

@@ -45,7 +45,9 @@ constexpr int kFlowTile = 256;
 // FLAT tiles of 1024 and 2048 nnz (k_flat) remember the rows their search found.
 bool uses_row_map(int variant, int tile) { return variant == PF_FLAT && (tile == 1024 || tile == 2048); }
 
-int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : 0; }
+int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : dtype == PF_F16 ? 2 : 0; }
+// Bytes of one split-row partial sum (head / tail slot): fp32 in the fp16 mode.
+int slot_bytes(int dtype) { return dtype == PF_F16 ? 4 : value_bytes(dtype); }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -53,7 +55,7 @@ int default_tile(int variant, int dtype)
 {
     if (variant == PF_PREFREE) return 512;  // 128 threads x P_NNZ 4, preFreeSpMV.cu:583-587
     if (variant == PF_ADAPTIVE) return dtype == PF_F64 ? 512 : 440;
-    return dtype == PF_F64 ? 1024 : 2048;  // FLAT: the measured best per value type on C2-C5
+    return dtype == PF_F64 ? 1024 : 2048;  // FLAT: the measured best per value type on C2-C5 (fp16 as fp32)
 }
 
 // Wave64s of the ADAPTIVE kernel resident at once on an MI355X (256 CUs x 4
@@ -100,7 +102,10 @@ std::mutex g_table_mu;
 std::vector<TableRow> g_table;
 bool g_table_env_done = false;
 
-int parse_dtype(const std::string &s) { return s == "f64" ? PF_F64 : s == "f32" ? PF_F32 : -1; }
+int parse_dtype(const std::string &s)
+{
+    return s == "f64" ? PF_F64 : s == "f32" ? PF_F32 : s == "f16" ? PF_F16 : -1;
+}
 int parse_variant(const std::string &s)
 {
     return s == "adaptive" ? PF_ADAPTIVE : s == "flat" ? PF_FLAT : s == "prefree" ? PF_PREFREE : -1;
@@ -169,7 +174,7 @@ bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
 }
 
 // PF_AUTO: a tuning-table row if one matches; else
-//   * no row longer than PFK_ALIGN_ROW_MAX: FLAT (1024 nnz per tile for fp64,
+//   * no row longer than PFK_ALIGN_ROW_MAX, or fp16 values (FLAT only): FLAT (1024 nnz per tile for fp64,
 //     2048 for fp32) with row-aligned tiles, one launch per call;
 //   * a matrix too small to give half the resident waves a 512-key tile:
 //     ADAPTIVE with the smallest tile (one wave per tile, launch-bound anyway);
@@ -185,7 +190,7 @@ Choice auto_choice(const pf_row_stats &s, int dtype)
     Choice c;
     if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
-    if (s.max_row_len <= PFK_ALIGN_ROW_MAX) {
+    if (s.max_row_len <= PFK_ALIGN_ROW_MAX || dtype == PF_F16) {  // fp16: FLAT tiles only
         c.variant = PF_FLAT;
         c.tile = default_tile(PF_FLAT, dtype);
         return c;
@@ -256,7 +261,7 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     // one interpolated probe round of 64 rows spaced 64 apart brackets the row.
     const bool regular = s.max_row_len <= 64;
     r.guess_spread = regular ? 64 : 0;
-    const long long vb = value_bytes(dtype);
+    const long long vb = slot_bytes(dtype);
     if (variant == PF_ADAPTIVE) {
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
         const long long total = nnz + m;
@@ -355,7 +360,7 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     char *w = static_cast<char *>(p->ws);
     p->err = reinterpret_cast<int *>(w);
     if (info.variant != PF_PREFREE) {
-        const size_t vb = (size_t)value_bytes(dtype);
+        const size_t vb = (size_t)slot_bytes(dtype);
         const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
         p->head = w + 256;
         p->tail = w + 256 + slots;

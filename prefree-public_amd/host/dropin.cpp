@@ -49,7 +49,7 @@ template <typename T>
 void run(T *csrVal, int *csrRowPtr, int *csrColInd, T *X_val, T *Y_val, int rowA, int colA, int nnzA,
          double *cdTime, double *cdPre)
 {
-    const int dtype = sizeof(T) == 8 ? PF_F64 : PF_F32;
+    const int dtype = sizeof(T) == 8 ? PF_F64 : sizeof(T) == 4 ? PF_F32 : PF_F16;
     if (rowA < 0 || colA < 0 || nnzA < 0) die("argument check", PF_ERR_INVALID);
     void *stream = nullptr;
     check(pfk_stream_create(&stream), "stream create");
@@ -123,4 +123,11 @@ void preFreeSpMV(float *csrVal, int *csrRowPtr, int *csrColInd, float *X_val, fl
                  int nnzA, double *cdTime, double *cdPre)
 {
     run<float>(csrVal, csrRowPtr, csrColInd, X_val, Y_val, rowA, colA, nnzA, cdTime, cdPre);
+}
+
+void preFreeSpMV(pf_half *csrVal, int *csrRowPtr, int *csrColInd, pf_half *X_val, pf_half *Y_val, int rowA, int colA,
+                 int nnzA, double *cdTime, double *cdPre)
+{
+    static_assert(sizeof(pf_half) == 2, "pf_half holds 16 bits");
+    run<pf_half>(csrVal, csrRowPtr, csrColInd, X_val, Y_val, rowA, colA, nnzA, cdTime, cdPre);
 }

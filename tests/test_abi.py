@@ -140,6 +140,21 @@ def test_select_row_aligned_threshold():
         assert pf.select(make_stats(1000000, 20000000, 5), "f64", variant).row_aligned == 0
 
 
+def test_select_f16_is_flat_only():
+    """fp16 values: FLAT (2048 nnz per tile) for every matrix, row-aligned when rows fit; the other
+    variants have no fp16 kernels."""
+    short = pf.select(make_stats(4194304, 20963328, 5), "f16", "auto")
+    assert short.variant == pf.FLAT and short.tile == 2048 and short.row_aligned == 1 and short.needs_fixup == 0
+    dense = pf.select(make_stats(1000000, 315647995, 499000), "f16", "auto")
+    assert dense.variant == pf.FLAT and dense.tile == 2048 and dense.row_aligned == 0 and dense.needs_fixup == 1
+    assert pf.supported_tiles("flat", "f16") == [1024, 2048]
+    assert pf.supported_tiles("adaptive", "f16") == [] and pf.supported_tiles("prefree", "f16") == []
+    for variant in ("adaptive", "prefree"):
+        with pytest.raises(pf.PrefreeError) as e:
+            pf.select(make_stats(1000, 5000, 5), "f16", variant)
+        assert e.value.status == 5
+
+
 def test_select_rejects_bad_arguments():
     s = make_stats(10, 10, 1)
     with pytest.raises(pf.PrefreeError):

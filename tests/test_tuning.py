@@ -50,7 +50,7 @@ def test_clearing_the_table_restores_the_rules(table):
     assert pf.select(make_stats(4194304, 20963328, 5), "f64", "auto").variant == pf.FLAT
 
 
-@pytest.mark.parametrize("text", ["x 10 f64 adaptive\n", "x 10 f16 flat 4096 0 0\n", "x 10 f64 dense 4096 0 0\n",
+@pytest.mark.parametrize("text", ["x 10 f64 adaptive\n", "x 10 f8 flat 1024 0 0\n", "x 10 f64 dense 4096 0 0\n",
                                   "x 10 f64 flat 4096 0 3\n", "x 10 f64 flat -5 0 0\n"])
 def test_malformed_tables_are_rejected(table, text):
     table.write_text(text)
