@@ -35,6 +35,8 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.dirname(HERE)
 CLASSES = ("small", "medium", "large")
+# The tile kernels of prefree-public_amd/csrc/prefree_kernels.hip (the dominant kernel of a step).
+TILE_KERNELS = ("k_wave", "k_rows", "k_flat", "k_flow", "k_tiles", "k_prefree")
 
 
 def load_pkg():
@@ -60,7 +62,7 @@ def load_matrix(spec, dtype, values, seed=1):
     """(row_ptr, col, val, x, m, n) on the host for a .mtx path or 'synthetic:C<cfg>[:scale]'."""
     import numpy as np
     pf = load_pkg()
-    np_t = np.float64 if dtype == "f64" else np.float32
+    np_t = {"f64": np.float64, "f32": np.float32, "f16": np.float16}[dtype]
     if spec.startswith("synthetic:"):
         parts = spec.split(":")
         cfg = int(parts[1].lstrip("Cc"))
@@ -208,7 +210,7 @@ def counters_for(matrix, dtype, b):
             return {"error": f"rocprofv3 {counter} exit {r.returncode}"}
         rows = list(csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))))
         main = [float(x["Counter_Value"]) for x in rows if x["Counter_Name"] == counter and
-                any(k in x["Kernel_Name"] for k in ("k_wave", "k_tiles", "k_prefree"))]
+                any(k in x["Kernel_Name"] for k in TILE_KERNELS)]
         copy = [float(x["Counter_Value"]) for x in rows if x["Counter_Name"] == counter and "neg" in x["Kernel_Name"]]
         if not main or not copy:
             return {"error": f"no {counter} rows"}
