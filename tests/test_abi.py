@@ -50,6 +50,7 @@ def test_dropin_cxx_symbols():
                          check=True).stdout
     assert "preFreeSpMV(double*, int*, int*, double*, double*, int, int, int, double*, double*)" in out
     assert "preFreeSpMV(float*, int*, int*, float*, float*, int, int, int, double*, double*)" in out
+    assert "preFreeSpMV(pf_half*, int*, int*, pf_half*, pf_half*, int, int, int, double*, double*)" in out
 
 
 def test_kernel_library_targets_gfx950():
