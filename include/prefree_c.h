@@ -86,6 +86,8 @@ typedef struct pf_plan_info {
     size_t workspace_bytes;
     int row_aligned;      /* FLAT 1024/2048: 1 = each tile owns the rows starting in it (all rows hold at
                              most 256 nnz); no row is split and no combine kernel runs */
+    int x_windows;        /* split-row FLAT 1024/2048: 1 = tiles dealt to XCDs by the eighth of x they
+                             start in (chosen when rows span 4+ tiles and x exceeds one XCD's 4 MB L2) */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -122,6 +124,10 @@ int pf_plan_set_keep_cached(pf_plan *plan, int keep_cached);
  * row holds at most 256 nnz), 0 = nnz tiles with split rows combined by a
  * second kernel.  Both give the same y. */
 int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned);
+/* Split-row FLAT 1024/2048 only: 1 = the plan's first call records, with the row map, which eighth of x
+ * each tile starts in, and later calls deal the tiles to the 8 XCDs by it (long rows then read one XCD's
+ * share of x from its L2); 0 = tiles dealt by position.  Both give the same y. */
+int pf_plan_set_x_windows(pf_plan *plan, int x_windows);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).

@@ -51,7 +51,14 @@ typedef struct pfk_spmv_args {
     int map_ready;     /* 1: row_map holds the rows an earlier call found; 0: search (and record them) */
     int row_aligned;   /* FLAT 1024/2048: 1 = each tile owns the rows starting in it (every row must hold
                           at most PFK_ALIGN_ROW_MAX nnz); no split rows, no pfk_spmv_fixup */
+    int *sched;        /* split-row FLAT 1024/2048: x-window schedule of the tiles, [PFK_SCHED_INTS(ntiles,
+                          sched_cap)] ints whose first 16 are zero before the call that records the row map;
+                          NULL = tiles dealt to XCDs by position */
+    long long sched_cap; /* tiles per XCD list: at least ceil(ntiles / 8) */
 } pfk_spmv_args;
+
+/* Ints of an x-window schedule. */
+#define PFK_SCHED_INTS(ntiles, cap) (16 + 8 * (cap) + (ntiles))
 
 /* Longest row a row-aligned FLAT plan accepts. */
 #define PFK_ALIGN_ROW_MAX 256

@@ -59,7 +59,7 @@ class PlanInfo(ctypes.Structure):
                 ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
                 ("grid", ctypes.c_longlong),
-                ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int)]
+                ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -90,7 +90,8 @@ class SpmvArgs(ctypes.Structure):
                 ("nnz", ctypes.c_int), ("tile", ctypes.c_int), ("guess_spread", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p), ("row_map", ctypes.c_void_p),
-                ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int)]
+                ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int), ("sched", ctypes.c_void_p),
+                ("sched_cap", ctypes.c_longlong)]
 
 
 _lib = None
@@ -124,6 +125,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_run_tiles, [_vp, _i])
         _sig(L.pf_plan_set_keep_cached, [_vp, _i])
         _sig(L.pf_plan_set_row_aligned, [_vp, _i])
+        _sig(L.pf_plan_set_x_windows, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -269,6 +271,9 @@ class Plan:
 
     def set_row_aligned(self, row_aligned):
         _check(lib().pf_plan_set_row_aligned(self._h, int(bool(row_aligned))), "pf_plan_set_row_aligned")
+
+    def set_x_windows(self, x_windows):
+        _check(lib().pf_plan_set_x_windows(self._h, int(bool(x_windows))), "pf_plan_set_x_windows")
 
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),

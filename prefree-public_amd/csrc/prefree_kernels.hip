@@ -87,6 +87,8 @@ struct Args {
     acc_t<T> *__restrict__ tail;
     int *__restrict__ owner;
     int *__restrict__ err;
+    int *__restrict__ sched;      // split-row FLAT x-window schedule (see k_flat), or null
+    long long sched_cap;          // tiles per XCD list
 };
 
 // Long-row threshold of ADAPTIVE for tile size K (keys per wave tile).  A
@@ -977,6 +979,58 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
     if (err && lane == 0) atomicOr(a.err, 1);
 }
 
+// ---- x-window schedule of split-row FLAT tiles ------------------------------
+//
+// For matrices whose long rows sweep an x larger than one XCD's L2 (sorted
+// columns: a row of 300k nnz touches every line of an 8 MB x), the tiles are
+// dealt to XCDs by the part of x they start in rather than by position: tile t
+// goes to list k = 8 * col[t*K] / n.  The first call of a plan (the one that
+// searches rows) appends each tile to its list; later calls run workgroup
+// (XCD k, slot s) on the s-th tile of list k, so the XCD's long-row tiles read
+// one eighth of x, which its L2 holds.  Lists hold at most cap tiles; a tile
+// finding its list full goes to an overflow list whose tiles fill the other
+// XCDs' spare slots, so every XCD gets at most cap tiles whatever the columns.
+// Every tile still runs exactly once with the same work, so y is unchanged.
+// Layout (ints): [0, 8) list counts, [8] overflow count, [16, 16 + 8 cap) the
+// lists, then the overflow list (ntiles).  The counts start at 0 before the
+// recording call.
+constexpr int kSchedHead = 16;
+
+__device__ __forceinline__ void sched_record(int *sched, long long cap, long long t, int col0, int n)
+{
+    long long k = n > 0 ? ((long long)col0 * kXcds) / n : 0;
+    k = k < 0 ? 0 : (k >= kXcds ? kXcds - 1 : k);
+    const int pos = atomicAdd(&sched[k], 1);
+    if (pos < cap) {
+        sched[kSchedHead + k * cap + pos] = (int)t;
+    } else {
+        const int o = atomicAdd(&sched[kXcds], 1);
+        sched[kSchedHead + kXcds * cap + o] = (int)t;
+    }
+}
+
+// The tile of this workgroup under a recorded schedule, -1 for a spare slot.
+__device__ __forceinline__ long long sched_tile(const int *__restrict__ sched, long long cap, long long ntiles)
+{
+    const int k = (int)(blockIdx.x % kXcds);
+    const long long s = blockIdx.x / kXcds;
+    long long before = 0, mine = 0;
+#pragma unroll
+    for (int i = 0; i < kXcds; ++i) {
+        const long long ci = min((long long)sched[i], cap);
+        if (i < k) before += cap - ci;
+        if (i == k) mine = ci;
+    }
+    long long t = -1;
+    if (s < mine) {
+        t = sched[kSchedHead + k * cap + s];
+    } else {
+        const long long j = before + (s - mine);
+        if (j < (long long)sched[kXcds]) t = sched[kSchedHead + kXcds * cap + j];
+    }
+    return t < ntiles ? t : -1;
+}
+
 // ---- k_flat: FLAT tiles with the row search remembered across calls ---------
 //
 // One workgroup (4 wave64s) per tile of K nnz, XCD-interleaved.  A FLAT tile's
@@ -1019,9 +1073,9 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const long long t = xcd_tile(a.g8);
-    if (t >= a.ntiles)
-        return;  // whole workgroup: padding of the XCD mapping
+    const long long t = (MODE == kFlatMemo && a.sched) ? sched_tile(a.sched, a.sched_cap, a.ntiles) : xcd_tile(a.g8);
+    if (t < 0 || t >= a.ntiles)
+        return;  // whole workgroup: padding of the XCD mapping, or a spare schedule slot
     const int m = a.m, nnz = a.nnz;
     const bool last = t == a.ntiles - 1;
     const int kb = (int)(t * K);
@@ -1044,6 +1098,8 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
             s_info[0] = e0.x; s_info[1] = e0.y; s_info[2] = e1.x; s_info[3] = e1.y;
         }
     } else if (wave == 2) {  // f: first row with row_ptr >= kb
+        if (MODE == kFlatSearch && a.sched && lane == 0)
+            sched_record(a.sched, a.sched_cap, t, kb < nnz ? a.col[kb] : 0, a.n);
         const int f = wave_search_lt<false>(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
                                             a.guess_spread, lane) + 1;
         if (lane == 0) {
@@ -1953,6 +2009,8 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.tail = static_cast<acc_t<T> *>(a->tail_slot);
     r.owner = a->owner_row;
     r.err = a->err_flag;
+    r.sched = a->sched;
+    r.sched_cap = a->sched_cap;
     return r;
 }
 
@@ -2091,8 +2149,8 @@ int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
     if (dbg)
         hipLaunchKernelGGL((k_flat<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr, dbg);
     else if (a->row_map && a->map_ready)
-        hipLaunchKernelGGL((k_flat<T, K, kFlatMemo>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, a->row_map,
-                           nullptr);
+        hipLaunchKernelGGL((k_flat<T, K, kFlatMemo>), dim3((unsigned)(a->sched ? a->sched_cap * kXcds : grid)),
+                           dim3(kBS), 0, S(stream), r, a->row_map, nullptr);
     else
         hipLaunchKernelGGL((k_flat<T, K, kFlatSearch>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
                            a->row_map, nullptr);

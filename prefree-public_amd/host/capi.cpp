@@ -45,6 +45,20 @@ constexpr int kFlowTile = 256;
 // FLAT tiles of 1024 and 2048 nnz (k_flat) remember the rows their search found.
 bool uses_row_map(int variant, int tile) { return variant == PF_FLAT && (tile == 1024 || tile == 2048); }
 
+constexpr long long kXcdL2Bytes = 4LL << 20;  // MI355X: 4 MB of L2 per XCD
+
+// Tiles per XCD list of an x-window schedule: an even share plus 2% slack.
+long long sched_cap(long long ntiles) { return (ntiles + kXcds - 1) / kXcds + ntiles / 400 + 1; }
+
+int value_bytes(int dtype);
+
+// Rows that span several tiles over an x larger than one XCD's L2: deal the
+// split-row FLAT tiles to XCDs by the part of x they start in.
+int x_windows_rule(const pf_row_stats &s, long long n, int dtype, int tile, int row_aligned)
+{
+    return (!row_aligned && s.max_row_len >= 4LL * tile && n * value_bytes(dtype) > kXcdL2Bytes) ? 1 : 0;
+}
+
 int value_bytes(int dtype) { return dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : dtype == PF_F16 ? 2 : 0; }
 // Bytes of one split-row partial sum (head / tail slot): fp32 in the fp16 mode.
 int slot_bytes(int dtype) { return dtype == PF_F16 ? 4 : value_bytes(dtype); }
@@ -174,24 +188,27 @@ bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
 }
 
 // PF_AUTO: a tuning-table row if one matches; else
-//   * no row longer than PFK_ALIGN_ROW_MAX, or fp16 values (FLAT only): FLAT (1024 nnz per tile for fp64,
-//     2048 for fp32) with row-aligned tiles, one launch per call;
+//   * no row longer than PFK_ALIGN_ROW_MAX, or fp16 values (FLAT only): FLAT
+//     (1024 nnz per tile for fp64, 2048 for fp32 / fp16), row-aligned when the
+//     rows fit: one launch per call;
 //   * a matrix too small to give half the resident waves a 512-key tile:
 //     ADAPTIVE with the smallest tile (one wave per tile, launch-bound anyway);
-//   * long rows carrying most of the nnz (mean >= 16 and rows beyond ADAPTIVE's
-//     long-row threshold, e.g. a few dense rows): ADAPTIVE 512, whose runs
-//     keep a long row's pieces on one wave;
-//   * otherwise FLAT with split rows.
-// (Measured on MI355X: C2 row-aligned FLAT 58.4 us vs ADAPTIVE 75.0; C4 346 vs
-// 400; C1 3.3 vs ADAPTIVE-188 4.5; C3 split FLAT 222 vs ADAPTIVE 230; C5
-// ADAPTIVE 1489 vs FLAT 1582.)
+//   * long rows carrying most of the nnz (mean >= 16, e.g. a few dense rows):
+//     split-row FLAT with 2048-nnz tiles;
+//   * otherwise split-row FLAT with 1024-nnz tiles.
+// Split-row FLAT plans deal their tiles to XCDs by x window when rows span
+// several tiles over an x larger than one XCD's L2 (x_windows_rule).
+// (Measured on MI355X, us per call: C2 row-aligned FLAT 58.4 vs ADAPTIVE 75.0;
+// C4 346 vs 400; C1 3.3 vs ADAPTIVE-188 4.5; C5 FLAT 2048 with x windows 1107 vs
+// ADAPTIVE 1494, fp32 679 vs 882; C3 FLAT 1024 with x windows 210 vs 2048 219
+// vs ADAPTIVE 230.)
 Choice auto_choice(const pf_row_stats &s, int dtype)
 {
     Choice c;
     if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
-    if (s.max_row_len <= PFK_ALIGN_ROW_MAX || dtype == PF_F16) {  // fp16: FLAT tiles only
-        c.variant = PF_FLAT;
+    c.variant = PF_FLAT;
+    if (s.max_row_len <= PFK_ALIGN_ROW_MAX || dtype == PF_F16) {
         c.tile = default_tile(PF_FLAT, dtype);
         return c;
     }
@@ -201,14 +218,7 @@ Choice auto_choice(const pf_row_stats &s, int dtype)
         c.tile = 188;
         return c;
     }
-    const bool long_rows = s.max_row_len > pfk_adaptive_long_row_min(dtype, big);
-    if (long_rows && nnz >= 16 * m) {
-        c.variant = PF_ADAPTIVE;
-        c.tile = big;
-        return c;
-    }
-    c.variant = PF_FLAT;
-    c.tile = default_tile(PF_FLAT, dtype);
+    c.tile = nnz >= 16 * m ? 2048 : 1024;
     return c;
 }
 
@@ -281,10 +291,12 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.workspace_bytes = (size_t)(r.ntiles * (2 * vb + 4) + 3 * 256);
         if (uses_row_map(PF_FLAT, tile)) {
             r.workspace_bytes += (size_t)(r.ntiles + 1) * 8 + 256;
+            r.workspace_bytes += (size_t)PFK_SCHED_INTS(r.ntiles, sched_cap(r.ntiles)) * 4 + 512;
             // Short rows only: each tile owns the rows starting in it, nothing
             // is split and a step is one launch.
             r.row_aligned = s.max_row_len <= PFK_ALIGN_ROW_MAX ? 1 : 0;
             if (r.row_aligned) r.needs_fixup = 0;
+            r.x_windows = x_windows_rule(s, s.m, dtype, tile, r.row_aligned);  // n taken as m; plans use n
         }
         if (tile == kFlowTile) {  // runs of tiles, rows carried across tile edges inside a run
             r.run_tiles = choose_run(tile, r.ntiles, nominal_resident_waves(dtype, tile));
@@ -316,6 +328,8 @@ struct pf_plan {
     int *err = nullptr;
     int *row_map = nullptr;  // FLAT 1024/2048: tile -> (first row, row_ptr there), found by the first call
     bool map_ready = false;  // set once a call that records the map has been issued
+    int *sched = nullptr;    // split-row FLAT 1024/2048: x-window schedule, recorded with the map
+    long long sched_cap = 0;
 };
 
 namespace {
@@ -345,6 +359,8 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
         }
     }
     if (c.tile == info.tile && c.variant == info.variant) apply_overrides(c, info);
+    if (uses_row_map(info.variant, info.tile))
+        info.x_windows = x_windows_rule(s, n, dtype, info.tile, info.row_aligned);
 
     pf_plan *p = new pf_plan();
     p->m = m;
@@ -367,7 +383,10 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
         p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
         if (uses_row_map(info.variant, info.tile)) {
             const size_t owners = ((size_t)info.ntiles * 4 + 255) & ~(size_t)255;
+            const size_t map = ((size_t)(info.ntiles + 1) * 8 + 255) & ~(size_t)255;
             p->row_map = reinterpret_cast<int *>(w + 256 + 2 * slots + owners);
+            p->sched = reinterpret_cast<int *>(w + 256 + 2 * slots + owners + map);
+            p->sched_cap = sched_cap(info.ntiles);
         }
     }
     rc = pfk_fill_zero(p->err, 256, stream);
@@ -537,6 +556,17 @@ int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned)
         return fail(PF_ERR_INVALID, "a row holds more than " + std::to_string(PFK_ALIGN_ROW_MAX) + " nnz");
     plan->info.row_aligned = row_aligned;
     plan->info.needs_fixup = row_aligned ? 0 : (plan->info.ntiles > 1);
+    if (row_aligned) plan->info.x_windows = 0;
+    return PF_OK;
+}
+
+int pf_plan_set_x_windows(pf_plan *plan, int x_windows)
+{
+    if (!plan || (x_windows != 0 && x_windows != 1)) return fail(PF_ERR_INVALID, "x_windows must be 0 or 1");
+    if (!uses_row_map(plan->info.variant, plan->info.tile) || (x_windows && plan->info.row_aligned))
+        return fail(PF_ERR_UNSUPPORTED, "x-window schedules are for split-row FLAT 1024 or 2048 plans");
+    if (x_windows && !plan->info.x_windows) plan->map_ready = false;  // the next call records the schedule
+    plan->info.x_windows = x_windows;
     return PF_OK;
 }
 
@@ -576,6 +606,10 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.row_map = plan->row_map;
     a.map_ready = plan->map_ready ? 1 : 0;
     a.row_aligned = plan->info.row_aligned;
+    a.sched = (plan->info.x_windows && plan->sched) ? plan->sched : nullptr;
+    a.sched_cap = plan->sched_cap;
+    if (a.sched && !plan->map_ready)  // the recording call starts from empty lists
+        PF_TRY(pfk_fill_zero(a.sched, 16 * sizeof(int), stream), "schedule reset");
     const int dt = plan->info.dtype;
     switch (plan->info.variant) {
     case PF_ADAPTIVE:
@@ -766,6 +800,8 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
         std::swap(plan->err, best_plan->err);
         std::swap(plan->row_map, best_plan->row_map);
         std::swap(plan->map_ready, best_plan->map_ready);
+        std::swap(plan->sched, best_plan->sched);
+        std::swap(plan->sched_cap, best_plan->sched_cap);
         pf_plan_destroy(best_plan);
     }
     // y = A x with the chosen configuration, so that the caller's y is defined.

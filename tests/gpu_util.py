@@ -24,7 +24,8 @@ def dev(a, min_len=4):
     return torch.from_numpy(a).to(DEV)
 
 
-def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2, row_aligned=None):
+def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2, row_aligned=None,
+             x_windows=None):
     """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info).
 
     The plan executes `repeat` times, y refilled with `fill` before each call,
@@ -32,7 +33,8 @@ def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("n
     kind from later ones (FLAT records the rows its search found and later
     calls read them), so the first and the last y must agree bit for bit
     (up to atomic ordering for the reference's PREFREE algorithm).
-    row_aligned (FLAT 1024/2048): force row-aligned (1) or split-row (0) tiles."""
+    row_aligned (FLAT 1024/2048): force row-aligned (1) or split-row (0) tiles; x_windows (split-row
+    FLAT): force the x-window schedule on (1) or off (0)."""
     m, n, nnz = len(rp) - 1, len(x), len(col)
     d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
     y = torch.full((max(m, 1),), fill, dtype=TORCH[dtype], device=DEV)
@@ -41,6 +43,8 @@ def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("n
     with pf.Plan(d_rp, d_col, m, n, nnz, dtype, variant, tile, stream=stream) as p:
         if row_aligned is not None:
             p.set_row_aligned(row_aligned)
+        if x_windows is not None:
+            p.set_x_windows(x_windows)
         for k in range(repeat):
             y.fill_(fill)
             p.execute(d_rp, d_col, d_val, d_x, y, stream=stream)

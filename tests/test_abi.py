@@ -112,13 +112,19 @@ def test_select_auto_very_short_rows_is_flat():
         assert i.variant == pf.FLAT and i.tile == tile and i.row_aligned == 1 and i.needs_fixup == 0
 
 
-def test_select_auto_power_law_is_flat_dense_rows_adaptive():
-    """C3 shape (short rows plus a few long ones) -> FLAT; C5 shape (dense rows hold most nnz) -> ADAPTIVE 512."""
+def test_select_auto_long_rows_are_split_row_flat():
+    """C3 shape (short rows plus a few long ones) -> split-row FLAT 1024; C5 shape (dense rows hold most nnz)
+    -> split-row FLAT 2048; both with the x-window schedule when x exceeds one XCD's 4 MB L2."""
     c3 = pf.select(make_stats(2000000, 15200000, 200000), "f64", "auto")
     assert c3.variant == pf.FLAT and c3.tile == 1024 and c3.row_aligned == 0 and c3.needs_fixup == 1
+    assert c3.x_windows == 1                                     # x = 16 MB
     c5 = pf.select(make_stats(1000000, 315647995, 499000), "f64", "auto")
-    assert c5.variant == pf.ADAPTIVE and c5.tile == 512 and c5.needs_fixup == 1 and c5.run_tiles == 16
-    assert c5.run_tiles == run_for(c5.ntiles, 256 * 4 * 3)
+    assert c5.variant == pf.FLAT and c5.tile == 2048 and c5.row_aligned == 0 and c5.needs_fixup == 1
+    assert c5.x_windows == 1                                     # x = 8 MB
+    c5f = pf.select(make_stats(1000000, 315647995, 499000), "f32", "auto")
+    assert c5f.variant == pf.FLAT and c5f.tile == 2048 and c5f.x_windows == 0   # x = 4 MB fits one L2
+    small = pf.select(make_stats(30000, 200000, 3000), "f64", "auto")
+    assert small.variant == pf.ADAPTIVE and small.tile == 188    # too small for 512-key tiles
 
 
 def test_select_long_rows_need_the_combine_kernel():

@@ -225,6 +225,57 @@ def test_row_aligned_refused_for_long_rows():
         torch.cuda.synchronize()
 
 
+def x_window_cases():
+    out = [(name, rp, col, n) for name, rp, col, n in CASES if len(col) > 4096]
+    for cfg, scale in ((5, 40000), (3, 60000)):
+        rp, col, _ = pf.synth_csr(cfg, seed=23, scale_n=scale, dtypes=())
+        out.append((f"C{cfg}", rp, col, len(rp) - 1))
+    # long rows whose columns all lie in the first eighth of x: every tile picks list 0, so all but
+    # cap of them go through the overflow list to the other XCDs' spare slots
+    rng = np.random.default_rng(31)
+    lens = rng.integers(3000, 9000, size=40)
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    n = 80000
+    col = np.concatenate([np.sort(rng.choice(n // 8, size=k, replace=False)) for k in lens]).astype(np.int32)
+    out.append(("skewed_first_eighth", rp, col, n))
+    return out
+
+
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_flat_x_window_schedule_same_y(tile):
+    """Split-row FLAT with tiles dealt to XCDs by x window (recorded by the first call, used from the
+    second) gives exactly the y of the positional mapping, on KAT and U[-1,1] inputs."""
+    for name, rp, col, n in x_window_cases():
+        for kat in (True, False):
+            if kat:
+                val, x = oracle.initvec(len(col)), oracle.initvec(n)
+            else:
+                rng = np.random.default_rng(len(col))
+                val, x = rng.uniform(-1, 1, len(col)), rng.uniform(-1, 1, n)
+            ys = []
+            for xw in (1, 0):
+                y, info = gpu_spmv(rp, col, val, x, "flat", tile=tile, row_aligned=0, x_windows=xw, repeat=3)
+                assert info["x_windows"] == xw and info["row_aligned"] == 0
+                ys.append(y)
+            assert np.array_equal(ys[0], ys[1]), name
+            assert_parity(rp, col, val, x, ys[0], "f64", exact=kat and kat_exact_possible(rp, "f64"), what=name)
+
+
+def test_x_window_schedule_planning_rule():
+    """On for split-row FLAT when rows span 4+ tiles over an x beyond 4 MB; refused for row-aligned plans."""
+    from gpu_util import dev
+    rp, col, _ = pf.synth_csr(5, seed=2, scale_n=600000, dtypes=())   # x 4.8 MB, rows up to 500k
+    m = len(rp) - 1
+    with pf.Plan(dev(rp), dev(col), m, m, len(col), "f64", "flat", 1024) as p:
+        assert p.info.row_aligned == 0 and p.info.x_windows == 1
+    rp, col, _ = pf.synth_csr(2, seed=2, scale_n=300, dtypes=())
+    m = len(rp) - 1
+    with pf.Plan(dev(rp), dev(col), m, m, len(col), "f64", "flat", 1024) as p:
+        assert p.info.row_aligned == 1 and p.info.x_windows == 0
+        with pytest.raises(pf.PrefreeError):
+            p.set_x_windows(1)
+
+
 @pytest.mark.parametrize("variant", ["adaptive", "flat"])
 def test_deterministic(variant):
     rp, col, v = pf.synth_csr(5, seed=4, scale_n=40000)
