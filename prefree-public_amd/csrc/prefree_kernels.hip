@@ -361,6 +361,13 @@ struct ReduceLds {
     T red[kWaves];
 };
 
+// The row-aligned kernels' lists also keep the sums of the listed rows.
+template <typename T, int WCAP, int BCAP>
+struct RowsReduceLds : ReduceLds<T, WCAP, BCAP> {
+    T ws[WCAP];
+    T bs[BCAP];
+};
+
 // Row sums of a tile whose products sit in s_prod (index = nnz - base).
 // bounds(i, ra, rb) gives row_ptr[r], row_ptr[r+1] of local row i; put(i, s)
 // stores the sum.  Rows of <= kThreadMax products: one lane each, summed in
@@ -1277,36 +1284,114 @@ __device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsS
         if (tid + q * kBS < d.cnt) s_rp[tid + q * kBS] = rr[q];
 }
 
+// fp64 / fp32 row sums of a row-aligned tile whose bounds fit LDS, written as
+// 16-byte non-temporal stores of consecutive rows.  Rows of at most
+// kThreadMax products are summed by one lane, in nnz order, into registers;
+// longer rows are listed and summed by a wave (or the workgroup) into LDS
+// slots.  Once every product has been read, the sums are written over the
+// product buffer and stored from there, so the staging costs no LDS of its own
+// (occupancy stays that of the product buffer).  The range check of the store
+// resource, exactly the tile's rows, drops the dwords past the last row.
+template <typename T, int K>
+__device__ __forceinline__ void rows_sums_staged(const RowsDesc &d, T *s_prod, const int *s_rp,
+                                                 RowsReduceLds<T, RowsShape<T, K>::kWaveCap,
+                                                               RowsShape<T, K>::kBlockCap> &L,
+                                                 __amdgpu_buffer_rsrc_t ry)
+{
+    using S = RowsShape<T, K>;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    T ys[S::kRpPer];
+    bool mine[S::kRpPer];
+#pragma unroll
+    for (int q = 0; q < S::kRpPer; ++q) {
+        ys[q] = T(0);
+        mine[q] = false;
+        const int i = tid + q * kBS;
+        if (i < d.nr) {
+            const int ra = max(s_rp[i], d.A);
+            const int rb = min(s_rp[i + 1], d.B);
+            const int a0 = ra - d.kb;
+            const int len = rb - ra;
+            if (len <= kThreadMax) {
+                T acc = T(0);
+                for (int j = 0; j < len; ++j)
+                    acc += s_prod[a0 + j];
+                ys[q] = acc;
+                mine[q] = true;
+            } else if (len <= kWaveMax) {
+                const int j = atomicAdd(&L.nw, 1);
+                if (j < S::kWaveCap) { L.wl[j] = i; L.wa[j] = a0; L.wb[j] = a0 + len; }
+            } else {
+                const int j = atomicAdd(&L.nb, 1);
+                if (j < S::kBlockCap) { L.bl[j] = i; L.ba[j] = a0; L.bb[j] = a0 + len; }
+            }
+        }
+    }
+    lds_sync();
+    const int nw = min(L.nw, S::kWaveCap);
+    const int nb = min(L.nb, S::kBlockCap);
+    for (int j = wave; j < nw; j += kWaves) {
+        T acc = T(0);
+        for (int q = L.wa[j] + lane; q < L.wb[j]; q += kWave)
+            acc += s_prod[q];
+        acc = wave_sum(acc);
+        if (lane == 0) L.ws[j] = acc;
+    }
+    for (int j = 0; j < nb; ++j) {
+        T acc = T(0);
+        for (int q = L.ba[j] + tid; q < L.bb[j]; q += kBS)
+            acc += s_prod[q];
+        acc = wave_sum(acc);
+        if (lane == 0) L.red[wave] = acc;
+        lds_sync();
+        if (tid == 0) {
+            T tot = L.red[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w)
+                tot += L.red[w];
+            L.bs[j] = tot;
+        }
+        lds_sync();
+    }
+    lds_sync();  // every product has been read: the buffer takes the sums
+    T *s_y = s_prod;
+#pragma unroll
+    for (int q = 0; q < S::kRpPer; ++q)
+        if (mine[q]) s_y[tid + q * kBS] = ys[q];
+    for (int j = tid; j < nw; j += kBS) s_y[L.wl[j]] = L.ws[j];
+    for (int j = tid; j < nb; j += kBS) s_y[L.bl[j]] = L.bs[j];
+    lds_sync();
+    constexpr int kPer = 16 / (int)sizeof(T);
+    const int n16 = (d.nr + kPer - 1) / kPer;
+    for (int j = tid; j < n16; j += kBS)
+        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16, 0, kAuxNt);
+}
+
 // Row sums of a staged row-aligned tile into y.  Bounds come from LDS; a tile
 // with more rows than LDS holds (long runs of empty rows) reads the rest from
 // row_ptr in a separate branch, so the common path waits on LDS only and
 // leaves the y stores and any loads already issued for the next tile in flight.
 template <typename T, int K>
-__device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, const acc_t<T> *s_prod,
+__device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, acc_t<T> *s_prod,
                                             const int *s_rp,
-                                            ReduceLds<acc_t<T>, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
+                                            RowsReduceLds<acc_t<T>, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
 {
     using S = RowsShape<T, K>;
     using P = acc_t<T>;
     if (d.nr < S::kRpCap) {
-        // fp64 / fp32: row sums staged in LDS, then y[f0 .. f0 + nr) written as
-        // 16-byte non-temporal stores through a resource over exactly those rows
-        // (the range check drops the whole dwords past the last row).  y is not
-        // read again here; keeping it out of L2 leaves room for x (C4: 345
-        // instead of 377 us per call with 8-byte stores through L2).
+        // y[f0 .. f0 + nr) through a resource over exactly those rows, written
+        // non-temporally: y is not read again here, and keeping it out of L2
+        // leaves room for x (C4: 345 instead of 377 us per call with 8-byte
+        // stores through L2).
         const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f0, (long long)d.nr * (long long)sizeof(T));
         const auto bounds = [&](int i, int &ra, int &rb) {
             ra = s_rp[i];
             rb = s_rp[i + 1];
         };
         if constexpr (sizeof(T) >= 4) {
-            __shared__ __attribute__((aligned(16))) T s_y[S::kRpCap + 4];
-            reduce_tile(s_prod, L, d.kb, d.A, d.B, d.nr, bounds, [&](int i, P s) { s_y[i] = T(s); });
-            constexpr int kPer = 16 / (int)sizeof(T);
-            const int n16 = (d.nr + kPer - 1) / kPer;
-            for (int j = (int)threadIdx.x; j < n16; j += kBS)
-                __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16,
-                                                       0, kAuxNt);
+            rows_sums_staged<T, K>(d, s_prod, s_rp, L, ry);
         } else {
             // fp16: one 2-byte store per row.  The range check works on whole
             // dwords, so a 16-byte store ending in a half-covered dword would
@@ -1337,7 +1422,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     __shared__ __attribute__((aligned(16))) acc_t<T> s_prod[DESC ? 4 : S::kProd];
     __shared__ int s_rp[DESC ? 4 : S::kRpCap];
     __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l] (search modes)
-    __shared__ ReduceLds<acc_t<T>, S::kWaveCap, S::kBlockCap> L;
+    __shared__ RowsReduceLds<acc_t<T>, S::kWaveCap, S::kBlockCap> L;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
