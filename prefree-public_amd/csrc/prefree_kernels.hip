@@ -1413,7 +1413,7 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
     }
 }
 
-template <typename T, int K, int MODE>
+template <typename T, int K, int MODE, bool PRIO = false>
 __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, int *__restrict__ dbg)
 {
     using S = RowsShape<T, K>;
@@ -1424,6 +1424,14 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     __shared__ int s_info[4];  // f, row_ptr[f], l, row_ptr[l] (search modes)
     __shared__ RowsReduceLds<acc_t<T>, S::kWaveCap, S::kBlockCap> L;
 
+    // PRIO (chosen at launch for matrices of very short rows, under 4 nnz on
+    // average): raised wave priority while the tile's loads are issued, so a
+    // workgroup that has just started gets its memory streams going ahead of
+    // the long per-row phase of older workgroups on the CU (C4: 320 instead of
+    // 332 us per call).  With longer rows it delays the older workgroups'
+    // stores instead (C2: 60.2 instead of 58.1 us), and even untaken it changes
+    // the code, hence a separate instantiation.
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -1498,6 +1506,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     T xv[VPT][4], ov, xo;
     int rr[S::kRpPer];
     rows_loads<T, K>(a, d, c, xv, ov, xo, rr);
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     rows_stage<T, K>(d, v, xv, ov, xo, rr, s_prod, s_rp);
     lds_sync();
 
@@ -2222,6 +2231,9 @@ int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
         if (dbg)
             hipLaunchKernelGGL((k_rows<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr,
                                dbg);
+        else if (a->row_map && a->map_ready && (long long)a->nnz < 4LL * a->m)  // very short rows
+            hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, true>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
+                               a->row_map, nullptr);
         else if (a->row_map && a->map_ready)
             hipLaunchKernelGGL((k_rows<T, K, kFlatMemo>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r,
                                a->row_map, nullptr);
