@@ -13,7 +13,12 @@
 // warm-up and timed launches) is printed as our_total; a failed check exits
 // with status 1 instead of printing "Success!" regardless.
 //
-// usage: cdspmv <matrix.mtx> [--f32] [--variant auto|prefree|adaptive|flat] [--no-check]
+// --f16 runs the reference's fp16 build (valT = half, include/common.h:43-46):
+// values are IEEE binary16 (pf_half), the sequential check rounds every product
+// and every sum to binary16 as the reference's half operators do, and the
+// relative tolerance is the reference's 1e-1 (test_cdspmv.cpp:37-52).
+//
+// usage: cdspmv <matrix.mtx> [--f32|--f16] [--variant auto|prefree|adaptive|flat] [--no-check]
 #include "PreFree.h"
 #include "prefree_c.h"
 
@@ -27,10 +32,56 @@
 
 namespace {
 
+// IEEE binary16 <-> float.  Every binary16 value is a float, so widening is
+// exact; narrowing scales by a power of two (exact) and rounds the scaled
+// significand with nearbyint, which rounds to nearest even in the default mode.
+float widen(pf_half h)
+{
+    const int s = h.bits >> 15, e = (h.bits >> 10) & 31, f = h.bits & 1023;
+    const float mag = e == 31 ? (f ? NAN : INFINITY)
+                    : e == 0  ? std::ldexp((float)f, -24)
+                              : std::ldexp((float)(f | 1024), e - 25);
+    return s ? -mag : mag;
+}
+
+pf_half narrow(float v)
+{
+    const unsigned short sign = std::signbit(v) ? 0x8000 : 0;
+    const float a = std::fabs(v);
+    if (std::isnan(a)) return pf_half{0x7e00};
+    if (std::isinf(a)) return pf_half{(unsigned short)(sign | 0x7c00)};
+    if (a < 0x1p-14f) return pf_half{(unsigned short)(sign | (unsigned short)std::nearbyint(a * 0x1p24f))};
+    int ex = 0;
+    std::frexp(a, &ex);                         // a = g * 2^ex, g in [0.5, 1)
+    int e = ex - 1;                             // a in [2^e, 2^(e+1))
+    float q = std::nearbyint(std::ldexp(a, 10 - e));   // 11-bit significand, 1024..2048
+    if (q == 2048.0f) q = 1024.0f, ++e;
+    if (e > 15) return pf_half{(unsigned short)(sign | 0x7c00)};
+    return pf_half{(unsigned short)(sign | ((e + 15) << 10) | ((int)q - 1024))};
+}
+
+double to_double(double v) { return v; }
+double to_double(float v) { return v; }
+double to_double(pf_half v) { return widen(v); }
+
+template <typename T> T from_float(float v) { return (T)v; }
+template <> pf_half from_float<pf_half>(float v) { return narrow(v); }
+
+// One operation of the reference's sequential SpMV in type T.  For binary16
+// the float result of a product or a sum of two binary16 values is rounded
+// once more to binary16; float carries 24 bits >= 2*11+2, so the two
+// roundings give the correctly rounded binary16 result of each operation.
+double mul_add(double t, double a, double b) { return t + a * b; }
+float mul_add(float t, float a, float b) { return t + a * b; }
+pf_half mul_add(pf_half t, pf_half a, pf_half b)
+{
+    return narrow(widen(t) + widen(narrow(widen(a) * widen(b))));
+}
+
 template <typename T>
 void init_vec(T *v, long long n)
 {
-    for (long long i = 0; i < n; ++i) v[i] = (T)(float)(i % 15);
+    for (long long i = 0; i < n; ++i) v[i] = from_float<T>((float)(i % 15));
 }
 
 // The harness's reference y: one accumulator per row, products added in
@@ -39,9 +90,9 @@ template <typename T>
 void serial_spmv(const T *val, const int *rp, const int *col, const T *x, T *y, int m)
 {
     for (int i = 0; i < m; ++i) {
-        T t = T(0);
-        for (int j = rp[i]; j < rp[i + 1]; ++j) t = t + val[j] * x[col[j]];
-        y[i] = y[i] + t;
+        T t = from_float<T>(0.0f);
+        for (int j = rp[i]; j < rp[i + 1]; ++j) t = mul_add(t, val[j], x[col[j]]);
+        y[i] = t;                                  // y starts at zero: y[i] + t == t
     }
 }
 
@@ -50,7 +101,7 @@ int check(const T *ref, const T *ours, int n, double tol)
 {
     int bad = 0;
     for (int i = 0; i < n; ++i) {
-        const double a = ref[i], b = ours[i];
+        const double a = to_double(ref[i]), b = to_double(ours[i]);
         const double den = std::fmax(std::fabs(a), std::fabs(b));
         const bool differ = std::isnan(a) != std::isnan(b) || (den > 0 && std::fabs(a - b) / den > tol);
         if (differ) {
@@ -69,7 +120,7 @@ int check(const T *ref, const T *ours, int n, double tol)
 template <typename T>
 int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_check)
 {
-    std::vector<T> val((size_t)nnz), x((size_t)n), y((size_t)m, T(0)), ys((size_t)m, T(0));
+    std::vector<T> val((size_t)nnz), x((size_t)n), y((size_t)m, from_float<T>(0.0f)), ys((size_t)m, from_float<T>(0.0f));
     init_vec(val.data(), nnz);
     init_vec(x.data(), n);
     std::printf("INIT DONE\n");
@@ -92,7 +143,8 @@ int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_chec
     (void)path;
     if (!do_check) return 0;
     serial_spmv(val.data(), rp, col, x.data(), ys.data(), m);
-    return check(ys.data(), y.data(), m, sizeof(T) == 8 ? 1e-8 : 1e-4) == 0 ? 0 : 1;
+    const double tol = sizeof(T) == 8 ? 1e-8 : sizeof(T) == 4 ? 1e-4 : 1e-1;
+    return check(ys.data(), y.data(), m, tol) == 0 ? 0 : 1;
 }
 
 }  // namespace
@@ -100,17 +152,18 @@ int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_chec
 int main(int argc, char **argv)
 {
     const char *path = nullptr;
-    bool f32 = false, do_check = true;
+    bool f32 = false, f16 = false, do_check = true;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
-        if (a == "--f32") f32 = true;
+        if (a == "--f32") f32 = true, f16 = false;
+        else if (a == "--f16") f16 = true, f32 = false;
         else if (a == "--no-check") do_check = false;
         else if (a == "--variant" && i + 1 < argc) setenv("PREFREE_VARIANT", argv[++i], 1);
         else if (a == "-h" || a == "--help") path = nullptr, i = argc;
         else if (!path) path = argv[i];
     }
     if (!path) {
-        std::printf("Run the code by './cdspmv matrix.mtx [--f32] [--variant auto|prefree|adaptive|flat] [--no-check]'.\n");
+        std::printf("Run the code by './cdspmv matrix.mtx [--f32|--f16] [--variant auto|prefree|adaptive|flat] [--no-check]'.\n");
         return 0;
     }
     std::printf("\n===%s===\n\n", path);
@@ -122,7 +175,9 @@ int main(int argc, char **argv)
         std::fprintf(stderr, "cdspmv: cannot read %s: %s\n", path, pf_mtx_last_error());
         return 2;
     }
-    const int rc = f32 ? run<float>(path, m, n, nnz, rp, col, do_check) : run<double>(path, m, n, nnz, rp, col, do_check);
+    const int rc = f16 ? run<pf_half>(path, m, n, nnz, rp, col, do_check)
+                 : f32 ? run<float>(path, m, n, nnz, rp, col, do_check)
+                       : run<double>(path, m, n, nnz, rp, col, do_check);
     pf_host_free(rp);
     pf_host_free(col);
     pf_host_free(val);

@@ -61,6 +61,29 @@ def test_cli_laplacian_passes_check(tmp_path, prec, variant):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("cfg,scale", [(2, 64), (3, 5000)])
+@pytest.mark.parametrize("variant", ["auto", "flat"])
+def test_cli_f16_passes_check(tmp_path, cfg, scale, variant):
+    """The reference's fp16 build: binary16 values, the sequential check rounds every operation."""
+    rp, col, _ = pf.synth_csr(cfg, seed=3, scale_n=scale, dtypes=())
+    f = str(tmp_path / "a.mtx")
+    write_mtx(f, rp, col)
+    r = run([f, "--f16", "--variant", variant])
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "Success!" in r.stdout and "our_perf:" in r.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", ["prefree", "adaptive"])
+def test_cli_f16_unsupported_variant_fails_loudly(tmp_path, variant):
+    rp, col, _ = pf.synth_csr(2, seed=1, scale_n=32, dtypes=())
+    f = str(tmp_path / "lap.mtx")
+    write_mtx(f, rp, col)
+    r = run([f, "--f16", "--variant", variant])
+    assert r.returncode != 0 and "PreFree error" in r.stdout + r.stderr
+
+
+@pytest.mark.gpu
 def test_cli_symmetric_power_law(tmp_path):
     rp, col, _ = pf.synth_csr(3, seed=2, scale_n=5000, dtypes=())
     f = str(tmp_path / "pl.mtx")
