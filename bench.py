@@ -107,6 +107,8 @@ def main():
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--x-windows", type=int, default=-1, choices=[-1, 0, 1],
                     help="split-row FLAT: force the x-window tile schedule off (0) or on (1); -1 = the plan's choice")
+    ap.add_argument("--chunk-nnz", type=int, default=-1,
+                    help="FLAT 1024/2048: nnz per XCD chunk of tiles (0 = one chunk per XCD); -1 = the plan's choice")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cold-steps", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -156,6 +158,8 @@ def main():
     t_plan = (time.perf_counter() - t_plan) * 1e3
     if args.x_windows >= 0:
         plan.set_x_windows(args.x_windows)
+    if args.chunk_nnz >= 0:
+        plan.set_chunk_nnz(args.chunk_nnz)
     info = plan.info.as_dict()
 
     def step():
@@ -271,6 +275,7 @@ def main():
                    "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
                    "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
                    "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
+                   "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
                    "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3)},
         "gbps_effective": round(gbs, 1),
         "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),

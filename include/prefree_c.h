@@ -88,6 +88,8 @@ typedef struct pf_plan_info {
                              most 256 nnz); no row is split and no combine kernel runs */
     int x_windows;        /* split-row FLAT 1024/2048: 1 = tiles dealt to XCDs by the eighth of x they
                              start in (chosen when rows span 4+ tiles and x exceeds one XCD's 4 MB L2) */
+    long long chunk_nnz;  /* FLAT 1024/2048 without x windows: tiles dealt to the 8 XCDs in chunks of
+                             consecutive tiles of about this many nnz (0 = one chunk per XCD) */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -128,6 +130,10 @@ int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned);
  * each tile starts in, and later calls deal the tiles to the 8 XCDs by it (long rows then read one XCD's
  * share of x from its L2); 0 = tiles dealt by position.  Both give the same y. */
 int pf_plan_set_x_windows(pf_plan *plan, int x_windows);
+/* FLAT 1024/2048 only: nnz per chunk of consecutive tiles given to one XCD (0 = one chunk of an eighth
+ * of the tiles per XCD).  Small chunks keep the eight XCDs streaming neighbouring addresses; large ones
+ * keep more of a row's x neighbourhood in one XCD's L2.  All values give the same y. */
+int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).
@@ -155,6 +161,7 @@ typedef struct pf_tune_result {
     int candidates;     /* configurations timed (including the plan's own) */
     double us;          /* microseconds per SpMV of the chosen configuration */
     double default_us;  /* of the configuration the plan had before tuning */
+    long long chunk_nnz; /* FLAT 1024/2048: XCD chunk of the chosen configuration (see pf_plan_info) */
 } pf_tune_result;
 int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x,
                      void *d_y, int reps, int flags, void *stream, pf_tune_result *result);

@@ -55,6 +55,9 @@ typedef struct pfk_spmv_args {
                           sched_cap)] ints whose first 16 are zero before the call that records the row map;
                           NULL = tiles dealt to XCDs by position */
     long long sched_cap; /* tiles per XCD list: at least ceil(ntiles / 8) */
+    long long chunk_nnz; /* FLAT 1024/2048 without a schedule: the tiles go to the 8 XCDs in chunks of
+                            consecutive tiles of about chunk_nnz nnz, chunk i to XCD i % 8; 0 = one chunk
+                            of ceil(ntiles / 8) tiles per XCD */
 } pfk_spmv_args;
 
 /* Ints of an x-window schedule. */
@@ -79,6 +82,8 @@ int pfk_adaptive_long_row_min(int dtype, int tile);
 int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves);
 /* The same for the FLAT kernel of 256-nnz tiles (k_flow). */
 int pfk_flow_resident_waves(int dtype, long long *waves);
+/* Workgroups a FLAT 1024/2048 launch without a schedule uses for ntiles tiles and chunk_nnz. */
+long long pfk_flat_grid(long long ntiles, int tile, long long chunk_nnz);
 
 /* Row statistics.  d_out: 44 unsigned long long (layout in prefree_kernels.hip). */
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,

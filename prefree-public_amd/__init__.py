@@ -59,7 +59,8 @@ class PlanInfo(ctypes.Structure):
                 ("long_row_min", ctypes.c_int), ("guess_spread", ctypes.c_int), ("needs_fixup", ctypes.c_int),
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
                 ("grid", ctypes.c_longlong),
-                ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int)]
+                ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
+                ("chunk_nnz", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -71,7 +72,7 @@ class TuneResult(ctypes.Structure):
     """pf_tune_result, include/prefree_c.h."""
     _fields_ = [("variant", ctypes.c_int), ("tile", ctypes.c_int), ("run_tiles", ctypes.c_int),
                 ("keep_cached", ctypes.c_int), ("candidates", ctypes.c_int), ("us", ctypes.c_double),
-                ("default_us", ctypes.c_double)]
+                ("default_us", ctypes.c_double), ("chunk_nnz", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -91,7 +92,7 @@ class SpmvArgs(ctypes.Structure):
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p), ("row_map", ctypes.c_void_p),
                 ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int), ("sched", ctypes.c_void_p),
-                ("sched_cap", ctypes.c_longlong)]
+                ("sched_cap", ctypes.c_longlong), ("chunk_nnz", ctypes.c_longlong)]
 
 
 _lib = None
@@ -126,6 +127,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_keep_cached, [_vp, _i])
         _sig(L.pf_plan_set_row_aligned, [_vp, _i])
         _sig(L.pf_plan_set_x_windows, [_vp, _i])
+        _sig(L.pf_plan_set_chunk_nnz, [_vp, _ll])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -164,6 +166,7 @@ def klib() -> ctypes.CDLL:
         _sig(K.pfk_debug_prefree_rows, [_vp, _i, _i, _i, _vp, _vp])
         _sig(K.pfk_adaptive_long_row_min, [_i, _i])
         _sig(K.pfk_supported_tiles, [_i, _i, ctypes.POINTER(_i), _i])
+        _sig(K.pfk_flat_grid, [ctypes.c_longlong, _i, ctypes.c_longlong], ctypes.c_longlong)
         _sig(K.pfk_device_name, [ctypes.c_char_p, _i])
         _sig(K.pfk_last_error, [], ctypes.c_char_p)
         _klib = K
@@ -275,6 +278,9 @@ class Plan:
     def set_x_windows(self, x_windows):
         _check(lib().pf_plan_set_x_windows(self._h, int(bool(x_windows))), "pf_plan_set_x_windows")
 
+    def set_chunk_nnz(self, chunk_nnz):
+        _check(lib().pf_plan_set_chunk_nnz(self._h, int(chunk_nnz)), "pf_plan_set_chunk_nnz")
+
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),
                "pf_plan_execute")
@@ -307,13 +313,14 @@ def spmv(row_ptr, col, val, x, y, m, n, nnz, dtype="f64", variant="auto", stream
 
 
 def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, run_tiles=0, stream=None,
-                     row_aligned=False):
+                     row_aligned=False, chunk_nnz=0):
     """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT (split or row-aligned
-    tiles) into `out` (int32[8*ntiles])."""
+    tiles, dealt to the XCDs in chunks of chunk_nnz) into `out` (int32[8*ntiles])."""
     total = nnz + m if merged else nnz
     ntiles = max(1, -(-total // tile))
     a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
-                 run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag), row_aligned=int(bool(row_aligned)))
+                 run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag), row_aligned=int(bool(row_aligned)),
+                 chunk_nnz=int(chunk_nnz))
     _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
            "pfk_debug_tile_desc")
     return ntiles

@@ -80,7 +80,8 @@ struct Args {
     int nnz;
     int guess_spread;
     long long ntiles;
-    long long g8;        // k_tiles: tiles per XCD (ceil(ntiles / 8))
+    long long g8;        // tiles per XCD, padded to whole chunks (grid = 8 * g8)
+    long long xch;       // tiles per chunk (see xcd_tile)
     long long tx;        // k_stream: tiles per XCD
     long long tpw;       // k_stream: tiles per workgroup
     acc_t<T> *__restrict__ head;  // split-row partial sums (fp32 in the fp16 mode)
@@ -104,12 +105,16 @@ constexpr int adaptive_lmax(int K) { return (K == 238 || K == 494) ? 16 : (K <= 
     X(double, PF_F64, 188) X(double, PF_F64, 238) X(double, PF_F64, 494) X(double, PF_F64, 512) \
     X(float, PF_F32, 440) X(float, PF_F32, 494) X(float, PF_F32, 1024)
 
-// Logical tile of this workgroup: XCD x (= blockIdx % 8) takes the contiguous
-// tiles [x*g8, (x+1)*g8), so neighbouring rows (and their x entries) share an L2.
-__device__ __forceinline__ long long xcd_tile(long long g8)
+// Logical tile of this workgroup.  Workgroups go to the XCDs round robin
+// (XCD x = blockIdx % 8).  The tiles are cut into chunks of xch contiguous
+// tiles, and in round r XCD x takes chunk 8r + x, so neighbouring rows (and
+// their x entries) share an L2 while the eight XCDs stream neighbouring
+// addresses.  With xch = g8 (one round) XCD x takes tiles [x*g8, (x+1)*g8).
+__device__ __forceinline__ long long xcd_tile(long long xch)
 {
     const long long b = blockIdx.x;
-    return (b % kXcds) * g8 + b / kXcds;
+    const long long q = b / kXcds;
+    return (q / xch) * (kXcds * xch) + (b % kXcds) * xch + q % xch;
 }
 
 // ---- 16-byte streaming loads through buffer resources ----------------------
@@ -447,7 +452,7 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
     __shared__ ReduceLds<T, S::kWaveCap, S::kBlockCap> L;
 
     const int tid = threadIdx.x;
-    const long long t = xcd_tile(a.g8);
+    const long long t = xcd_tile(a.xch);
     if (t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping
 
@@ -1080,7 +1085,7 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const long long t = (MODE == kFlatMemo && a.sched) ? sched_tile(a.sched, a.sched_cap, a.ntiles) : xcd_tile(a.g8);
+    const long long t = (MODE == kFlatMemo && a.sched) ? sched_tile(a.sched, a.sched_cap, a.ntiles) : xcd_tile(a.xch);
     if (t < 0 || t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping, or a spare schedule slot
     const int m = a.m, nnz = a.nnz;
@@ -1435,7 +1440,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const long long t = xcd_tile(a.g8);
+    const long long t = xcd_tile(a.xch);
     if (t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping
     const int m = a.m, nnz = a.nnz;
@@ -1746,7 +1751,7 @@ template <bool MERGE, int K, int LMAX, int SPAN_MAX>
 __global__ __launch_bounds__(kBS) void k_tile_desc(Args<double> a, int *__restrict__ out)
 {
     __shared__ int s_rows[2];
-    const long long t = xcd_tile(a.g8);
+    const long long t = xcd_tile(a.xch);
     if (t >= a.ntiles)
         return;
     uint32_t kb, ke;
@@ -1849,7 +1854,7 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const long long b = xcd_tile(a.g8);
+    const long long b = xcd_tile(a.xch);
     if (b >= a.ntiles)
         return;
     const int m = a.m;
@@ -2082,6 +2087,20 @@ inline unsigned grid_for(long long work, long long per_block, long long cap)
     return (unsigned)(g < 1 ? 1 : g);
 }
 
+// XCD chunks (see xcd_tile) for tiles of tile_nnz: chunks of about chunk_nnz
+// nnz, or one chunk of ceil(ntiles / 8) tiles per XCD when chunk_nnz is 0.
+// The rounds are balanced: every XCD gets the same number of chunks, of
+// ceil(g / rounds) tiles, so the last round does not fall on a few XCDs.
+void chunk_shape(long long ntiles, long long tile_nnz, long long chunk_nnz, long long &xch, long long &g8)
+{
+    const long long g = (ntiles + kXcds - 1) / kXcds;
+    long long target = chunk_nnz > 0 ? chunk_nnz / tile_nnz : g;
+    if (target < 1) target = 1;
+    const long long rounds = (g + target - 1) / target;
+    xch = (g + rounds - 1) / rounds;
+    g8 = rounds * xch;
+}
+
 template <typename T>
 Args<T> make_args(const pfk_spmv_args *a)
 {
@@ -2097,6 +2116,7 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.guess_spread = a->guess_spread;
     r.ntiles = a->ntiles;
     r.g8 = (a->ntiles + kXcds - 1) / kXcds;
+    r.xch = r.g8;
     r.tx = r.g8;
     r.tpw = 1;
     r.head = static_cast<acc_t<T> *>(a->head_slot);
@@ -2226,6 +2246,7 @@ template <typename T, int K>
 int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
 {
     Args<T> r = make_args<T>(a);
+    chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8);
     const long long grid = r.g8 * kXcds;
     if (a->row_aligned) {
         if (dbg)
@@ -2309,6 +2330,14 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream)
          : dtype == PF_F16 ? dispatch_flat<half_t>(a, stream) : PF_ERR_INVALID;
+}
+
+long long pfk_flat_grid(long long ntiles, int tile, long long chunk_nnz)
+{
+    if (ntiles < 1 || tile < 1) return 0;
+    long long xch = 0, g8 = 0;
+    chunk_shape(ntiles, tile, chunk_nnz, xch, g8);
+    return g8 * kXcds;
 }
 
 int pfk_flow_resident_waves(int dtype, long long *waves)

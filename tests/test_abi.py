@@ -86,12 +86,36 @@ def test_select_auto_banded_is_flat():
     assert i.variant == pf.FLAT and i.tile == 1024
     assert i.ntiles == -(-20963328 // 1024)
     assert i.row_aligned == 1 and i.needs_fixup == 0     # rows <= 256 nnz: tiles own whole rows
-    assert i.grid % 8 == 0 and i.grid >= i.ntiles and i.grid - 8 < i.ntiles
+    # tiles go to the XCDs in chunks of 2^15 nnz (32 tiles); the grid pads each XCD to whole chunks,
+    # fewer than 8 workgroups per round of chunks
+    assert i.chunk_nnz == 1 << 15
+    rounds = -(-(-(-i.ntiles // 8)) // 32)
+    assert i.grid % 8 == 0 and i.grid >= i.ntiles and i.grid - i.ntiles < 8 * rounds
     assert i.guess_spread == 64
     i32 = pf.select(s, "f32", "auto")
     assert i32.variant == pf.FLAT and i32.tile == 2048
     wide = pf.select(make_stats(4194304, 4194304 * 40, 60), "f64", "auto")   # rows up to 60 nnz: still FLAT
     assert wide.variant == pf.FLAT and wide.tile == 1024
+
+
+def test_chunk_rule_and_grid():
+    """Very short rows (under 4 nnz on average, C4's shape) keep one XCD chunk of an eighth of the tiles;
+    the grid then pads the tiles to a multiple of 8 only."""
+    c4 = pf.select(make_stats(20000000, 50000000, 30), "f64", "auto")
+    assert c4.variant == pf.FLAT and c4.row_aligned == 1 and c4.chunk_nnz == 0
+    assert c4.grid % 8 == 0 and c4.grid >= c4.ntiles and c4.grid - 8 < c4.ntiles
+    split = pf.select(make_stats(2000000, 16000000, 200000), "f64", "flat")
+    assert split.row_aligned == 0 and split.chunk_nnz == 1 << 15
+    assert pf.select(make_stats(2000000, 16000000, 200000), "f64", "prefree").chunk_nnz == 0
+    K = pf.klib()
+    for ntiles in (1, 7, 8, 9, 255, 20464, 24414):
+        for tile in (1024, 2048):
+            for chunk in (0, 1, tile, 1 << 15, 1 << 40):
+                grid = K.pfk_flat_grid(ntiles, tile, chunk)
+                g = -(-ntiles // 8)
+                per = g if chunk == 0 else max(1, chunk // tile)
+                rounds = -(-g // per)
+                assert grid % 8 == 0 and ntiles <= grid < ntiles + 8 * rounds, (ntiles, tile, chunk, grid)
 
 
 def test_select_auto_small_matrix():

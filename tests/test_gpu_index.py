@@ -57,13 +57,13 @@ def test_tile_descriptors_match_model(merged, tile, spread, run):
         assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
 
 
-@pytest.mark.parametrize("spread", [0, 64, 1000])
+@pytest.mark.parametrize("spread,chunk", [(0, 0), (64, 1 << 15), (1000, 3000)])
 @pytest.mark.parametrize("tile", [1024, 2048])
-def test_row_aligned_descriptors_match_model(tile, spread):
+def test_row_aligned_descriptors_match_model(tile, spread, chunk):
     """Row-aligned FLAT tiles (rows starting in the tile, whole): exact descriptors wherever no
     tile's last row reaches 256 or more nnz past the tile's nominal end (always so when rows hold at
     most 256 nnz, the planning rule); otherwise the kernel refuses (error flag), since its product
-    buffer holds K + 255 nnz."""
+    buffer holds K + 255 nnz.  Every tile reports once whatever the XCD chunk (slots start at -7)."""
     for name, rp in CASES:
         m, nnz = len(rp) - 1, int(rp[-1])
         if m == 0:
@@ -73,7 +73,7 @@ def test_row_aligned_descriptors_match_model(tile, spread):
         out = torch.full((8 * ntiles,), -7, dtype=torch.int32, device=DEV)
         err = torch.zeros(64, dtype=torch.int32, device=DEV)
         got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, False, out, err, guess_spread=spread,
-                                        row_aligned=True)
+                                        row_aligned=True, chunk_nnz=chunk)
         torch.cuda.synchronize()
         assert got_tiles == ntiles
         kb = np.arange(ntiles - 1, dtype=np.int64) * tile

@@ -210,6 +210,49 @@ def test_flat_row_aligned_and_split_tiles(tile, dtype):
         assert np.array_equal(ys[None][short], ref[short]), name
 
 
+CHUNKS = [0, 1, 3000, 1 << 15, 1 << 40]   # one chunk per XCD, one tile per chunk, ..., one round
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_flat_xcd_chunks_same_y(tile, dtype):
+    """FLAT tiles dealt to the XCDs in chunks of any size give the same y bit for bit, row-aligned
+    and split-row, on tile counts that fill no round of chunks evenly; y starts as NaN, so a tile
+    left out or computed twice shows."""
+    cases = [(name, rp, col, n) for name, rp, col, n in short_row_cases() if len(col) > 0]
+    rng = np.random.default_rng(41)
+    lens = rng.integers(0, 40, size=9001)                       # ragged rows, 180k nnz
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    col = rng.integers(0, 9001, size=int(rp[-1])).astype(np.int32)
+    cases.append(("ragged", rp, col, 9001))
+    for name, rp, col, n in cases:
+        rng = np.random.default_rng(len(col))
+        val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+        x = rng.uniform(-1, 1, n).astype(NP[dtype])
+        for ra in (None, 0):
+            ys = []
+            for chunk in CHUNKS:
+                y, info = gpu_spmv(rp, col, val, x, "flat", tile=tile, dtype=dtype, row_aligned=ra, chunk_nnz=chunk)
+                assert info["chunk_nnz"] == chunk and info["grid"] % 8 == 0 and info["grid"] >= info["ntiles"]
+                ys.append(y)
+            for chunk, y in zip(CHUNKS[1:], ys[1:]):
+                assert np.array_equal(y, ys[0], equal_nan=True), (name, ra, chunk)
+            assert_parity(rp, col, val, x, ys[0], dtype, what=f"{name}/ra={ra}")
+
+
+def test_chunk_setter_rejects():
+    from gpu_util import dev
+    rp, col, _ = pf.synth_csr(2, seed=3, scale_n=64, dtypes=())
+    d_rp, d_col = dev(rp), dev(col)
+    with pf.Plan(d_rp, d_col, len(rp) - 1, len(rp) - 1, len(col), "f64", "flat", 1024) as p:
+        assert p.info.chunk_nnz == 1 << 15                    # 5 nnz per row: chunks of 2^15 nnz
+        with pytest.raises(pf.PrefreeError):
+            p.set_chunk_nnz(-1)
+    with pf.Plan(d_rp, d_col, len(rp) - 1, len(rp) - 1, len(col), "f64", "adaptive", 0) as p:
+        with pytest.raises(pf.PrefreeError):
+            p.set_chunk_nnz(1 << 15)
+
+
 def test_row_aligned_refused_for_long_rows():
     import torch
     from gpu_util import dev
