@@ -1228,12 +1228,19 @@ struct RowsDesc {
 };
 
 // The tile's loads after its col / val: the overflow col / val, the x gathers
-// of the nominal range and of the overflow, then row_ptr[f0 .. f0 + cnt).  The
+// of the nominal range and of the overflow, and row_ptr[f0 .. f0 + cnt).  The
 // overflow loads and gathers are issued by every lane (an empty range or an
 // out-of-range offset reads nothing), so the compiler's wait counts in front
-// of the gathers are exact; the row_ptr loads skip whole waves past cnt and
-// come last, where a wait for all of them costs nothing.
-template <typename T, int K>
+// of the gathers are exact.  The row_ptr loads skip whole waves past cnt.
+//   EARLY_RP false: the row_ptr loads come last, where a wait for all of them
+//     costs nothing.
+//   EARLY_RP true (matrices of very short rows, where row_ptr is a third of
+//     the stream): they are issued before the gathers, so their latency runs
+//     alongside the col / val stream's; the wait in front of the gathers then
+//     also covers some of them (the compiler cannot count loads a wave may
+//     skip).  C4: 310.5 instead of 320.4 us (fp64), 224.3 instead of 227.9
+//     (fp32); on C2 it costs 0.5-0.7 us in fp32 / fp16, hence the split.
+template <typename T, int K, bool EARLY_RP>
 __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, const int (&c)[RowsShape<T, K>::kVPT][4],
                                            T (&xv)[RowsShape<T, K>::kVPT][4], T &ov, T &xo,
                                            int (&rr)[RowsShape<T, K>::kRpPer])
@@ -1246,6 +1253,19 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
     const __amdgpu_buffer_rsrc_t rvo = make_rsrc(a.val + ob, (long long)d.nov * (long long)sizeof(T));
     const int oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
     ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+    const __amdgpu_buffer_rsrc_t rrp = make_rsrc(a.rp + d.f0, (long long)d.cnt * 4);
+    const auto rp_loads = [&] {
+#pragma unroll
+        for (int q = 0; q < S::kRpPer; ++q) {
+            rr[q] = 0;
+            if (q * kBS + wave * kWave < d.cnt)
+                rr[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rrp, (tid + q * kBS) * 4, 0, 0);
+        }
+    };
+    if constexpr (EARLY_RP) {
+        rp_loads();
+        __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the gathers
+    }
     const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
 #pragma unroll
     for (int k = 0; k < S::kVPT; ++k) {
@@ -1257,13 +1277,7 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
         }
     }
     xo = buf_load(rx, tid < d.nov ? (uint32_t)oc * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
-    const __amdgpu_buffer_rsrc_t rrp = make_rsrc(a.rp + d.f0, (long long)d.cnt * 4);
-#pragma unroll
-    for (int q = 0; q < S::kRpPer; ++q) {
-        rr[q] = 0;
-        if (q * kBS + wave * kWave < d.cnt)
-            rr[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rrp, (tid + q * kBS) * 4, 0, 0);
-    }
+    if constexpr (!EARLY_RP) rp_loads();
 }
 
 // Products and row bounds of a row-aligned tile into LDS.
@@ -1433,9 +1447,10 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     // average): raised wave priority while the tile's loads are issued, so a
     // workgroup that has just started gets its memory streams going ahead of
     // the long per-row phase of older workgroups on the CU (C4: 320 instead of
-    // 332 us per call).  With longer rows it delays the older workgroups'
-    // stores instead (C2: 60.2 instead of 58.1 us), and even untaken it changes
-    // the code, hence a separate instantiation.
+    // 332 us per call), and the row_ptr loads issued before the gathers (see
+    // rows_loads).  With longer rows the priority delays the older
+    // workgroups' stores instead (C2: 60.2 instead of 58.1 us), and even
+    // untaken it changes the code, hence a separate instantiation.
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -1510,7 +1525,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     const RowsDesc d{kb, B0, f0, nr, nov, A, B, min(nr + 1, S::kRpCap)};
     T xv[VPT][4], ov, xo;
     int rr[S::kRpPer];
-    rows_loads<T, K>(a, d, c, xv, ov, xo, rr);
+    rows_loads<T, K, PRIO>(a, d, c, xv, ov, xo, rr);
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     rows_stage<T, K>(d, v, xv, ov, xo, rr, s_prod, s_rp);
     lds_sync();
