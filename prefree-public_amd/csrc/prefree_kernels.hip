@@ -110,11 +110,15 @@ constexpr int adaptive_lmax(int K) { return (K == 238 || K == 494) ? 16 : (K <= 
 // tiles, and in round r XCD x takes chunk 8r + x, so neighbouring rows (and
 // their x entries) share an L2 while the eight XCDs stream neighbouring
 // addresses.  With xch = g8 (one round) XCD x takes tiles [x*g8, (x+1)*g8).
+// The grid is under 2^32 workgroups, so the arithmetic is 32-bit (a 64-bit
+// divide is a software routine of about 200 instructions).
 __device__ __forceinline__ long long xcd_tile(long long xch)
 {
-    const long long b = blockIdx.x;
-    const long long q = b / kXcds;
-    return (q / xch) * (kXcds * xch) + (b % kXcds) * xch + q % xch;
+    const uint32_t b = blockIdx.x;
+    const uint32_t q = b / kXcds;
+    const uint32_t c = (uint32_t)xch;
+    const uint32_t r = q / c;
+    return (long long)r * (kXcds * (long long)c) + (long long)(b % kXcds) * c + (q - r * c);
 }
 
 // ---- 16-byte streaming loads through buffer resources ----------------------
@@ -1251,8 +1255,21 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
     const int ob = d.nov > 0 ? d.kb + K : 0;
     const __amdgpu_buffer_rsrc_t rco = make_rsrc(a.col + ob, (long long)d.nov * 4);
     const __amdgpu_buffer_rsrc_t rvo = make_rsrc(a.val + ob, (long long)d.nov * (long long)sizeof(T));
-    const int oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
-    ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+    // With one col vector per lane and the row_ptr loads last, a wave whose
+    // lanes hold no overflow nnz skips the three overflow loads (C2 fp64:
+    // 55.6 instead of 56.6 us): the wait before the gathers then also covers
+    // the val loads issued right after col, which arrive with it.  With more
+    // col vectors, or row_ptr loads ahead of the gathers, that wait would also
+    // cover later vectors' loads or the row_ptr loads (C2 fp32 +0.4, fp16
+    // +1.3, C4 fp64 +19 us), so every wave issues them.  ov, oc and xo are
+    // read only by lanes below nov.
+    constexpr bool kSkipOvf = S::kVPT == 1 && !EARLY_RP;
+    const bool ovw = !kSkipOvf || wave * kWave < d.nov;  // wave-uniform
+    int oc;
+    if (ovw) {
+        oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
+        ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+    }
     const __amdgpu_buffer_rsrc_t rrp = make_rsrc(a.rp + d.f0, (long long)d.cnt * 4);
     const auto rp_loads = [&] {
 #pragma unroll
@@ -1276,7 +1293,7 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
             xv[k][j] = buf_load(rx, use ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
         }
     }
-    xo = buf_load(rx, tid < d.nov ? (uint32_t)oc * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    if (ovw) xo = buf_load(rx, tid < d.nov ? (uint32_t)oc * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
     if constexpr (!EARLY_RP) rp_loads();
 }
 
