@@ -284,24 +284,27 @@ def x_window_cases():
     return out
 
 
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
 @pytest.mark.parametrize("tile", [1024, 2048])
-def test_flat_x_window_schedule_same_y(tile):
+def test_flat_x_window_schedule_same_y(tile, dtype):
     """Split-row FLAT with tiles dealt to XCDs by x window (recorded by the first call, used from the
     second) gives exactly the y of the positional mapping, on KAT and U[-1,1] inputs."""
     for name, rp, col, n in x_window_cases():
         for kat in (True, False):
             if kat:
-                val, x = oracle.initvec(len(col)), oracle.initvec(n)
+                val, x = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
             else:
                 rng = np.random.default_rng(len(col))
-                val, x = rng.uniform(-1, 1, len(col)), rng.uniform(-1, 1, n)
+                val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+                x = rng.uniform(-1, 1, n).astype(NP[dtype])
             ys = []
             for xw in (1, 0):
-                y, info = gpu_spmv(rp, col, val, x, "flat", tile=tile, row_aligned=0, x_windows=xw, repeat=3)
+                y, info = gpu_spmv(rp, col, val, x, "flat", tile=tile, dtype=dtype, row_aligned=0, x_windows=xw,
+                                   repeat=3)
                 assert info["x_windows"] == xw and info["row_aligned"] == 0
                 ys.append(y)
-            assert np.array_equal(ys[0], ys[1]), name
-            assert_parity(rp, col, val, x, ys[0], "f64", exact=kat and kat_exact_possible(rp, "f64"), what=name)
+            assert np.array_equal(ys[0], ys[1], equal_nan=True), name
+            assert_parity(rp, col, val, x, ys[0], dtype, exact=kat and kat_exact_possible(rp, dtype), what=name)
 
 
 def test_x_window_schedule_planning_rule():
