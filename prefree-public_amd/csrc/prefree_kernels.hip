@@ -132,6 +132,7 @@ __device__ __forceinline__ long long xcd_tile(long long xch)
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer resource, 32-bit elements
 constexpr int kAuxNt = 2;               // cache policy bit 1: non-temporal (streamed once)
+constexpr int kAuxDev = 16;             // cache policy bit 4 (sc1): device scope, written through to memory
 
 // Callers pass wave-uniform base and size.  readfirstlane states that to the
 // compiler, which otherwise may keep the descriptor in VGPRs and wrap every
@@ -1328,7 +1329,7 @@ __device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsS
 // product buffer and stored from there, so the staging costs no LDS of its own
 // (occupancy stays that of the product buffer).  The range check of the store
 // resource, exactly the tile's rows, drops the dwords past the last row.
-template <typename T, int K>
+template <typename T, int K, int YAUX>
 __device__ __forceinline__ void rows_sums_staged(const RowsDesc &d, T *s_prod, const int *s_rp,
                                                  RowsReduceLds<T, RowsShape<T, K>::kWaveCap,
                                                                RowsShape<T, K>::kBlockCap> &L,
@@ -1402,14 +1403,15 @@ __device__ __forceinline__ void rows_sums_staged(const RowsDesc &d, T *s_prod, c
     constexpr int kPer = 16 / (int)sizeof(T);
     const int n16 = (d.nr + kPer - 1) / kPer;
     for (int j = tid; j < n16; j += kBS)
-        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16, 0, kAuxNt);
+        __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4 *>(s_y + j * kPer), ry, j * 16, 0, YAUX);
 }
 
 // Row sums of a staged row-aligned tile into y.  Bounds come from LDS; a tile
 // with more rows than LDS holds (long runs of empty rows) reads the rest from
 // row_ptr in a separate branch, so the common path waits on LDS only and
 // leaves the y stores and any loads already issued for the next tile in flight.
-template <typename T, int K>
+// YAUX is the cache policy of the fp64 / fp32 16-byte y stores.
+template <typename T, int K, int YAUX>
 __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, acc_t<T> *s_prod,
                                             const int *s_rp,
                                             RowsReduceLds<acc_t<T>, RowsShape<T, K>::kWaveCap, RowsShape<T, K>::kBlockCap> &L)
@@ -1418,16 +1420,16 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
     using P = acc_t<T>;
     if (d.nr < S::kRpCap) {
         // y[f0 .. f0 + nr) through a resource over exactly those rows, written
-        // non-temporally: y is not read again here, and keeping it out of L2
-        // leaves room for x (C4: 345 instead of 377 us per call with 8-byte
-        // stores through L2).
+        // with the policy YAUX (fp64 / fp32) or non-temporally (fp16): y is not
+        // read again here, and keeping it out of L2 leaves room for x (C4: 345
+        // instead of 377 us per call with 8-byte stores through L2).
         const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f0, (long long)d.nr * (long long)sizeof(T));
         const auto bounds = [&](int i, int &ra, int &rb) {
             ra = s_rp[i];
             rb = s_rp[i + 1];
         };
         if constexpr (sizeof(T) >= 4) {
-            rows_sums_staged<T, K>(d, s_prod, s_rp, L, ry);
+            rows_sums_staged<T, K, YAUX>(d, s_prod, s_rp, L, ry);
         } else {
             // fp16: one 2-byte store per row.  The range check works on whole
             // dwords, so a 16-byte store ending in a half-covered dword would
@@ -1547,7 +1549,11 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     rows_stage<T, K>(d, v, xv, ov, xo, rr, s_prod, s_rp);
     lds_sync();
 
-    rows_reduce<T, K>(a, d, s_prod, s_rp, L);
+    // y stores: device scope (written through to memory) in general, C2:
+    // 55.25 instead of 55.6 us (fp64), 36.0 instead of 36.5 (fp32);
+    // non-temporal in the short-row mode, where y is a sixth of the bytes and
+    // device scope took C4 from 320 to 357 us.
+    rows_reduce<T, K, PRIO ? kAuxNt : kAuxDev>(a, d, s_prod, s_rp, L);
 }
 
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
