@@ -1410,7 +1410,7 @@ __device__ __forceinline__ void rows_sums_staged(const RowsDesc &d, T *s_prod, c
 // with more rows than LDS holds (long runs of empty rows) reads the rest from
 // row_ptr in a separate branch, so the common path waits on LDS only and
 // leaves the y stores and any loads already issued for the next tile in flight.
-// YAUX is the cache policy of the fp64 / fp32 16-byte y stores.
+// YAUX is the cache policy of the y stores.
 template <typename T, int K, int YAUX>
 __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d, acc_t<T> *s_prod,
                                             const int *s_rp,
@@ -1420,9 +1420,9 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
     using P = acc_t<T>;
     if (d.nr < S::kRpCap) {
         // y[f0 .. f0 + nr) through a resource over exactly those rows, written
-        // with the policy YAUX (fp64 / fp32) or non-temporally (fp16): y is not
-        // read again here, and keeping it out of L2 leaves room for x (C4: 345
-        // instead of 377 us per call with 8-byte stores through L2).
+        // with the policy YAUX, not through L2: y is not read again here, and
+        // keeping it out of L2 leaves room for x (C4: 345 instead of 377 us per
+        // call with 8-byte stores through L2).
         const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f0, (long long)d.nr * (long long)sizeof(T));
         const auto bounds = [&](int i, int &ra, int &rb) {
             ra = s_rp[i];
@@ -1435,7 +1435,7 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
             // dwords, so a 16-byte store ending in a half-covered dword would
             // drop the tile's last row.
             reduce_tile(s_prod, L, d.kb, d.A, d.B, d.nr, bounds, [&](int i, P s) {
-                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, T(s)), ry, i * 2, 0, kAuxNt);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, T(s)), ry, i * 2, 0, YAUX);
             });
         }
     } else {  // more rows than LDS holds: any number, up to m
@@ -1550,9 +1550,9 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     lds_sync();
 
     // y stores: device scope (written through to memory) in general, C2:
-    // 55.25 instead of 55.6 us (fp64), 36.0 instead of 36.5 (fp32);
-    // non-temporal in the short-row mode, where y is a sixth of the bytes and
-    // device scope took C4 from 320 to 357 us.
+    // 55.25 instead of 55.6 us (fp64), 36.0 instead of 36.5 (fp32), 31.9
+    // instead of 32.55 (fp16); non-temporal in the short-row mode, where y is
+    // a sixth of the bytes and device scope took C4 from 320 to 357 us.
     rows_reduce<T, K, PRIO ? kAuxNt : kAuxDev>(a, d, s_prod, s_rp, L);
 }
 
