@@ -63,6 +63,10 @@ def edge_cases(seed=7):
     add("power_law_mix", list(pl), 30000)
     add("mixed_dense", list(np.where(rng.random(2000) < 0.005, rng.integers(3000, 9000, size=2000),
                                      rng.integers(8, 65, size=2000))), 10000)
+    # Rows of up to 256 nnz (row-aligned FLAT) whose last row runs 0..255 nnz past a tile's end: the
+    # overflow reaches every wave of the workgroup, not only the first 64 lanes.
+    add("rows_of_255", [255] * 160, 3000)
+    add("rows_65_to_256", list(rng.integers(65, 257, size=300)), 4000)
     return out
 
 
