@@ -67,6 +67,8 @@ def edge_cases(seed=7):
     # overflow reaches every wave of the workgroup, not only the first 64 lanes.
     add("rows_of_255", [255] * 160, 3000)
     add("rows_65_to_256", list(rng.integers(65, 257, size=300)), 4000)
+    # The same overflows under 4 nnz per row on average (the row-aligned kernel's short-row mode).
+    add("sparse_long_rows", list(np.where(rng.random(20000) < 0.02, rng.integers(65, 257, size=20000), 0)), 20000)
     return out
 
 
