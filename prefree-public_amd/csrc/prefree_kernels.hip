@@ -1234,9 +1234,10 @@ struct RowsDesc {
 
 // The tile's loads after its col / val: the overflow col / val, the x gathers
 // of the nominal range and of the overflow, and row_ptr[f0 .. f0 + cnt).  The
-// overflow loads and gathers are issued by every lane (an empty range or an
-// out-of-range offset reads nothing), so the compiler's wait counts in front
-// of the gathers are exact.  The row_ptr loads skip whole waves past cnt.
+// gathers are issued by every lane (an out-of-range offset reads nothing), and
+// so are the overflow loads except in the case below, so the compiler's wait
+// counts in front of the gathers are exact.  The row_ptr loads skip whole
+// waves past cnt.
 //   EARLY_RP false: the row_ptr loads come last, where a wait for all of them
 //     costs nothing.
 //   EARLY_RP true (matrices of very short rows, where row_ptr is a third of
