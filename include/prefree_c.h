@@ -137,7 +137,8 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).
- * val/x/y are double* for PF_F64 and float* for PF_F32.  Calls that share one
+ * val/x/y are double* for PF_F64, float* for PF_F32 and IEEE binary16 (2 bytes
+ * each) for PF_F16.  Calls that share one
  * plan must be ordered on one stream (the plan's workspace is reused). */
 int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val,
                     const void *d_x, void *d_y, void *stream);
