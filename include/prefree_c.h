@@ -169,7 +169,7 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
 
 /* Size-class table for PF_AUTO, as written by the offline tuner
  * (prefree-public_amd/tune/autotune.py).  Text, one row per line:
- *   <class> <nnz_upper | -1> <f64|f32> <adaptive|flat|prefree> <tile> <run_tiles | 0> <keep_cached>
+ *   <class> <nnz_upper | -1> <f64|f32|f16> <adaptive|flat|prefree> <tile> <run_tiles | 0> <keep_cached>
  * The first row whose dtype matches and whose bound exceeds the matrix's nnz
  * decides (run 0: the built-in run rule).  NULL clears the table.  Without a
  * call, $PREFREE_TUNING_TABLE is read once if set.  Plans made before the call

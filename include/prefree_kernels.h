@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-/* Arguments of one SpMV launch.  val/x/y are double* or float* by dtype. */
+/* Arguments of one SpMV launch.  val/x/y are double*, float* or IEEE binary16 by dtype. */
 typedef struct pfk_spmv_args {
     const int *row_ptr;
     const int *col;
