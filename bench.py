@@ -125,7 +125,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "the sharded design is described in DESIGN.md, no multi-GPU figure is produced.", file=sys.stderr)
+              "across GPUs the matrix would be split into row blocks of equal nnz, each GPU holding the x entries "
+              "its columns touch; no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

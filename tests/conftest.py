@@ -42,4 +42,4 @@ _load_pkg()
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X; run with -m gpu on the GPU box")
+    config.addinivalue_line("markers", "gpu: needs an MI355X; run with -m gpu on a machine that has one")
