@@ -69,6 +69,17 @@ def traffic_from_profiles(key):
         return None
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(rp, col, val, x, seconds, nnz):
     sys.path.insert(0, REPO)
     import numpy as np
@@ -79,18 +90,22 @@ def cpu_baseline(rp, col, val, x, seconds, nnz):
     if f16:  # the fp16 values widened to fp64: the sums this library's fp16 result is rounded from
         val, x = val.astype(np.float64), x.astype(np.float64)
     y = np.zeros(len(rp) - 1, dtype=val.dtype)
-    oracle.spmv_omp(rp, col, val, x, y=y)  # warm-up (page-in)
+    for _ in range(3):                      # warm-up (page-in, clocks)
+        oracle.spmv_omp(rp, col, val, x, y=y)
     reps, t0 = 0, time.perf_counter()
     while True:
         y[:] = 0
         oracle.spmv_omp(rp, col, val, x, y=y)
         reps += 1
         el = time.perf_counter() - t0
-        if (el >= seconds and reps >= 3) or reps >= 100000:
+        if (el >= seconds and reps >= 10) or reps >= 100000:
             break
     ms = el * 1e3 / reps
+    m, n, vb = len(rp) - 1, len(x), val.dtype.itemsize
+    bytes_eff = (nnz + m + n) * vb + nnz * 4 + (m + 1) * 4          # test/test_cdspmv.cpp:305, on the data timed
     return {"value": round(2.0 * nnz / (ms * 1e6), 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "ms_per_spmv": round(ms, 4),
+            "ms_per_spmv": round(ms, 4), "gbps_effective": round(bytes_eff / (ms * 1e6), 1),
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
             "sample": f"full matrix, {reps} SpMVs in {el:.1f} s (OpenMP restatement of spmv_serial, "
                       f"test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads"
                       + (", on the fp16 values widened to fp64" if f16 else "") + ")"}, y
