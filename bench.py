@@ -317,6 +317,9 @@ def main():
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profiles(key),
                      "kernel": kernel_name(info),
                      "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
+                     # the measured HBM bytes of the step kernel (profiles/traffic.json) over its time
+                     "traffic_gbps": (round(traffic_from_profiles(key) / (ms_kernel * 1e6), 1)
+                                      if traffic_from_profiles(key) else None),
                      "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
         "cold": ({"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
