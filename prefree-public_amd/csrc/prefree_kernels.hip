@@ -1,34 +1,48 @@
 // prefree_kernels.hip — gfx950 CSR SpMV kernels and the thin extern "C" HIP
 // layer declared in include/prefree_kernels.h.
 //
-// Three kernel families compute y = A·x (y overwritten):
+// The kernels compute y = A·x (y overwritten).  None needs a pre-pass: every
+// workgroup (or wave) finds its rows inside the SpMV kernel, by a wave search
+// of row_ptr (device_common.hpp: wave_search_lt) or, from a plan's second call
+// on, by reading the rows its first call found.
 //
-//  * k_tiles<MERGE=true>   (PF_ADAPTIVE)  CSR-adaptive row blocks found on the fly.
-//    Tile t owns the keys [t*K, (t+1)*K) of the merged sequence in which row r
-//    occupies keys row_ptr[r]+r .. row_ptr[r+1]+r (its nnz, then one key for
-//    its end), so a tile holds at most K rows+nnz whatever the row lengths.
-//    A row whose first key lies in the tile is reduced there whole, unless it
-//    is longer than LMAX; such long rows are cut at tile edges and their
-//    partials combined by k_fixup in tile order (deterministic, no atomics).
-//  * k_tiles<MERGE=false>  (PF_FLAT)  the same machinery on plain nnz tiles
-//    with LMAX = 0: every row crossing a tile edge is cut and combined.
-//  * k_prefree             (PF_PREFREE)  the reference algorithm
+//  * k_rows<T, K, MODE, PRIO>  (PF_FLAT, K = 1024 / 2048 nnz; the default when
+//    no row holds more than 256 nnz)  Tile t owns the rows starting in its nnz
+//    range, whole: one launch per step, no split rows.
+//  * k_flat<T, K, MODE>  (PF_FLAT 1024 / 2048, rows longer than 256 nnz)  The
+//    same nnz tiles with rows cut at tile edges; k_fixup combines the pieces.
+//    With the x-window schedule (sched_tile) tiles go to the XCDs by the part
+//    of x they start in.
+//  * k_flow<T>  (PF_FLAT 256)  A wave walks a run of 256-nnz tiles and carries
+//    a row's partial sum across their edges.
+//  * k_tiles<T, false, 4096>  (PF_FLAT 4096)  The first FLAT kernel: both tile
+//    edges searched on every call.
+//  * k_wave<T, K, LMAX, ...>  (PF_ADAPTIVE)  CSR-adaptive row blocks found on
+//    the fly: tile t owns the keys [t*K, (t+1)*K) of the merged sequence in
+//    which row r occupies keys row_ptr[r]+r .. row_ptr[r+1]+r, so a tile holds
+//    at most K rows+nnz; rows longer than LMAX are cut at tile edges.  Each
+//    wave64 walks a run of tiles with three in flight.
+//  * k_prefree<T, P>  (PF_PREFREE)  The reference algorithm
 //    (src/spmv_kernel/preFreeSpMV.cu:407-483): 128*P-nnz tiles, reduction
-//    ladder "code 3", atomicAdd on tile-boundary rows over a zeroed y.  Its
-//    first-row-per-tile map (the pre-pass pre_start_rowPerTile, :3-28) is
-//    computed inside the kernel by a wave-cooperative search of row_ptr.
+//    ladder "code 3", atomicAdd on tile-boundary rows over a zeroed y, its
+//    first-row-per-tile map (the pre-pass, :3-28) searched inside the kernel.
+//  * k_fixup<T, MERGE>  Split-row partials combined in tile order
+//    (deterministic, no atomics).
+//  * k_row_stats, k_col_check  Row statistics and the column range check, run
+//    once at planning; k_tile_desc / k_prefree_rows  descriptors for tests.
 //
-// No kernel needs a pre-pass: every workgroup finds its rows by searching
-// row_ptr (device_common.hpp: wave_search_lt).
-//
-// Data path of k_tiles (one workgroup = 4 wave64s = one tile):
-//   1. waves 0 and 1 search row_ptr for the rows at the two tile edges;
-//   2. col / val of the tile's nnz range stream in as 16-byte non-temporal
-//      loads (dwordx4: 4 col, 2 fp64 or 4 fp32 values per lane), x is gathered
-//      with ordinary loads so it stays in L2 / MALL; products go to LDS;
-//   3. rows of <= 16 products are summed by one lane each in nnz order
-//      (the exact order of the reference spmv_serial, test/test_cdspmv.cpp:4-20),
-//      rows of <= 512 by a wave (DPP sum), longer ones by the whole workgroup.
+// Shared data path of the FLAT tiles (one workgroup = 4 wave64s = one tile):
+//   1. col / val of the tile's nnz range stream in as 16-byte non-temporal
+//      loads before its rows are known; tiles go to the XCDs in chunks of
+//      neighbouring tiles (xcd_tile);
+//   2. x is gathered with ordinary loads, so it stays in L2 / MALL; products
+//      go to LDS;
+//   3. rows of <= 16 products are summed by one lane each in nnz order (the
+//      order of the reference spmv_serial, test/test_cdspmv.cpp:4-20), rows of
+//      <= 512 by a wave (DPP sum), longer ones by the whole workgroup;
+//   4. k_rows stages the sums in LDS and writes them as 16-byte stores of
+//      consecutive rows; k_flat writes each row's sum, or its head / tail
+//      partial, directly.
 #include "../../include/prefree_c.h"
 #include "../../include/prefree_kernels.h"
 #include "device_common.hpp"
