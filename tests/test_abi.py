@@ -98,6 +98,16 @@ def test_select_auto_banded_is_flat():
     assert wide.variant == pf.FLAT and wide.tile == 1024
 
 
+def test_chunk_rule_boundary():
+    """Chunks of 2^15 nnz from 4 nnz per row on average; below that, one chunk per XCD (the same bound
+    that selects the row-aligned kernel's short-row mode)."""
+    m = 1000000
+    assert pf.select(make_stats(m, 4 * m - 1, 20), "f64", "flat").chunk_nnz == 0
+    assert pf.select(make_stats(m, 4 * m, 20), "f64", "flat").chunk_nnz == 1 << 15
+    for dt in ("f32", "f16"):
+        assert pf.select(make_stats(m, 4 * m, 20), dt, "flat").chunk_nnz == 1 << 15
+
+
 def test_chunk_rule_and_grid():
     """Very short rows (under 4 nnz on average, C4's shape) keep one XCD chunk of an eighth of the tiles;
     the grid then pads the tiles to a multiple of 8 only."""

@@ -84,6 +84,9 @@ def test_autotune_picks_a_correct_faster_configuration(cfg, scale):
         assert (info.variant, info.tile) == (r["variant"], r["tile"])
         if info.variant == pf.ADAPTIVE:
             assert info.run_tiles == r["run_tiles"]
+        if info.variant == pf.FLAT and info.tile in (1024, 2048):   # XCD chunk: the plan's rule or a tried size
+            assert info.chunk_nnz == r["chunk_nnz"]
+            assert r["chunk_nnz"] in (0, 1 << 13, 1 << 15, 1 << 17)
         assert_parity(rp, col, v["f64"], x, y.cpu().numpy(), "f64", what=f"C{cfg} autotune y")
         y2 = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
         p.execute(*d, y2)
