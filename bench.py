@@ -1,27 +1,42 @@
 #!/usr/bin/env python3
-"""bench.py — CSR SpMV throughput on one MI355X.
+"""bench.py — CSR SpMV throughput on one MI355X, every benchmark configuration.
 
 One step = one y = A·x (pf_plan_execute) over the whole matrix, inputs already
-resident in HBM.  Default workload: C2, the 5-point Laplacian on a 2048x2048
-grid (n = 4,194,304, nnz = 20,963,328, fp64) — configs[1] of BASELINE.json,
-the single-GPU configuration the metric is quoted on.  --config 1..5 selects
-the other configurations (C4 also in fp32 with --dtype f32).
+resident in HBM.  The headline (`value`, `roofline`, `cpu_baseline`) is C5, the
+largest single-GPU configuration of BASELINE.json (mixed dense rows, n = 10^6,
+about 316M nnz, fp64); `configs` holds the same record for C1, C2, C3, C4,
+C4 in fp32 and C5.  --config N measures configuration N alone (and makes it
+the headline).
 
-Prints ONE JSON line.  `value` is GFLOP/s (2*nnz per step) from the host clock
-around exactly --steps back-to-back steps, bracketed by device
-synchronisation.  `roofline.achieved` is the effective-byte model of the
-reference harness (test/test_cdspmv.cpp:305: nnz*(val+4) + (rows+cols)*val +
-(rows+1)*4) divided by the kernel time per step measured with HIP events on
-the launch stream.  `cold` repeats the measurement with a 1 GiB write between
-steps so that no part of the matrix is served from the 256 MB MALL.
-`cpu_baseline` times the OpenMP restatement of the reference's spmv_serial
-(oracle/, all host cores) on the same matrix.
+Per configuration:
+  * hot      `steps` back-to-back steps.  `ms` is the host clock around them,
+             bracketed by device synchronisation; `kernel_ms` the HIP events on
+             the launch stream (the roofline's time base); a median of 40
+             event-timed batches when steps are launched one by one.
+  * rotated  the same steps alternating between enough device copies of the
+             whole working set (row_ptr, col, val, x, y) to exceed 768 MB, so a
+             step cannot find the previous step's lines in the 256 MB MALL.
+  * cold     a 1 GiB write before each step (evicts L2 and MALL; the flush's
+             own write-back overlaps the step's start).
+  * search   a plan that finds every tile's rows by searching row_ptr in the
+             kernel on every call, instead of reading the rows its first call
+             recorded (pf_plan_set_remember_rows(plan, 0)).
+  * cpu_baseline  the OpenMP restatement of the reference's spmv_serial
+             (oracle/, all host cores) on the same matrix, and `parity`, the
+             north-star row error of the GPU y against it.
+`roofline.achieved` is the reference harness's effective-byte model
+(test/test_cdspmv.cpp:305: nnz*(val+4) + (rows+cols)*val + (rows+1)*4) over
+`kernel_ms`; `roofline.traffic` the HBM bytes per step measured by rocprofv3
+(profiles/traffic.json) when committed for that plan.
+
+Prints ONE JSON line.
 """
 from __future__ import annotations
 
 import argparse
 import importlib.util
 import json
+import math
 import os
 import sys
 import time
@@ -37,6 +52,22 @@ WORKLOADS = {
     4: "C4 very sparse n=20,000,000 (Poisson 2.5, banded +-4096, 10% outliers)",
     5: "C5 mixed n=1,000,000 (0.1% dense rows of 50k-500k nnz)",
 }
+VALUES = {
+    1: "val, x ~ U[-1,1]",
+    2: "val 4 on the diagonal, -1 off it; x ~ U[-1,1]",
+    3: "val, x ~ U[-1,1]",
+    4: "val, x ~ U[-1,1]",
+    5: "val, x ~ U[-1,1]",
+}
+ALL_CONFIGS = [(1, "f64"), (2, "f64"), (3, "f64"), (4, "f64"), (4, "f32"), (5, "f64")]
+HEADLINE = (5, "f64")
+TOL = {"f64": 1e-12, "f32": 1e-5, "f16": 1e-3}
+ROTATE_BYTES = 768 << 20     # rotated copies together exceed 3x the 256 MB MALL
+ROTATE_MAX_COPIES = 1024
+
+
+def cfg_name(cfg, dt):
+    return f"C{cfg}" + ("" if dt == "f64" else f"_{dt}")
 
 
 def kernel_name(info):
@@ -81,6 +112,8 @@ def cpu_model():
 
 
 def cpu_baseline(rp, col, val, x, seconds, nnz):
+    """The OpenMP oracle timed on the host cores: 3 warm-up runs, then runs until
+    `seconds` have passed and at least 10 were made.  Returns (record, y)."""
     sys.path.insert(0, REPO)
     import numpy as np
     import oracle
@@ -106,17 +139,282 @@ def cpu_baseline(rp, col, val, x, seconds, nnz):
     return {"value": round(2.0 * nnz / (ms * 1e6), 3), "unit": "GFLOP/s", "cores": threads, "kind": "port",
             "ms_per_spmv": round(ms, 4), "gbps_effective": round(bytes_eff / (ms * 1e6), 1),
             "cpu_model": cpu_model(), "nproc": os.cpu_count(),
-            "sample": f"full matrix, {reps} SpMVs in {el:.1f} s (OpenMP restatement of spmv_serial, "
-                      f"test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads"
+            "sample": f"full matrix, {reps} SpMVs in {el:.1f} s after 3 warm-up SpMVs (OpenMP restatement of "
+                      f"spmv_serial, test/test_cdspmv.cpp:4-20, nnz-balanced row chunks, {threads} threads"
                       + (", on the fp16 values widened to fp64" if f16 else "") + ")"}, y
+
+
+class Stepper:
+    """Times `steps` calls of step(i) on `stream`: host clock and HIP events, eagerly
+    (with 40 event-timed batches for a median) or as one captured HIP graph."""
+
+    def __init__(self, torch, stream, use_graph):
+        self.torch, self.stream, self.use_graph = torch, stream, use_graph
+
+    def run(self, step, steps):
+        torch, stream = self.torch, self.stream
+        graph = None
+        if self.use_graph:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(steps):
+                    step(i, torch.cuda.current_stream())
+            torch.cuda.synchronize()
+            graph.replay()                   # untimed replay: the graph's first run
+            torch.cuda.synchronize()
+        n_batch = 0 if graph is not None else min(40, steps)
+        bounds = [round(j * steps / n_batch) for j in range(n_batch + 1)] if n_batch else []
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        marks = ([e0] + [torch.cuda.Event(enable_timing=True) for _ in range(n_batch - 1)] + [e1]) if n_batch else []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            k = 1
+            for i in range(steps):
+                if k < n_batch and i == bounds[k]:
+                    marks[k].record(stream)
+                    k += 1
+                step(i, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        host_ms = (t1 - t0) * 1e3 / steps
+        ev_ms = e0.elapsed_time(e1) / steps
+        median = None
+        if n_batch:
+            import numpy as np
+            per = [marks[j].elapsed_time(marks[j + 1]) / (bounds[j + 1] - bounds[j]) for j in range(n_batch)]
+            median = float(np.median(per))
+        desc = (f"median of {n_batch} event-timed batches of the steps, launched one by one" if n_batch
+                else "no median: the steps ran as one captured HIP graph replay")
+        del graph
+        return host_ms, ev_ms, median, desc
+
+
+def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
+    """One configuration: every leg of the module docstring.  Returns its record."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    vb = {"f64": 8, "f32": 4, "f16": 2}[dt]
+    tdt = {"f64": torch.float64, "f32": torch.float32, "f16": torch.float16}[dt]
+    legs = set(args.legs.split(","))
+
+    rp, col, vals = pf.synth_csr(cfg, seed=args.seed, dtypes=(dt,))
+    val = vals[dt]
+    m = len(rp) - 1
+    n = m
+    nnz = len(col)
+    x = pf.synth_x(cfg, n, seed=args.seed, dtypes=(dt,))[dt]
+    bytes_eff = (nnz + m + n) * vb + nnz * 4 + (m + 1) * 4          # test/test_cdspmv.cpp:305
+    bytes_gather = (2 * nnz + m) * vb + nnz * 4 + (m + 1) * 4       # test/test_cdspmv.cpp:306
+    flops = 2.0 * nnz
+
+    stream = torch.cuda.current_stream()
+    d_rp = torch.from_numpy(rp).to(dev)
+    d_col = torch.from_numpy(col).to(dev)
+    d_val = torch.from_numpy(val).to(dev)
+    d_x = torch.from_numpy(x).to(dev)
+    d_y = torch.full((m,), float("nan"), dtype=tdt, device=dev)
+    torch.cuda.synchronize()
+
+    def make_plan():
+        p = pf.Plan(d_rp, d_col, m, n, nnz, dt, args.variant, args.tile, stream=stream)
+        if args.x_windows >= 0:
+            p.set_x_windows(args.x_windows)
+        if args.chunk_nnz >= 0:
+            p.set_chunk_nnz(args.chunk_nnz)
+        return p
+
+    t_plan = time.perf_counter()
+    plan = make_plan()
+    t_plan = (time.perf_counter() - t_plan) * 1e3
+    info = plan.info.as_dict()
+    deterministic = info["variant_name"] != "prefree"   # PREFREE adds tile-boundary rows with atomics
+
+    # Warm-up (eager), then the launch mode: a captured graph when a step is
+    # launch-bound (under 20 us), otherwise launches one by one.
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    w0.record(stream)
+    for _ in range(max(1, warmup)):
+        plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=stream)
+    w1.record(stream)
+    torch.cuda.synchronize()
+    warm_us = w0.elapsed_time(w1) * 1e3 / max(1, warmup)
+    plan.check(stream=stream)
+    y_ref = d_y.clone()
+    use_graph = args.launch == "graph" or (args.launch == "auto" and warm_us < 20.0)
+    st = Stepper(torch, stream, use_graph)
+
+    def hot_step(i, s):
+        plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=s)
+
+    d_y.fill_(float("nan"))
+    host_ms, ev_ms, median, median_desc = st.run(hot_step, steps)
+    plan.check(stream=stream)
+    same_hot = bool(torch.equal(d_y, y_ref)) if deterministic else None
+    gbs = bytes_eff / (ev_ms * 1e6)
+    key = f"C{cfg}-{dt}-{info['variant_name']}-{info['tile']}" + (
+        f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
+        "-rows" if info["row_aligned"] else "")
+    traffic = traffic_from_profiles(key)
+    rec = {
+        "workload": WORKLOADS[cfg] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
+        "cfg": f"C{cfg}", "dtype": dt, "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
+        "values": VALUES[cfg],
+        "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
+        "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
+        "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
+        "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
+        "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3),
+        "steps": steps, "warmup": warmup,
+        "launch": ("one captured HIP graph of the timed steps" if use_graph else "eager launches from Python")
+                  + f"; eager warm-up step {warm_us:.1f} us",
+        "ms": round(host_ms, 6), "kernel_ms": round(ev_ms, 6),
+        "kernel_ms_median": round(median, 6) if median is not None else None, "median_of": median_desc,
+        "gflops": round(flops / (host_ms * 1e6), 3),
+        "gbps_effective": round(gbs, 1), "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
+        "bytes_model": {"effective": bytes_eff, "gather": bytes_gather, "source": "test/test_cdspmv.cpp:305-306"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernel_name(info),
+                     "launch_ms": round(ev_ms, 6), "algorithmic_bytes": bytes_eff,
+                     "traffic_gbps": round(traffic / (ev_ms * 1e6), 1) if traffic else None,
+                     "traffic_key": key,
+                     "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
+                              if info["needs_fixup"] else "step = one tile-kernel launch")},
+    }
+
+    # Rotated copies of the whole working set: no step finds its matrix in the MALL.
+    if "rotated" in legs:
+        copies = max(2, min(ROTATE_MAX_COPIES, math.ceil(ROTATE_BYTES / bytes_eff)))
+        bufs = [(d_rp, d_col, d_val, d_x, d_y)]
+        for _ in range(copies - 1):
+            bufs.append((d_rp.clone(), d_col.clone(), d_val.clone(), d_x.clone(),
+                         torch.full((m,), float("nan"), dtype=tdt, device=dev)))
+        torch.cuda.synchronize()
+
+        def rot_step(i, s):
+            b = bufs[i % copies]
+            plan.execute(b[0], b[1], b[2], b[3], b[4], stream=s)
+
+        for i in range(copies):                 # every copy once, untimed
+            rot_step(i, stream)
+        r_host, r_ev, r_med, _ = st.run(rot_step, max(steps, copies))
+        plan.check(stream=stream)
+        same_rot = all(bool(torch.equal(b[4], y_ref)) for b in bufs[1:]) if deterministic else None
+        rec["rotated"] = {"ms": round(r_host, 6), "kernel_ms": round(r_ev, 6),
+                          "kernel_ms_median": round(r_med, 6) if r_med is not None else None,
+                          "steps": max(steps, copies), "copies": copies,
+                          "working_set_bytes": copies * bytes_eff,
+                          "gbps_effective": round(bytes_eff / (r_ev * 1e6), 1),
+                          "frac": round(bytes_eff / (r_ev * 1e6) / PEAK_HBM_GBS, 4),
+                          "y_equal_to_hot": same_rot}
+        del bufs
+        torch.cuda.synchronize()
+
+    # Cold: a 1 GiB write between steps evicts L2 and MALL.
+    if "cold" in legs and args.cold_steps > 0:
+        flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        cold_ms = 0.0
+        c0 = torch.cuda.Event(enable_timing=True)
+        c1 = torch.cuda.Event(enable_timing=True)
+        for _ in range(args.cold_steps):
+            flush.zero_()
+            c0.record(stream)
+            plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=stream)
+            c1.record(stream)
+            c1.synchronize()
+            cold_ms += c0.elapsed_time(c1)
+        cold_ms /= args.cold_steps
+        del flush
+        rec["cold"] = {"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e6), 1),
+                       "frac": round(bytes_eff / (cold_ms * 1e6) / PEAK_HBM_GBS, 4),
+                       "steps": args.cold_steps, "flush": "1 GiB write before each step"}
+
+    # Rows searched inside the kernel on every call (no recorded row map).
+    if "search" in legs:
+        sp = make_plan()
+        sp.set_remember_rows(False)
+        d_ys = torch.full((m,), float("nan"), dtype=tdt, device=dev)
+        for _ in range(max(1, min(warmup, 50))):
+            sp.execute(d_rp, d_col, d_val, d_x, d_ys, stream=stream)
+
+        def search_step(i, s):
+            sp.execute(d_rp, d_col, d_val, d_x, d_ys, stream=s)
+
+        s_host, s_ev, s_med, _ = st.run(search_step, steps)
+        sp.check(stream=stream)
+        rec["search"] = {"ms": round(s_host, 6), "kernel_ms": round(s_ev, 6),
+                         "kernel_ms_median": round(s_med, 6) if s_med is not None else None,
+                         "vs_recorded_rows": round(s_ev / ev_ms, 4),
+                         "gbps_effective": round(bytes_eff / (s_ev * 1e6), 1),
+                         "y_equal_to_hot": bool(torch.equal(d_ys, y_ref)) if deterministic else None,
+                         "what": "every call searches row_ptr for each tile's rows inside the tile kernel"}
+        sp.close()
+        del d_ys
+
+    # The drop-in boundary (preFreeSpMV) takes host buffers: one SpMV including
+    # the host->device copies of the CSR and x, planning and the copy of y back.
+    if "host" in legs:
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        h_rp = torch.from_numpy(rp).to(dev)
+        h_col = torch.from_numpy(col).to(dev)
+        h_val = torch.from_numpy(val).to(dev)
+        h_x = torch.from_numpy(x).to(dev)
+        h_y = torch.empty(m, dtype=tdt, device=dev)
+        pf.spmv(h_rp, h_col, h_val, h_x, h_y, m, n, nnz, dt, args.variant, stream=stream)
+        y_host = h_y.cpu()
+        pcie_ms = (time.perf_counter() - h0) * 1e3
+        del h_rp, h_col, h_val, h_x, h_y, y_host
+        rec["host_buffers"] = {"ms": round(pcie_ms, 3), "gflops": round(flops / (pcie_ms * 1e6), 3),
+                               "what": "one SpMV from pageable host arrays: copies in, plan, execute, copy of y out"}
+
+    rec["y_equal_to_warmup"] = same_hot
+    y_gpu = d_y.cpu().numpy()
+    plan.close()
+    del d_rp, d_col, d_val, d_x, d_y, y_ref
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    if want_cpu:
+        import oracle
+        cpu, y_cpu = cpu_baseline(rp, col, val, x, args.cpu_seconds, nnz)
+        if dt == "f16":  # against the fp64 sums of the same fp16 data: one binary16 rounding per row,
+            # 2^-11 relative or, for a subnormal result, 2^-25 absolute (allowed for as 2^-24)
+            den = oracle.spmv_serial(rp, col, np.abs(val.astype(np.float64)), np.abs(x.astype(np.float64)))
+            dev_ = np.abs(y_gpu.astype(np.float64) - y_cpu)
+            zero_bad = int(np.count_nonzero((den == 0) & (y_gpu != 0)))
+            nz = den > 0
+            err = float((np.maximum(dev_[nz] - 2.0 ** -24, 0) / den[nz]).max()) if nz.any() else 0.0
+        else:
+            err, zero_bad, _ = oracle.rownorm_maxerr(rp, col, val, x, y_cpu, y_gpu)
+        rec["cpu_baseline"] = cpu
+        rec["parity"] = {"max_rownorm_err_vs_cpu": err, "zero_rows_bad": zero_bad, "tol": TOL[dt],
+                         "ok": bool(err <= TOL[dt] and zero_bad == 0),
+                         "bit_identical_rows": int(np.count_nonzero(y_gpu == y_cpu)), "rows": m}
+        rec["speedup_vs_cpu"] = round(cpu["ms_per_spmv"] / host_ms, 1)
+    else:
+        rec["cpu_baseline"] = None
+    return rec
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--steps", type=int, default=4000,
+                    help="timed steps of the headline configuration (exactly); the other configurations run "
+                         "max(steps, --min-steps)")
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
+    ap.add_argument("--min-steps", type=int, default=200)
+    ap.add_argument("--config", type=int, default=0, choices=[0] + sorted(WORKLOADS),
+                    help="0 = every configuration (C1-C5 fp64, C4 fp32) with C5 fp64 as the headline; "
+                         "N = configuration N alone, in --dtype")
     ap.add_argument("--dtype", default="f64", choices=["f64", "f32", "f16"])
     ap.add_argument("--variant", default="auto", choices=["auto", "adaptive", "flat", "prefree"])
     ap.add_argument("--tile", type=int, default=0)
@@ -125,8 +423,10 @@ def main():
     ap.add_argument("--chunk-nnz", type=int, default=-1,
                     help="FLAT 1024/2048: nnz per XCD chunk of tiles (0 = one chunk per XCD); -1 = the plan's choice")
     ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--cold-steps", type=int, default=100)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--legs", default="rotated,cold,search,host",
+                    help="legs measured besides the hot steps (comma list of rotated, cold, search, host)")
+    ap.add_argument("--cold-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=3.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--launch", default="auto", choices=["auto", "graph", "eager"],
                     help="timed steps as one captured HIP graph or launched one by one from Python; auto: graph "
@@ -143,214 +443,70 @@ def main():
               "across GPUs the matrix would be split into row blocks of equal nnz, each GPU holding the x entries "
               "its columns touch; no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
+    for leg in args.legs.split(","):
+        if leg and leg not in ("rotated", "cold", "search", "host"):
+            ap.error(f"unknown leg {leg}")
 
-    import numpy as np
     import torch
 
     pf = load_pkg()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    dt = args.dtype
-    vb = {"f64": 8, "f32": 4, "f16": 2}[dt]
-    tdt = {"f64": torch.float64, "f32": torch.float32, "f16": torch.float16}[dt]
-
-    rp, col, vals = pf.synth_csr(args.config, seed=args.seed, dtypes=(dt,))
-    val = vals[dt]
-    m = len(rp) - 1
-    n = m
-    nnz = len(col)
-    x = pf.synth_x(args.config, n, seed=args.seed, dtypes=(dt,))[dt]
-
-    stream = torch.cuda.current_stream()
-    d_rp = torch.from_numpy(rp).to(dev)
-    d_col = torch.from_numpy(col).to(dev)
-    d_val = torch.from_numpy(val).to(dev)
-    d_x = torch.from_numpy(x).to(dev)
-    d_y = torch.full((m,), float("nan"), dtype=tdt, device=dev)
-    torch.cuda.synchronize()
-
-    t_plan = time.perf_counter()
-    plan = pf.Plan(d_rp, d_col, m, n, nnz, dt, args.variant, args.tile, stream=stream)
-    t_plan = (time.perf_counter() - t_plan) * 1e3
-    if args.x_windows >= 0:
-        plan.set_x_windows(args.x_windows)
-    if args.chunk_nnz >= 0:
-        plan.set_chunk_nnz(args.chunk_nnz)
-    info = plan.info.as_dict()
-
-    def step():
-        plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=stream)
-
-    w0 = torch.cuda.Event(enable_timing=True)
-    w1 = torch.cuda.Event(enable_timing=True)
-    w0.record(stream)
-    for _ in range(args.warmup):
-        step()
-    w1.record(stream)
-    torch.cuda.synchronize()
-    warm_us = w0.elapsed_time(w1) * 1e3 / max(1, args.warmup)
-    plan.check(stream=stream)
-    y_eager = d_y.clone()
-    use_graph = args.launch == "graph" or (args.launch == "auto" and warm_us < 20.0)
-
-    # The timed steps as one HIP graph of exactly --steps SpMV launches (the
-    # plan's kernels only: no memset, no host synchronisation), so that the
-    # launch-bound small configurations measure the GPU rather than the rate
-    # at which Python can launch (--launch chooses; see its help).
-    graph = None
-    if use_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            cs = torch.cuda.current_stream()
-            for _ in range(args.steps):
-                plan.execute(d_rp, d_col, d_val, d_x, d_y, stream=cs)
-        torch.cuda.synchronize()
-        d_y.fill_(float("nan"))
-        graph.replay()                       # untimed replay, checked against the eager y below
-        torch.cuda.synchronize()
-        graph_same = bool(torch.equal(d_y, y_eager)) if info["variant_name"] != "prefree" else None
-
-    # Timed region: exactly --steps steps, device-synchronised on both sides.
-    # Launched one by one, the steps are also cut into batches by events on the
-    # launch stream, for a median of the per-step time next to the mean.
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    n_batch = 40 if graph is None and args.steps >= 40 else 0
-    bounds = [round(j * args.steps / n_batch) for j in range(n_batch + 1)] if n_batch else []
-    marks = [e0] + [torch.cuda.Event(enable_timing=True) for _ in range(n_batch - 1)] + [e1] if n_batch else []
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    if graph is not None:
-        graph.replay()
+    torch.cuda.set_device(torch.device("cuda:0"))
+    if args.config:
+        todo = [(args.config, args.dtype)]
+        head = todo[0]
     else:
-        k = 1
-        for i in range(args.steps):
-            if n_batch and k < n_batch and i == bounds[k]:
-                marks[k].record(stream)
-                k += 1
-            step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    ms_kernel = e0.elapsed_time(e1) / args.steps
-    ms_median = None
-    if n_batch:
-        per = [marks[j].elapsed_time(marks[j + 1]) / (bounds[j + 1] - bounds[j]) for j in range(n_batch)]
-        ms_median = float(np.median(per))
-    plan.check(stream=stream)
-
-    # Cold: a 1 GiB write between steps evicts the matrix from L2 and MALL.
-    flush = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-    cold_ms = 0.0
-    c0 = torch.cuda.Event(enable_timing=True)
-    c1 = torch.cuda.Event(enable_timing=True)
-    for _ in range(args.cold_steps):
-        flush.zero_()
-        c0.record(stream)
-        step()
-        c1.record(stream)
-        c1.synchronize()
-        cold_ms += c0.elapsed_time(c1)
-    cold_ms /= max(1, args.cold_steps)
-    del flush
-
-    # The drop-in boundary (preFreeSpMV) takes host buffers: one SpMV including
-    # the host->device copies of the CSR and x, planning and the copy of y back.
-    torch.cuda.synchronize()
-    h0 = time.perf_counter()
-    h_rp = torch.from_numpy(rp).to(dev)
-    h_col = torch.from_numpy(col).to(dev)
-    h_val = torch.from_numpy(val).to(dev)
-    h_x = torch.from_numpy(x).to(dev)
-    h_y = torch.empty(m, dtype=tdt, device=dev)
-    pf.spmv(h_rp, h_col, h_val, h_x, h_y, m, n, nnz, dt, args.variant, stream=stream)
-    y_host = h_y.cpu()
-    pcie_ms = (time.perf_counter() - h0) * 1e3
-    del h_rp, h_col, h_val, h_x, h_y, y_host
+        todo, head = ALL_CONFIGS, HEADLINE
+    records = {}
+    for cfg, dt in todo:
+        is_head = (cfg, dt) == head
+        steps = args.steps if is_head else max(args.steps, args.min_steps)
+        print(f"bench: {cfg_name(cfg, dt)} ({'headline, ' if is_head else ''}{steps} steps)", file=sys.stderr,
+              flush=True)
+        records[cfg_name(cfg, dt)] = measure(pf, torch, cfg, dt, args, steps, args.warmup, not args.no_cpu)
 
     if args.copy_calibration:
-        src = torch.ones(1 << 25, dtype=torch.float64, device=dev)  # 256 MiB
+        src = torch.ones(1 << 25, dtype=torch.float64, device="cuda:0")  # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(3):
             torch.neg(src, out=dst)  # an elementwise kernel: reads 256 MiB, writes 256 MiB
         torch.cuda.synchronize()
         del src, dst
 
-    y_gpu = d_y.cpu().numpy()
-    bytes_eff = (nnz + m + n) * vb + nnz * 4 + (m + 1) * 4          # test/test_cdspmv.cpp:305
-    bytes_gather = (2 * nnz + m) * vb + nnz * 4 + (m + 1) * 4       # test/test_cdspmv.cpp:306
-    gbs = bytes_eff / (ms_kernel * 1e-3) / 1e9
-    key = f"C{args.config}-{dt}-{info['variant_name']}-{info['tile']}" + (
-        f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
-        "-rows" if info["row_aligned"] else "")
-
+    h = records[cfg_name(*head)]
     result = {
         "metric": METRIC,
-        "value": round(2.0 * nnz / (ms_step * 1e6), 3),
+        "value": h["gflops"],
         "unit": "GFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 6),
-        "ms_per_step_median": (round(ms_median, 6) if ms_median is not None else None),
-        "median_of": (f"{n_batch} batches of the timed steps, HIP events on the launch stream" if n_batch
-                      else "not measured: the timed steps are one graph replay"),
+        "steps": h["steps"],
+        "warmup": h["warmup"],
+        "ms_per_step": h["ms"],
+        "ms_per_step_median": h["kernel_ms_median"],
+        "median_of": h["median_of"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dt,
-        "data": "synthetic (seeded generator prefree-public_amd/host/synth.cpp, U[-1,1] values)",
-        "config": {"workload": WORKLOADS[args.config] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
-                   "cfg": f"C{args.config}", "rows": m, "cols": n, "nnz": nnz, "seed": args.seed,
-                   "variant": info["variant_name"], "tile": info["tile"], "tiles": info["ntiles"],
-                   "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
-                   "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
-                   "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
-                   "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3)},
-        "gbps_effective": round(gbs, 1),
-        "pct_peak_hbm": round(100.0 * gbs / PEAK_HBM_GBS, 2),
-        "bytes_model": {"effective": bytes_eff, "gather": bytes_gather,
-                        "source": "test/test_cdspmv.cpp:305-306"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic_from_profiles(key),
-                     "kernel": kernel_name(info),
-                     "launch_ms": round(ms_kernel, 6), "algorithmic_bytes": bytes_eff,
-                     # the measured HBM bytes of the step kernel (profiles/traffic.json) over its time
-                     "traffic_gbps": (round(traffic_from_profiles(key) / (ms_kernel * 1e6), 1)
-                                      if traffic_from_profiles(key) else None),
-                     "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
-                              if info["needs_fixup"] else "step = one tile-kernel launch")},
-        "cold": ({"ms": round(cold_ms, 6), "gbps_effective": round(bytes_eff / (cold_ms * 1e-3) / 1e9, 1),
-                  "flush": "1 GiB write before each step"} if args.cold_steps > 0 else None),
-        "launch": ("one captured HIP graph of the timed steps (y checked bit for bit against an eager step: "
-                   f"{'equal' if graph_same else ('n/a' if graph_same is None else 'DIFFERENT')})"
-                   if graph is not None else "eager launches from Python")
-                  + f"; eager warm-up step {warm_us:.1f} us",
-        "host_buffers": {"ms": round(pcie_ms, 3), "gflops": round(2.0 * nnz / (pcie_ms * 1e6), 3),
-                         "what": "one SpMV from pageable host arrays: copies in, plan, execute, copy of y out"},
+        "dtype": h["dtype"],
+        "data": (f"synthetic, seed {args.seed} (seeded generator prefree-public_amd/host/synth.cpp); "
+                 f"{h['cfg']}: {h['values']}"),
+        "config": {k: h[k] for k in ("workload", "cfg", "rows", "cols", "nnz", "seed", "variant", "tile", "tiles",
+                                     "run_tiles", "row_aligned", "x_windows", "xcd_chunk_nnz", "split_row_combine",
+                                     "plan_ms")},
+        "gbps_effective": h["gbps_effective"],
+        "pct_peak_hbm": h["pct_peak_hbm"],
+        "bytes_model": h["bytes_model"],
+        "roofline": h["roofline"],
+        "rotated": h.get("rotated"),
+        "cold": h.get("cold"),
+        "search": h.get("search"),
+        "launch": h["launch"],
+        "host_buffers": h.get("host_buffers"),
         "device": pf.device_name(),
+        "cpu_baseline": h["cpu_baseline"],
+        "parity": h.get("parity"),
+        "speedup_vs_cpu": h.get("speedup_vs_cpu"),
+        "configs": records,
     }
-    if not args.no_cpu:
-        cpu, y_cpu = cpu_baseline(rp, col, val, x, args.cpu_seconds, nnz)
-        import oracle
-        if dt == "f16":  # against the fp64 sums of the same fp16 data: one binary16 rounding per row,
-            # 2^-11 relative or, for a subnormal result, 2^-25 absolute (allowed for as 2^-24)
-            den = oracle.spmv_serial(rp, col, np.abs(val.astype(np.float64)), np.abs(x.astype(np.float64)))
-            dev_ = np.abs(y_gpu.astype(np.float64) - y_cpu)
-            zero_bad = int(np.count_nonzero((den == 0) & (y_gpu != 0)))
-            nz = den > 0
-            err = float((np.maximum(dev_[nz] - 2.0 ** -24, 0) / den[nz]).max()) if nz.any() else 0.0
-        else:
-            err, zero_bad, _ = oracle.rownorm_maxerr(rp, col, val, x, y_cpu, y_gpu)
-        result["cpu_baseline"] = cpu
-        result["parity"] = {"max_rownorm_err_vs_cpu": err, "zero_rows_bad": zero_bad,
-                            "tol": {"f64": 1e-12, "f32": 1e-5, "f16": 1e-3}[dt]}
-        result["speedup_vs_cpu"] = round(cpu["ms_per_spmv"] / ms_step, 1)
-    else:
-        result["cpu_baseline"] = None
-    plan.close()
     print(json.dumps(result), flush=True)
 
 

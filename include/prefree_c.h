@@ -134,6 +134,11 @@ int pf_plan_set_x_windows(pf_plan *plan, int x_windows);
  * of the tiles per XCD).  Small chunks keep the eight XCDs streaming neighbouring addresses; large ones
  * keep more of a row's x neighbourhood in one XCD's L2.  All values give the same y. */
 int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
+/* FLAT 1024/2048: 1 (default) = the first call records each tile's first row and later calls read it;
+ * 0 = every call searches row_ptr inside the tile kernel (no recorded map, tiles dealt to XCDs by
+ * position).  Both give the same y.  The reference times its own row map as a separate pre-pass
+ * (preFreeSpMV.cu:604-622); 0 measures what finding the rows costs when nothing is remembered. */
+int pf_plan_set_remember_rows(pf_plan *plan, int remember);
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out);
 
 /* y = A·x on `stream` (asynchronous; no allocation, no synchronisation).

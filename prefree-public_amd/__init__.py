@@ -32,7 +32,7 @@ VARIANTS = {"auto": AUTO, "prefree": PREFREE, "adaptive": ADAPTIVE, "flat": FLAT
 VARIANT_NAMES = {v: k for k, v in VARIANTS.items()}
 DTYPES = {"f64": F64, "f32": F32, "f16": F16}
 STATUS = {0: "PF_OK", 1: "PF_ERR_INVALID", 2: "PF_ERR_ALIGN", 3: "PF_ERR_HIP", 4: "PF_ERR_NOMEM",
-          5: "PF_ERR_UNSUPPORTED", 6: "PF_ERR_CSR", 7: "PF_ERR_KERNEL"}
+          5: "PF_ERR_UNSUPPORTED", 6: "PF_ERR_CSR", 7: "PF_ERR_KERNEL", 8: "PF_ERR_IO"}
 
 
 class PrefreeError(RuntimeError):
@@ -128,6 +128,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_row_aligned, [_vp, _i])
         _sig(L.pf_plan_set_x_windows, [_vp, _i])
         _sig(L.pf_plan_set_chunk_nnz, [_vp, _ll])
+        _sig(L.pf_plan_set_remember_rows, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -280,6 +281,10 @@ class Plan:
 
     def set_chunk_nnz(self, chunk_nnz):
         _check(lib().pf_plan_set_chunk_nnz(self._h, int(chunk_nnz)), "pf_plan_set_chunk_nnz")
+
+    def set_remember_rows(self, remember):
+        """pf_plan_set_remember_rows: False = every call searches row_ptr (no recorded row map)."""
+        _check(lib().pf_plan_set_remember_rows(self._h, int(bool(remember))), "pf_plan_set_remember_rows")
 
     def execute(self, row_ptr, col, val, x, y, stream=None):
         _check(lib().pf_plan_execute(self._h, _p(row_ptr), _p(col), _p(val), _p(x), _p(y), _s(stream)),

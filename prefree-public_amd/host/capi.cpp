@@ -348,6 +348,7 @@ struct pf_plan {
     bool map_ready = false;  // set once a call that records the map has been issued
     int *sched = nullptr;    // split-row FLAT 1024/2048: x-window schedule, recorded with the map
     long long sched_cap = 0;
+    bool remember_rows = true;  // false: every call searches row_ptr (no row map, no schedule)
 };
 
 namespace {
@@ -598,6 +599,14 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz)
     return PF_OK;
 }
 
+int pf_plan_set_remember_rows(pf_plan *plan, int remember)
+{
+    if (!plan || (remember != 0 && remember != 1)) return fail(PF_ERR_INVALID, "remember must be 0 or 1");
+    if (remember && !plan->remember_rows) plan->map_ready = false;  // the next call records the map afresh
+    plan->remember_rows = remember != 0;
+    return PF_OK;
+}
+
 int pf_plan_get_stats(const pf_plan *plan, pf_row_stats *out)
 {
     if (!plan || !out) return fail(PF_ERR_INVALID, "NULL plan or output");
@@ -631,10 +640,10 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.tail_slot = plan->tail;
     a.owner_row = plan->owner;
     a.err_flag = plan->err;
-    a.row_map = plan->row_map;
-    a.map_ready = plan->map_ready ? 1 : 0;
+    a.row_map = plan->remember_rows ? plan->row_map : nullptr;
+    a.map_ready = (plan->remember_rows && plan->map_ready) ? 1 : 0;
     a.row_aligned = plan->info.row_aligned;
-    a.sched = (plan->info.x_windows && plan->sched) ? plan->sched : nullptr;
+    a.sched = (plan->remember_rows && plan->info.x_windows && plan->sched) ? plan->sched : nullptr;
     a.sched_cap = plan->sched_cap;
     a.chunk_nnz = plan->info.chunk_nnz;
     if (a.sched && !plan->map_ready)  // the recording call starts from empty lists
@@ -647,7 +656,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         return PF_OK;
     case PF_FLAT:
         PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");  // tile 256 launches its own combine
-        if (plan->row_map) plan->map_ready = true;  // later calls on this stream read the recorded rows
+        if (a.row_map) plan->map_ready = true;  // later calls on this stream read the recorded rows
         if (plan->info.needs_fixup && plan->info.tile != kFlowTile)
             PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
         return PF_OK;
