@@ -185,6 +185,17 @@ int pf_set_tuning_table(const char *path);
 int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
             int m, int n, int nnz, int dtype, int variant, void *stream);
 
+/* No counterpart in the reference: pf_spmv for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, result and
+ * errors as pf_spmv, but no hipMalloc / hipFree and no allocating library call: the row statistics and
+ * the plan's workspace live in a fixed 8 MiB device array of the library (PFK_SCRATCH_BYTES, one per
+ * device, kept until the process ends).  Matrices whose workspace does not fit are refused with
+ * PF_ERR_UNSUPPORTED before any launch (about 230M nnz for fp64 FLAT 2048-nnz tiles, 120M for
+ * 1024-nnz tiles; pf_last_error gives the bytes needed).  Synchronises `stream`.  Calls that overlap on
+ * one device (two streams, two host threads) share that array and race: order them. */
+int pf_spmv_noalloc(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
+                    int m, int n, int nnz, int dtype, int variant, void *stream);
+
 /* ---- synthetic matrices (the benchmark configurations) --------------------
  * cfg 1..5 = C1..C5: 1 uniform 4096^2 16/row, 2 5-point Laplacian 2048^2,
  * 3 power-law n=2M, 4 very sparse n=20M, 5 mixed dense rows n=1M.  Scaled-down

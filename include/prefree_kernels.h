@@ -96,6 +96,14 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
  * the last one = m), the map the reference pre-pass writes. */
 int pfk_debug_prefree_rows(const int *row_ptr, int m, int nnz, int tile, int *d_out, void *stream);
 
+/* No counterpart in the reference.  Device scratch for pf_spmv_noalloc, the entry point for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc): a
+ * file-scope __device__ array of PFK_SCRATCH_BYTES bytes, 256-byte aligned, one copy per device, held
+ * until the process ends.  Writes the current device's address of it (looked up once per device with
+ * hipGetSymbolAddress) and its size.  Every user on one device shares the same bytes. */
+#define PFK_SCRATCH_BYTES (8u << 20)
+int pfk_scratch(void **ptr, size_t *bytes);
+
 /* Runtime wrappers. */
 int pfk_malloc(void **p, size_t bytes);
 int pfk_free(void *p);

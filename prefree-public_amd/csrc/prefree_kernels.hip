@@ -52,6 +52,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 using namespace pfdev;
@@ -2109,6 +2110,22 @@ __global__ __launch_bounds__(kBS) void k_fill_zero(uint32_t *__restrict__ p, siz
         p[i] = 0u;
 }
 
+// ---- scratch of the no-allocation entry point --------------------------------
+//
+// pf_spmv_noalloc takes its row statistics and plan workspace from this array
+// instead of allocating.  Each device holds its own copy, at its own address,
+// for the life of the process.  In host code `scratch` only names the symbol:
+// kernels get the address pfk_scratch looks up with hipGetSymbolAddress.
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[PFK_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
 // ---- host side of the thin layer -------------------------------------------
 
 thread_local char g_err[256] = "";
@@ -2659,6 +2676,32 @@ int pfk_device_name(char *buf, int len)
     hipDeviceProp_t p;
     PFK_HIP(hipGetDeviceProperties(&p, dev));
     snprintf(buf, (size_t)len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return PF_OK;
+}
+
+int pfk_scratch(void **ptr, size_t *bytes)
+{
+    if (!ptr || !bytes) return PF_ERR_INVALID;
+    *ptr = nullptr;
+    *bytes = 0;
+    int dev = 0;
+    PFK_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) {
+        snprintf(g_err, sizeof g_err, "device %d: scratch is kept for devices 0..%d", dev, kMaxDevices - 1);
+        return PF_ERR_UNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {  // once per device, with that device current
+        void *p = nullptr;
+        PFK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) {
+            snprintf(g_err, sizeof g_err, "hipGetSymbolAddress(scratch) gave a null address");
+            return PF_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    *bytes = PFK_SCRATCH_BYTES;
     return PF_OK;
 }
 

@@ -353,10 +353,10 @@ struct pf_plan {
 
 namespace {
 
-// The plan for a validated matrix with known statistics (shared by plan
-// creation and the tuner's candidates).
-int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
-               void *stream, pf_plan **plan)
+// Launch configuration of a plan for a validated matrix with known statistics
+// (host only, apart from occupancy queries): variant and tile (PF_AUTO
+// resolved), run length, x windows, workspace size.
+int plan_info(const pf_row_stats &s, int n, int dtype, int variant, int tile, pf_plan_info *out)
 {
     Choice c;
     if (variant == PF_AUTO) {  // an explicit tile is kept only if the chosen variant has it
@@ -380,22 +380,20 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     if (c.tile == info.tile && c.variant == info.variant) apply_overrides(c, info);
     if (uses_row_map(info.variant, info.tile))
         info.x_windows = x_windows_rule(s, n, dtype, info.tile, info.row_aligned);
+    *out = info;
+    return PF_OK;
+}
 
-    pf_plan *p = new pf_plan();
-    p->m = m;
-    p->n = n;
-    p->nnz = nnz;
-    p->info = info;
-    p->stats = s;
-    int rc = pfk_malloc(&p->ws, info.workspace_bytes);
-    if (rc != PF_OK) {
-        delete p;
-        return from_kernel_layer(rc, "plan workspace");
-    }
-    char *w = static_cast<char *>(p->ws);
+// Points the plan's arrays into its workspace `w` (info.workspace_bytes bytes,
+// 256-byte aligned): error flag, head / tail slots, owners, row map, schedule.
+void plan_carve(pf_plan *p, void *w0)
+{
+    const pf_plan_info &info = p->info;
+    char *w = static_cast<char *>(w0);
+    p->ws = w0;
     p->err = reinterpret_cast<int *>(w);
     if (info.variant != PF_PREFREE) {
-        const size_t vb = (size_t)slot_bytes(dtype);
+        const size_t vb = (size_t)slot_bytes(info.dtype);
         const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
         p->head = w + 256;
         p->tail = w + 256 + slots;
@@ -408,25 +406,57 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
             p->sched_cap = sched_cap(info.ntiles);
         }
     }
-    rc = pfk_fill_zero(p->err, 256, stream);
-    // Every owner slot starts as "no split row": a combine kernel never reads an unset slot.
+}
+
+// Fresh workspace state on `stream` (fill kernels, no memset): error flag
+// clear, every owner slot "no split row" (a combine kernel never reads an
+// unset slot), and ADAPTIVE's split-row owner table, which depends on
+// row_ptr only.  Asynchronous.
+int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
+{
+    const pf_plan_info &info = p->info;
+    int rc = pfk_fill_zero(p->err, 256, stream);
     if (rc == PF_OK && p->owner) rc = pfk_fill_u32(p->owner, (size_t)info.ntiles, 0xFFFFFFFFu, stream);
     if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
-        // The split-row owner of every tile depends on row_ptr only: build it once.
         pfk_spmv_args a;
         std::memset(&a, 0, sizeof a);
         a.row_ptr = d_row_ptr;
-        a.m = m;
-        a.n = n;
-        a.nnz = nnz;
+        a.m = p->m;
+        a.n = p->n;
+        a.nnz = p->nnz;
         a.tile = info.tile;
         a.guess_spread = info.guess_spread;
         a.run_tiles = info.run_tiles;
         a.ntiles = info.ntiles;
         a.owner_row = p->owner;
         a.err_flag = p->err;
-        rc = pfk_adaptive_owners(dtype, &a, stream);
+        rc = pfk_adaptive_owners(info.dtype, &a, stream);
     }
+    return rc;
+}
+
+// The plan for a validated matrix with known statistics (shared by plan
+// creation and the tuner's candidates): workspace allocated and initialised.
+int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
+               void *stream, pf_plan **plan)
+{
+    pf_plan_info info;
+    const int st = plan_info(s, n, dtype, variant, tile, &info);
+    if (st != PF_OK) return st;
+    pf_plan *p = new pf_plan();
+    p->m = m;
+    p->n = n;
+    p->nnz = nnz;
+    p->info = info;
+    p->stats = s;
+    void *w = nullptr;
+    int rc = pfk_malloc(&w, info.workspace_bytes);
+    if (rc != PF_OK) {
+        delete p;
+        return from_kernel_layer(rc, "plan workspace");
+    }
+    plan_carve(p, w);
+    rc = plan_init(p, d_row_ptr, stream);
     if (rc == PF_OK) rc = pfk_stream_sync(stream);
     if (rc != PF_OK) {
         pfk_free(p->ws);
@@ -436,6 +466,60 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     *plan = p;
     return PF_OK;
 }
+
+// Argument checks shared by plan creation and the no-allocation entry point.
+int check_matrix_args(const int *d_row_ptr, const int *d_col, int m, int n, int nnz, int dtype, int variant)
+{
+    if (m < 0 || n < 0 || nnz < 0 || value_bytes(dtype) == 0 || variant < PF_AUTO || variant > PF_FLAT)
+        return fail(PF_ERR_INVALID, "bad size, dtype or variant");
+    if (m > 0 && !d_row_ptr) return fail(PF_ERR_INVALID, "row_ptr is NULL");
+    if ((unsigned long long)nnz + (unsigned long long)m >= 0xFFFFFFFFull)
+        return fail(PF_ERR_UNSUPPORTED, "nnz + m must stay below 2^32");
+    // x and y are addressed through buffer resources with 32-bit byte offsets.
+    if ((unsigned long long)n * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull ||
+        (unsigned long long)m * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull)
+        return fail(PF_ERR_UNSUPPORTED, "x and y must each stay below 4 GiB");
+    if (d_col && !aligned16(d_col)) return fail(PF_ERR_ALIGN, "col not 16-byte aligned");
+    if (nnz > 0 && m == 0) return fail(PF_ERR_CSR, "nnz > 0 with no rows");
+    return PF_OK;
+}
+
+// Row statistics of a device CSR through a caller-supplied block of 44
+// unsigned long long (synchronises `stream`).
+int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int m, int n, long long nnz,
+              pf_row_stats *out, void *stream)
+{
+    unsigned long long h[44];
+    int st = pfk_row_stats(d_row_ptr, d_col, m, n, nnz, d, stream);
+    if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream);
+    if (st != PF_OK) return from_kernel_layer(st, "row statistics");
+    std::memset(out, 0, sizeof *out);
+    out->m = m;
+    out->nnz = nnz;
+    out->max_row_len = (long long)h[0];
+    out->min_row_len = m > 0 ? (long long)h[1] : 0;
+    out->n_empty_rows = (long long)h[2];
+    out->n_decreasing = (long long)h[3];
+    out->row_ptr_first = (long long)h[4];
+    out->row_ptr_last = (long long)h[5];
+    out->n_bad_cols = (d_col && nnz > 0) ? (long long)h[6] : (nnz > 0 ? -1 : 0);
+    for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
+    return PF_OK;
+}
+
+int check_csr_stats(const pf_row_stats &s, int nnz)
+{
+    if (s.row_ptr_first != 0 || s.row_ptr_last != nnz || s.n_decreasing != 0 || s.n_bad_cols > 0)
+        return fail(PF_ERR_CSR, "row_ptr[0]=" + std::to_string(s.row_ptr_first) + " row_ptr[m]=" +
+                                    std::to_string(s.row_ptr_last) + " decreasing=" +
+                                    std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
+    return PF_OK;
+}
+
+// Bytes of pf_spmv_noalloc's scratch taken by the row statistics block; the
+// workspace starts after it, 256-byte aligned.
+constexpr size_t kNoallocStatsBytes = 512;
 
 }  // namespace
 
@@ -467,25 +551,10 @@ int pf_row_stats_compute(const int *d_row_ptr, const int *d_col, int m, int n, l
     if (!out || !d_row_ptr || m < 0 || n < 0 || nnz < 0)
         return fail(PF_ERR_INVALID, "pf_row_stats_compute: bad argument");
     unsigned long long *d = nullptr;
-    unsigned long long h[44];
-    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), sizeof h), "stats buffer");
-    int st = pfk_row_stats(d_row_ptr, d_col, m, n, nnz, d, stream);
-    if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
-    if (st == PF_OK) st = pfk_stream_sync(stream);
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), 44 * sizeof(unsigned long long)), "stats buffer");
+    const int st = stats_via(d, d_row_ptr, d_col, m, n, nnz, out, stream);
     pfk_free(d);
-    if (st != PF_OK) return from_kernel_layer(st, "row statistics");
-    std::memset(out, 0, sizeof *out);
-    out->m = m;
-    out->nnz = nnz;
-    out->max_row_len = (long long)h[0];
-    out->min_row_len = m > 0 ? (long long)h[1] : 0;
-    out->n_empty_rows = (long long)h[2];
-    out->n_decreasing = (long long)h[3];
-    out->row_ptr_first = (long long)h[4];
-    out->row_ptr_last = (long long)h[5];
-    out->n_bad_cols = (d_col && nnz > 0) ? (long long)h[6] : (nnz > 0 ? -1 : 0);
-    for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
-    return PF_OK;
+    return st;
 }
 
 int pf_select(const pf_row_stats *stats, int dtype, int variant, pf_plan_info *out)
@@ -509,29 +578,17 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
 {
     if (!plan) return fail(PF_ERR_INVALID, "plan is NULL");
     *plan = nullptr;
-    if (m < 0 || n < 0 || nnz < 0 || value_bytes(dtype) == 0 || variant < PF_AUTO || variant > PF_FLAT)
-        return fail(PF_ERR_INVALID, "pf_plan_create: bad size, dtype or variant");
-    if (m > 0 && !d_row_ptr) return fail(PF_ERR_INVALID, "row_ptr is NULL");
-    if ((unsigned long long)nnz + (unsigned long long)m >= 0xFFFFFFFFull)
-        return fail(PF_ERR_UNSUPPORTED, "nnz + m must stay below 2^32");
-    // x and y are addressed through buffer resources with 32-bit byte offsets.
-    if ((unsigned long long)n * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull ||
-        (unsigned long long)m * (unsigned long long)value_bytes(dtype) >= 0xFFFFFFF0ull)
-        return fail(PF_ERR_UNSUPPORTED, "x and y must each stay below 4 GiB");
-    if (d_col && !aligned16(d_col)) return fail(PF_ERR_ALIGN, "col not 16-byte aligned");
-    if (nnz > 0 && m == 0) return fail(PF_ERR_CSR, "nnz > 0 with no rows");
-
+    int st = check_matrix_args(d_row_ptr, d_col, m, n, nnz, dtype, variant);
+    if (st != PF_OK) return st;
     pf_row_stats s;
     std::memset(&s, 0, sizeof s);
     s.m = m;
     s.nnz = nnz;
     if (m > 0) {
-        const int st = pf_row_stats_compute(d_row_ptr, d_col, m, n, nnz, &s, stream);
+        st = pf_row_stats_compute(d_row_ptr, d_col, m, n, nnz, &s, stream);
         if (st != PF_OK) return st;
-        if (s.row_ptr_first != 0 || s.row_ptr_last != nnz || s.n_decreasing != 0 || s.n_bad_cols > 0)
-            return fail(PF_ERR_CSR, "row_ptr[0]=" + std::to_string(s.row_ptr_first) + " row_ptr[m]=" +
-                                        std::to_string(s.row_ptr_last) + " decreasing=" +
-                                        std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
+        st = check_csr_stats(s, nnz);
+        if (st != PF_OK) return st;
     }
     return plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan);
 }
@@ -698,6 +755,53 @@ int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const voi
     if (st == PF_OK) st = pf_plan_check(p, stream);
     const int st2 = pf_plan_destroy(p);
     return st != PF_OK ? st : st2;
+}
+
+int pf_spmv_noalloc(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y, int m,
+                    int n, int nnz, int dtype, int variant, void *stream)
+{
+    int st = check_matrix_args(d_row_ptr, d_col, m, n, nnz, dtype, variant);
+    if (st != PF_OK) return st;
+    if (m == 0) return PF_OK;
+    if (!d_y || (nnz > 0 && (!d_col || !d_val || !d_x))) return fail(PF_ERR_INVALID, "NULL matrix or vector pointer");
+    const size_t room = (size_t)PFK_SCRATCH_BYTES - kNoallocStatsBytes;
+    if (variant != PF_AUTO) {  // an explicit variant's workspace follows from (m, nnz): refuse before any launch
+        pf_row_stats g;
+        std::memset(&g, 0, sizeof g);
+        g.m = m;
+        g.nnz = nnz;
+        pf_plan_info guess;
+        st = finish_info(g, dtype, variant, default_tile(variant, dtype), &guess);
+        if (st != PF_OK) return st;
+        if (guess.workspace_bytes > room)
+            return fail(PF_ERR_UNSUPPORTED, "pf_spmv_noalloc: the workspace needs " +
+                                                std::to_string(guess.workspace_bytes) + " bytes, the scratch holds " +
+                                                std::to_string(room) + "; use pf_spmv");
+    }
+    void *scr = nullptr;
+    size_t scr_bytes = 0;
+    PF_TRY(pfk_scratch(&scr, &scr_bytes), "scratch");
+    if (scr_bytes < kNoallocStatsBytes + 256) return fail(PF_ERR_UNSUPPORTED, "scratch too small");
+    pf_plan p;  // on the stack: no allocation of any kind
+    p.m = m;
+    p.n = n;
+    p.nnz = nnz;
+    st = stats_via(static_cast<unsigned long long *>(scr), d_row_ptr, d_col, m, n, nnz, &p.stats, stream);
+    if (st != PF_OK) return st;
+    st = check_csr_stats(p.stats, nnz);
+    if (st != PF_OK) return st;
+    st = plan_info(p.stats, n, dtype, variant, 0, &p.info);
+    if (st != PF_OK) return st;
+    if (p.info.workspace_bytes > scr_bytes - kNoallocStatsBytes)
+        return fail(PF_ERR_UNSUPPORTED, "pf_spmv_noalloc: the workspace needs " + std::to_string(p.info.workspace_bytes) +
+                                            " bytes, the scratch holds " +
+                                            std::to_string(scr_bytes - kNoallocStatsBytes) + "; use pf_spmv");
+    plan_carve(&p, static_cast<char *>(scr) + kNoallocStatsBytes);
+    st = plan_init(&p, d_row_ptr, stream);
+    if (st != PF_OK) return from_kernel_layer(st, "scratch workspace init");
+    st = pf_plan_execute(&p, d_row_ptr, d_col, d_val, d_x, d_y, stream);
+    if (st == PF_OK) st = pf_plan_check(&p, stream);  // synchronises: the scratch is free again on return
+    return st;
 }
 
 int pf_set_tuning_table(const char *path)

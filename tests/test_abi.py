@@ -221,3 +221,15 @@ def test_validation_before_gpu():
     m, n, z = ctypes.c_int(), ctypes.c_int(), ctypes.c_longlong()
     assert L.pf_synth_dims(9, 1, 0, ctypes.byref(m), ctypes.byref(n), ctypes.byref(z)) == 1
     assert L.pf_plan_destroy(None) == 0
+
+
+def test_noalloc_rejects_oversized_workspace_before_launch():
+    # pf_spmv_noalloc: FLAT with 1024-nnz tiles on 300M nnz needs about 10 MB of workspace, more than the
+    # 8 MiB scratch; refused from the sizes alone, before any GPU call (the pointers are never read).
+    L = pf.lib()
+    f = L.pf_spmv_noalloc
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int] * 5 + [ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    st = f(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1, 1, 300_000_000, pf.F64, pf.FLAT, None)
+    assert st == 5  # PF_ERR_UNSUPPORTED
+    assert b"scratch" in L.pf_last_error()
