@@ -404,6 +404,57 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
     return rec
 
 
+def run_probe(pf, torch, args):
+    """--probe gather: the x gathers alone (pfk_probe_gather), hot, as a ceiling for the SpMV kernels.
+
+    Random 8-byte reads over a 16 MB and an 8 MB array (16M indices each), and each configuration's own
+    column indices over its own x, with every compiled cache policy of the x loads for the random and
+    C3 / C5 cases.  Events around `reps` back-to-back launches after 5 untimed ones."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(args.seed)
+    policies = [0, 1, 2, 3, 16, 17, 18, 19]
+    cases = []
+    for mb in (16, 8):
+        n = (mb << 20) // 8
+        cases.append((f"random-{mb}MB", rng.integers(0, n, 16 << 20, dtype=np.int32), n, policies))
+    for cfg in (1, 2, 3, 4, 5):
+        m, n, nnz = pf.synth_dims(cfg, seed=args.seed)
+        _, col, _ = pf.synth_csr(cfg, seed=args.seed, dtypes=("f64",))
+        cases.append((f"C{cfg}-columns", col, n, policies if cfg in (3, 5) else [0]))
+    out = {}
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for name, idx, n, pols in cases:
+        d_idx = torch.from_numpy(np.ascontiguousarray(idx)).to(dev)
+        d_x = torch.rand(n, dtype=torch.float64, device=dev)
+        d_out = torch.empty(4 * (-(-len(idx) // 1024)), dtype=torch.float64, device=dev)
+        rec = {"gathers": int(len(idx)), "x_bytes": int(n * 8), "policy_us": {}}
+        for pol in pols:
+            for _ in range(5):
+                pf.probe_gather("f64", d_idx, d_x, d_out, pol, stream=stream)
+            reps = max(5, min(args.probe_reps, int(2e9 // max(1, len(idx)))))
+            e0.record(stream)
+            for _ in range(reps):
+                pf.probe_gather("f64", d_idx, d_x, d_out, pol, stream=stream)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            rec["policy_us"][str(pol)] = round(us, 2)
+        us0 = rec["policy_us"]["0"]
+        rec["us"] = us0
+        rec["ggathers_per_s"] = round(len(idx) / us0 / 1e3, 2)
+        out[name] = rec
+        print(f"probe {name}: {rec['policy_us']}", file=sys.stderr, flush=True)
+        del d_idx, d_x, d_out
+    print(json.dumps({"probe": "gather", "device": pf.device_name(), "seed": args.seed,
+                      "what": "x gathers alone: 16-byte non-temporal index loads + one x read per index, "
+                              "cache policy bits of the x loads (1 sc0, 2 nt, 16 sc1) as keys, microseconds per launch",
+                      "cases": out}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -432,6 +483,10 @@ def main():
                     help="timed steps as one captured HIP graph or launched one by one from Python; auto: graph "
                          "when an eager warm-up step takes under 20 us (launch-bound), eager otherwise (a graph "
                          "adds about 0.5 us per kernel on MI355X)")
+    ap.add_argument("--probe", default="", choices=["", "gather"],
+                    help="gather: time the x gathers alone (random indices and each configuration's columns) "
+                         "instead of the SpMV")
+    ap.add_argument("--probe-reps", type=int, default=50)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the measurement, run a plain copy kernel over 256 MiB 3 times (known bytes, "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -451,6 +506,9 @@ def main():
 
     pf = load_pkg()
     torch.cuda.set_device(torch.device("cuda:0"))
+    if args.probe == "gather":
+        run_probe(pf, torch, args)
+        return
     if args.config:
         todo = [(args.config, args.dtype)]
         head = todo[0]

@@ -96,6 +96,15 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
  * the last one = m), the map the reference pre-pass writes. */
 int pfk_debug_prefree_rows(const int *row_ptr, int m, int nnz, int tile, int *d_out, void *stream);
 
+/* Measurement only (bench.py --probe gather), no counterpart in the reference: the x gathers of an SpMV
+ * alone.  One workgroup per 1024 indices streams them (16-byte non-temporal loads, as col is streamed) and
+ * reads x[idx[j]] through a buffer resource over x[0, n) with cache policy bits `policy` (gfx950: 1 = sc0,
+ * 2 = nt, 16 = sc1; 0, 1, 2, 3, 16, 17, 18 and 19 are compiled); an index outside [0, n) reads zero.
+ * `out` receives 4 sums per 1024 indices: out_len values of dtype (PF_F64 / PF_F32) must hold
+ * 4 * ceil(count / 1024) of them.  idx 16-byte aligned, 1 <= count < 2^31. */
+int pfk_probe_gather(int dtype, const int *idx, long long count, const void *x, long long n, void *out,
+                     long long out_len, int policy, void *stream);
+
 /* No counterpart in the reference.  Device scratch for pf_spmv_noalloc, the entry point for callers that
  * cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc): a
  * file-scope __device__ array of PFK_SCRATCH_BYTES bytes, 256-byte aligned, one copy per device, held

@@ -169,6 +169,7 @@ def klib() -> ctypes.CDLL:
         _sig(K.pfk_supported_tiles, [_i, _i, ctypes.POINTER(_i), _i])
         _sig(K.pfk_flat_grid, [ctypes.c_longlong, _i, ctypes.c_longlong], ctypes.c_longlong)
         _sig(K.pfk_device_name, [ctypes.c_char_p, _i])
+        _sig(K.pfk_probe_gather, [_i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _vp])
         _sig(K.pfk_last_error, [], ctypes.c_char_p)
         _klib = K
     return _klib
@@ -354,6 +355,13 @@ def supported_tiles(variant, dtype):
     buf = (ctypes.c_int * 8)()
     n = klib().pfk_supported_tiles(variant_code(variant), dtype_code(dtype), buf, 8)
     return [buf[i] for i in range(n)]
+
+
+def probe_gather(dtype, idx, x, out, policy=0, stream=None):
+    """pfk_probe_gather: the x gathers of an SpMV alone (measurement only); `out` holds
+    4 * ceil(len(idx) / 1024) values of dtype."""
+    _check(klib().pfk_probe_gather(dtype_code(dtype), _p(idx), int(idx.numel()), _p(x), int(x.numel()), _p(out),
+                                   int(out.numel()), int(policy), _s(stream)), "pfk_probe_gather")
 
 
 def device_name() -> str:

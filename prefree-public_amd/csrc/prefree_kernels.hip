@@ -214,6 +214,29 @@ __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer
     v[3] = __builtin_bit_cast(half_t, (unsigned short)(vv.y >> 16));
 }
 
+// col and val of one nnz (element offset e of a resource pair): the wave-strided
+// layout, in which a wave's load covers 64 consecutive nnz.
+template <int AUX = kAuxNt>
+__device__ __forceinline__ void load1(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int e, int &c, double &v)
+{
+    c = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, e * 4, 0, AUX);
+    v = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rv, e * 8, 0, AUX));
+}
+
+template <int AUX = kAuxNt>
+__device__ __forceinline__ void load1(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int e, int &c, float &v)
+{
+    c = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, e * 4, 0, AUX);
+    v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rv, e * 4, 0, AUX));
+}
+
+template <int AUX = kAuxNt>
+__device__ __forceinline__ void load1(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int e, int &c, half_t &v)
+{
+    c = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, e * 4, 0, AUX);
+    v = __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(rv, e * 2, 0, AUX));
+}
+
 __device__ __forceinline__ void store4(double *s, const double (&p)[4])
 {
     reinterpret_cast<f64x2 *>(s)[0] = f64x2{p[0], p[1]};
@@ -1080,6 +1103,27 @@ __device__ __forceinline__ long long sched_tile(const int *__restrict__ sched, l
 // while x is gathered.
 
 constexpr int kFlatSearch = 0, kFlatMemo = 1, kFlatDesc = 2;
+// Element layout of the FLAT tiles (k_flat, k_rows).  Wave-strided for fp64
+// and fp32: element (k, j) of a lane is nnz 1024k + 256 wave + 64j + lane of
+// the tile, loaded with one 4- or 8-byte load, so each of a wave's loads and x
+// gathers covers 64 consecutive nnz.  On rows with sorted columns a gather then
+// touches about a quarter of the x lines it touches when a lane holds 4
+// consecutive nnz (a wave's gather spanning 256 nnz), and the L1 and L2
+// process that many fewer lines: C5 1104 -> 1016 us, C2 55.2 -> 51.3, C4
+// 311 -> 300.  fp16 keeps 4 consecutive nnz per lane (16-byte col loads, 8-byte
+// val loads): its 2-byte val loads would cover only 128 bytes per wave
+// (C2 fp16 34.2 instead of 32.0 us).
+template <typename T>
+constexpr bool strided_layout() { return sizeof(T) >= 4; }
+
+// Offset in its tile of element (k, j) of this lane (k < K / 1024, j < 4).
+template <typename T>
+__device__ __forceinline__ int tile_elem(int k, int j)
+{
+    const int tid = (int)threadIdx.x;
+    return strided_layout<T>() ? k * (4 * kBS) + (tid & ~(kWave - 1)) * 4 + j * kWave + (tid & (kWave - 1))
+                               : 4 * (tid + k * kBS) + j;
+}
 
 template <typename T, int K>
 struct FlatShape {
@@ -1120,8 +1164,15 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B - kb) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B - kb));
 #pragma unroll
-        for (int k = 0; k < VPT; ++k)
-            load4(rc, rv, tid + k * kBS, c[k], v[k]);
+        for (int k = 0; k < VPT; ++k) {
+            if constexpr (strided_layout<T>()) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    load1(rc, rv, tile_elem<T>(k, j), c[k][j], v[k][j]);
+            } else {
+                load4(rc, rv, tid + k * kBS, c[k], v[k]);
+            }
+        }
     }
     if (MODE == kFlatMemo) {
         if (tid == 0) {
@@ -1180,15 +1231,25 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
         const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
-            const int vec = tid + k * kBS;
-            const bool in = 4 * vec < B - kb;
-            P p[4];
+            if constexpr (strided_layout<T>()) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const T xv = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
-                p[j] = P(v[k][j]) * P(xv);  // slots past the tile are never read
+                for (int j = 0; j < 4; ++j) {
+                    const int e = tile_elem<T>(k, j);
+                    const T xv = buf_load(rx, e < B - kb ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
+                                          (T *)nullptr);
+                    s_prod[e] = P(v[k][j]) * P(xv);  // slots past the tile are never read
+                }
+            } else {
+                const int vec = tid + k * kBS;
+                const bool in = 4 * vec < B - kb;
+                P p[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const T xv = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+                    p[j] = P(v[k][j]) * P(xv);  // slots past the tile are never read
+                }
+                store4(s_prod + 4 * vec, p);
             }
-            store4(s_prod + 4 * vec, p);
         }
     }
     lds_sync();
@@ -1305,7 +1366,7 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
     for (int k = 0; k < S::kVPT; ++k) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int g = d.kb + 4 * (tid + k * kBS) + j;
+            const int g = d.kb + tile_elem<T>(k, j);
             const bool use = g >= d.A && g < d.B && g < d.B0;  // slots outside [A, B) are never read
             xv[k][j] = buf_load(rx, use ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
         }
@@ -1325,11 +1386,17 @@ __device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsS
     const int tid = threadIdx.x;
 #pragma unroll
     for (int k = 0; k < S::kVPT; ++k) {
-        P p[4];
+        if constexpr (strided_layout<T>()) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            p[j] = P(v[k][j]) * P(xv[k][j]);
-        store4(s_prod + 4 * (tid + k * kBS), p);
+            for (int j = 0; j < 4; ++j)
+                s_prod[tile_elem<T>(k, j)] = P(v[k][j]) * P(xv[k][j]);
+        } else {
+            P p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                p[j] = P(v[k][j]) * P(xv[k][j]);
+            store4(s_prod + 4 * (tid + k * kBS), p);
+        }
     }
     if (tid < d.nov) s_prod[K + tid] = P(ov) * P(xo);
 #pragma unroll
@@ -1511,8 +1578,15 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B0 - kb) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B0 - kb));
 #pragma unroll
-        for (int k = 0; k < VPT; ++k)
-            load4(rc, rv, tid + k * kBS, c[k], v[k]);
+        for (int k = 0; k < VPT; ++k) {
+            if constexpr (strided_layout<T>()) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    load1(rc, rv, tile_elem<T>(k, j), c[k][j], v[k][j]);
+            } else {
+                load4(rc, rv, tid + k * kBS, c[k], v[k]);
+            }
+        }
     }
     if (MODE != kFlatMemo) {
         if (wave == 2) {  // f: first row with row_ptr >= kb
@@ -2028,6 +2102,50 @@ __global__ __launch_bounds__(kWave) void k_prefree_rows(const int *__restrict__ 
     }
     if (lane == 0)
         out[b] = r;
+}
+
+// ---- gather probe: the x-gather ceiling (measurement only, not an SpMV path) --
+//
+// One workgroup per 1024 indices, as a 1024-nnz FLAT tile: each lane streams
+// 4 indices with one 16-byte non-temporal load (the way col is streamed) and
+// gathers x at them through a resource over x with cache policy AUX; each
+// wave stores one sum, so the gathers cannot be dropped and the stores cost
+// next to nothing.  Run over a matrix's own column indices, it gives the time
+// the x gathers of its SpMV take with nothing else in flight.
+
+constexpr int kProbeTile = 1024;
+
+template <int AUX>
+__device__ __forceinline__ double probe_load(__amdgpu_buffer_rsrc_t r, uint32_t off, double *)
+{
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX));
+}
+
+template <int AUX>
+__device__ __forceinline__ float probe_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, AUX));
+}
+
+template <typename T, int AUX>
+__global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ idx, long long count,
+                                                      const T *__restrict__ x, long long n, T *__restrict__ out)
+{
+    const long long t = blockIdx.x;
+    const long long kb = t * kProbeTile;
+    const long long rest = count - kb;
+    const int len = (int)(rest < kProbeTile ? rest : kProbeTile);
+    const __amdgpu_buffer_rsrc_t ri = make_rsrc(idx + kb, (long long)len * 4);
+    const u32x4 cc = __builtin_amdgcn_raw_buffer_load_b128(ri, (int)threadIdx.x * 16, 0, kAuxNt);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(x, n * (long long)sizeof(T));
+    const int base = 4 * (int)threadIdx.x;
+    const unsigned c[4] = {cc.x, cc.y, cc.z, cc.w};
+    T s = T(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        s += probe_load<AUX>(rx, base + j < len ? c[j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    s = wave_sum(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) out[t * kWaves + threadIdx.x / kWave] = s;
 }
 
 // ---- statistics, fills -----------------------------------------------------
@@ -2570,6 +2688,38 @@ int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int 
         }
     }
     return PF_ERR_UNSUPPORTED;
+}
+
+int pfk_probe_gather(int dtype, const int *idx, long long count, const void *x, long long n, void *out,
+                     long long out_len, int policy, void *stream)
+{
+    if (!idx || !x || !out || count < 1 || count > 0x7FFFFFFFll || n < 1 || ((uintptr_t)idx & 15))
+        return PF_ERR_INVALID;
+    const long long vb = dtype == PF_F64 ? 8 : dtype == PF_F32 ? 4 : 0;
+    if (!vb || n * vb >= (long long)kOob) return PF_ERR_INVALID;
+    const long long tiles = (count + kProbeTile - 1) / kProbeTile;
+    if (out_len < tiles * kWaves) {
+        snprintf(g_err, sizeof g_err, "probe output holds %lld values, %lld needed", out_len, tiles * kWaves);
+        return PF_ERR_INVALID;
+    }
+#define PF_PROBE(AUX)                                                                                          \
+    case AUX:                                                                                                  \
+        if (dtype == PF_F64)                                                                                   \
+            hipLaunchKernelGGL((k_probe_gather<double, AUX>), dim3((unsigned)tiles), dim3(kBS), 0, S(stream), idx, \
+                               count, static_cast<const double *>(x), n, static_cast<double *>(out));          \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_probe_gather<float, AUX>), dim3((unsigned)tiles), dim3(kBS), 0, S(stream), idx,  \
+                               count, static_cast<const float *>(x), n, static_cast<float *>(out));            \
+        break;
+    switch (policy) {
+    PF_PROBE(0) PF_PROBE(1) PF_PROBE(2) PF_PROBE(3) PF_PROBE(16) PF_PROBE(17) PF_PROBE(18) PF_PROBE(19)
+    default:
+        snprintf(g_err, sizeof g_err, "cache policy %d not compiled into the gather probe", policy);
+        return PF_ERR_UNSUPPORTED;
+    }
+#undef PF_PROBE
+    PFK_LAUNCHED("k_probe_gather");
+    return PF_OK;
 }
 
 int pfk_debug_prefree_rows(const int *row_ptr, int m, int nnz, int tile, int *d_out, void *stream)
