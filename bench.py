@@ -228,6 +228,8 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
             p.set_x_windows(args.x_windows)
         if args.chunk_nnz >= 0:
             p.set_chunk_nnz(args.chunk_nnz)
+        if args.ladder and p.info.variant == pf.PREFREE:
+            p.set_ladder(args.ladder)
         return p
 
     t_plan = time.perf_counter()
@@ -272,6 +274,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
         "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
         "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3),
+        "ladder": info["ladder"] if info["variant_name"] == "prefree" else None,
         "steps": steps, "warmup": warmup,
         "launch": ("one captured HIP graph of the timed steps" if use_graph else "eager launches from Python")
                   + f"; eager warm-up step {warm_us:.1f} us",
@@ -473,6 +476,8 @@ def main():
                     help="split-row FLAT: force the x-window tile schedule off (0) or on (1); -1 = the plan's choice")
     ap.add_argument("--chunk-nnz", type=int, default=-1,
                     help="FLAT 1024/2048: nnz per XCD chunk of tiles (0 = one chunk per XCD); -1 = the plan's choice")
+    ap.add_argument("--ladder", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
+                    help="PREFREE: the reference's reduction ladder 1..5 (0 = its active ladder, 3)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--legs", default="rotated,cold,search,host",
                     help="legs measured besides the hot steps (comma list of rotated, cold, search, host)")

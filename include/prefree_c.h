@@ -90,6 +90,7 @@ typedef struct pf_plan_info {
                              start in (chosen when rows span 4+ tiles and x exceeds one XCD's 4 MB L2) */
     long long chunk_nnz;  /* FLAT 1024/2048 without x windows: tiles dealt to the 8 XCDs in chunks of
                              consecutive tiles of about this many nnz (0 = one chunk per XCD) */
+    int ladder;           /* PREFREE: the reduction ladder 1..5 (see pf_plan_set_ladder); 0 otherwise */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -134,6 +135,16 @@ int pf_plan_set_x_windows(pf_plan *plan, int x_windows);
  * of the tiles per XCD).  Small chunks keep the eight XCDs streaming neighbouring addresses; large ones
  * keep more of a row's x neighbourhood in one XCD's L2.  All values give the same y. */
 int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
+/* PREFREE only: the per-tile reduction ladder, the reference tuner's TEST_CODE_VERSION
+ * (scripts/profile_and_generate.py:109-235, ladders at src/spmv_kernel/preFreeSpMV.cu:440-559):
+ *   1 thread per row always; 2 block for a single-row tile, else thread per row;
+ *   3 (default, the reference's active ladder) thread per row above 32 rows, block for one row,
+ *     else 4 lanes per row;
+ *   4 as 3, but a tile of 2..32 rows whose longest row holds over 90% of their nnz sums it with 96
+ *     threads and the other rows with one thread each (red_row_long_short_specialized);
+ *   5 thread per row above 128 rows, block for one row, else groups of 128/rows lanes (2..32) per row.
+ * The tile size (pf_plan_create_tuned: 512 or 1024 nnz) is the reference's P_NNZ 4 or 8. */
+int pf_plan_set_ladder(pf_plan *plan, int ladder);
 /* FLAT 1024/2048: 1 (default) = the first call records each tile's first row and later calls read it;
  * 0 = every call searches row_ptr inside the tile kernel (no recorded map, tiles dealt to XCDs by
  * position).  Both give the same y.  The reference times its own row map as a separate pre-pass

@@ -58,7 +58,23 @@ typedef struct pfk_spmv_args {
     long long chunk_nnz; /* FLAT 1024/2048 without a schedule: the tiles go to the 8 XCDs in chunks of
                             consecutive tiles of about chunk_nnz nnz, chunk i to XCD i % 8; 0 = one chunk
                             of ceil(ntiles / 8) tiles per XCD */
+    int ladder;          /* PREFREE: reduction ladder 1..5, the reference tuner's TEST_CODE_VERSION
+                            (scripts/profile_and_generate.py:109-235); 0 = 3, the active ladder of
+                            preFreeSpMV.cu:466-483 */
+    /* Bytes the caller allocated behind each workspace pointer.  Every entry point checks them before
+     * any launch against what its kernels touch: head and tail ntiles slots of PFK_SLOT_BYTES(dtype),
+     * owner ntiles ints (ADAPTIVE, split-row FLAT, the combine kernel, pfk_adaptive_owners), the row
+     * map 8 * (ntiles + 1) bytes and the schedule PFK_SCHED_INTS(ntiles, sched_cap) ints when given;
+     * a shortfall is PF_ERR_INVALID with nothing launched. */
+    size_t head_bytes;
+    size_t tail_bytes;
+    size_t owner_bytes;
+    size_t row_map_bytes;
+    size_t sched_bytes;
 } pfk_spmv_args;
+
+/* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
+#define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
 
 /* Ints of an x-window schedule. */
 #define PFK_SCHED_INTS(ntiles, cap) (16 + 8 * (cap) + (ntiles))

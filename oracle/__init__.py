@@ -43,6 +43,10 @@ def lib() -> ctypes.CDLL:
                                             ctypes.c_int, ctypes.c_int, _ip, _ip]
         L.oracle_prefree_sim_f64.argtypes = [_dp, _ip, _ip, _dp, _dp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                              ctypes.c_int]
+        L.oracle_prefree_sim_code_f64.argtypes = [_dp, _ip, _ip, _dp, _dp] + [ctypes.c_int] * 6 + [_ip, _ip]
+        L.oracle_prefree_sim_code_f64.restype = ctypes.c_int
+        L.oracle_prefree_vector_size.argtypes = [ctypes.c_int]
+        L.oracle_prefree_vector_size.restype = ctypes.c_int
         L.oracle_eqcheck_f64.argtypes = [_dp, _dp, ctypes.c_int, ctypes.c_double]
         L.oracle_eqcheck_f64.restype = ctypes.c_longlong
         for f in (L.oracle_bytes_effective, L.oracle_bytes_gather):
@@ -117,16 +121,32 @@ def tile_row_range(row_ptr, tile, start_row, b, faithful_sentinel=False):
     return s.value, e.value
 
 
-def prefree_sim(row_ptr, col, val, x, faithful_sentinel=False, reverse_tiles=False):
-    """One execution of preFreeSpMV_kernel<4,128> (preFreeSpMV.cu:407-483) on the CPU."""
+def prefree_sim(row_ptr, col, val, x, faithful_sentinel=False, reverse_tiles=False, code=3, p_nnz=4, y=None,
+                counts=False):
+    """One execution of preFreeSpMV_kernel<p_nnz,128> with reduction ladder `code`
+    (preFreeSpMV.cu:407-561; code 3 is the active ladder :466-483, 1/2/4/5 the
+    tuner's alternatives :440-461 and :485-559) on the CPU.  y defaults to zeros
+    (the reference memsets it, :644).  counts=True also returns, per row, the
+    number of plain stores and of atomic adds it received."""
     _check_csr(row_ptr, col)
     assert val.dtype == np.float64
     m = len(row_ptr) - 1
-    y = np.zeros(m, dtype=np.float64)
-    lib().oracle_prefree_sim_f64(_ptr(val, ctypes.c_double), _ptr(row_ptr, ctypes.c_int), _ptr(col, ctypes.c_int),
-                                 _ptr(x, ctypes.c_double), _ptr(y, ctypes.c_double), m, int(row_ptr[-1]),
-                                 int(bool(faithful_sentinel)), int(bool(reverse_tiles)))
-    return y
+    y = np.zeros(m, dtype=np.float64) if y is None else np.array(y, dtype=np.float64, copy=True)
+    plain = np.zeros(max(m, 1), dtype=np.int32)
+    atomics = np.zeros(max(m, 1), dtype=np.int32)
+    st = lib().oracle_prefree_sim_code_f64(_ptr(val, ctypes.c_double), _ptr(row_ptr, ctypes.c_int),
+                                           _ptr(col, ctypes.c_int), _ptr(x, ctypes.c_double),
+                                           _ptr(y, ctypes.c_double), m, int(row_ptr[-1]), int(code), int(p_nnz),
+                                           int(bool(faithful_sentinel)), int(bool(reverse_tiles)),
+                                           _ptr(plain, ctypes.c_int), _ptr(atomics, ctypes.c_int))
+    if st != 0:
+        raise ValueError(f"unknown ladder code {code} or P_NNZ {p_nnz}")
+    return (y, plain[:m], atomics[:m]) if counts else y
+
+
+def prefree_vector_size(n):
+    """calculate_vector_size<128>, preFreeSpMV.cu:394-405 (0 for n <= 0)."""
+    return int(lib().oracle_prefree_vector_size(int(n)))
 
 
 def eqcheck(ref, ours, tol=1e-8):

@@ -130,11 +130,21 @@ void oracle_tile_row_range(const int *row_ptr, int m, int tile, const int *start
     *end = e;
 }
 
-/* ---- one execution of preFreeSpMV_kernel<4,128>, preFreeSpMV.cu:407-483 --- */
+/* ---- one execution of preFreeSpMV_kernel<P_NNZ,128>, preFreeSpMV.cu:407-561 --
+ *
+ * The reduction ladder is selected by `code`, the tuner's TEST_CODE_VERSION
+ * (scripts/profile_and_generate.py:109-235): 1 = red_row_thread only (:440-446),
+ * 2 = block / thread (:448-461), 3 = thread / block / vector<4> (:466-483, the
+ * active ladder), 4 = as 3 with red_row_long_short_specialized<96> for
+ * imbalanced tiles (:485-511 with :152-392), 5 = thread / block / vector<VS>
+ * with VS from calculate_vector_size (:513-559, :394-405).  Every warp-level
+ * tree is restated as lane 0 of a 32-lane warp sees it.  Tiles run one after
+ * the other (reverse_tiles: last first), so atomicAdd becomes a plain += in
+ * that order.  `plain` (optional, m ints) counts the rows' non-atomic stores
+ * and `atomics` (optional) their atomic adds. */
 
 #define SIM_BLOCK 128
-#define SIM_PNNZ 4
-#define SIM_TILE (SIM_BLOCK * SIM_PNNZ)
+#define SIM_TILE_MAX (SIM_BLOCK * 8)
 
 /* warpReduceSum tree seen by lane 0 of a 32-lane warp (offsets 16..1),
  * preFreeSpMV.cu:49-53 and :100-114. */
@@ -148,69 +158,245 @@ static double warp32_lane0(const double *v)
     return y2[0] + y2[1];
 }
 
-void oracle_prefree_sim_f64(const double *val, const int *row_ptr, const int *col,
-                            const double *x, double *y, int m, int nnz, int faithful_sentinel,
-                            int reverse_tiles)
+/* warpReduceSum<VS> (:100-114) seen by lane 0 of a VS-lane group: offsets VS/2..1. */
+static double group_lane0(double *v, int vs)
 {
+    for (int o = vs / 2; o >= 1; o /= 2)
+        for (int i = 0; i < o; i++) v[i] = v[i] + v[i + o];
+    return v[0];
+}
+
+typedef struct {
+    const int *rp;
+    const double *s;
+    double *y;
+    int *plain, *atomics;
+    int base, tile, start, end;
+} sim_tile;
+
+static void sim_range(const sim_tile *t, int r, int *a, int *e)
+{
+    int lo = t->rp[r] - t->base; if (lo < 0) lo = 0;
+    int hi = t->rp[r + 1] - t->base; if (hi > t->tile) hi = t->tile;
+    *a = lo;
+    *e = hi;
+}
+
+static void sim_put(const sim_tile *t, int r, double sum)
+{
+    if (r == t->start || r == t->end - 1) {
+        t->y[r] += sum;                   /* atomicAdd */
+        if (t->atomics) t->atomics[r]++;
+    } else {
+        t->y[r] = sum;
+        if (t->plain) t->plain[r]++;
+    }
+}
+
+/* red_row_thread, :71-98 */
+static void sim_thread(const sim_tile *t)
+{
+    for (int r = t->start; r < t->end; r++) {
+        int a, e;
+        sim_range(t, r, &a, &e);
+        double sum = 0;
+        for (int i = a; i < e; i++) sum += t->s[i];
+        sim_put(t, r, sum);
+    }
+}
+
+/* red_row_block, :30-69 (always an atomicAdd) */
+static void sim_block(const sim_tile *t)
+{
+    const int r = t->start;
+    int a, e;
+    sim_range(t, r, &a, &e);
+    double th[SIM_BLOCK];
+    for (int k = 0; k < SIM_BLOCK; k++) {
+        double acc = 0;
+        for (int j = a + k; j < e; j += SIM_BLOCK) acc += t->s[j];
+        th[k] = acc;
+    }
+    double fin = 0;
+    for (int w = 0; w < SIM_BLOCK / 32; w++) fin += warp32_lane0(th + 32 * w);
+    t->y[r] += fin;
+    if (t->atomics) t->atomics[r]++;
+}
+
+/* red_row_vector<VS>, :116-150 */
+static void sim_vector(const sim_tile *t, int vs)
+{
+    for (int r = t->start; r < t->end; r++) {
+        int a, e;
+        sim_range(t, r, &a, &e);
+        double l[32];
+        for (int q = 0; q < vs; q++) {
+            double acc = 0;
+            for (int i = a + q; i < e; i += vs) acc += t->s[i];
+            l[q] = acc;
+        }
+        sim_put(t, r, group_lane0(l, vs));
+    }
+}
+
+/* is_imbalanced_warp, :342-373: the longest of the first 32 rows (whole row
+ * lengths) holds more than 90% of their nnz, compared in float. */
+static int sim_imbalanced(const sim_tile *t)
+{
+    const int n = t->end - t->start;
+    long long total = 0;
+    int mx = 0;
+    for (int lane = 0; lane < 32; lane++) {
+        int len = 0;
+        if (lane < n) len = t->rp[t->start + lane + 1] - t->rp[t->start + lane];
+        total += len;
+        if (len > mx) mx = len;
+    }
+    const float dominance = 0.9f;
+    return n > 1 && total > 0 && (float)mx > (float)(int)total * dominance;
+}
+
+/* red_row_long_short_specialized<96>, :152-340 (called with 2 <= n <= 32) */
+static void sim_long_short(const sim_tile *t)
+{
+    const int n = t->end - t->start;
+    /* phase 1: longest row by a shfl_down max-with-index tree; a lane past the
+     * warp's end keeps its own value; a tie keeps the lane's own index */
+    int len[32], idx[32];
+    for (int lane = 0; lane < 32; lane++) {
+        len[lane] = lane < n ? t->rp[t->start + lane + 1] - t->rp[t->start + lane] : -1;
+        idx[lane] = lane;
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+        int nl[32], ni[32];
+        for (int lane = 0; lane < 32; lane++) {
+            const int src = lane + o < 32 ? lane + o : lane;
+            nl[lane] = len[lane];
+            ni[lane] = idx[lane];
+            if (len[src] > len[lane]) { nl[lane] = len[src]; ni[lane] = idx[src]; }
+        }
+        memcpy(len, nl, sizeof len);
+        memcpy(idx, ni, sizeof idx);
+    }
+    const int li = idx[0];
+    double fin_sums[32];
+    for (int i = 0; i < 32; i++) fin_sums[i] = 0.0;
+    /* phase 2, team A: 96 threads stride the long row; one tree per 32-lane warp */
+    double th[96];
+    {
+        int a, e;
+        sim_range(t, t->start + li, &a, &e);
+        for (int k = 0; k < 96; k++) {
+            double acc = 0;
+            for (int j = a + k; j < e; j += 96) acc += t->s[j];
+            th[k] = acc;
+        }
+    }
+    double wsum[3];
+    for (int w = 0; w < 3; w++) wsum[w] = warp32_lane0(th + 32 * w);
+    /* phase 2, team B: one thread per other row, short sums unrolled left to right */
+    for (int i = 0; i < n; i++) {
+        if (i == li) continue;
+        int a, e;
+        sim_range(t, t->start + i, &a, &e);
+        const int l = e - a;
+        const double *s = t->s;
+        double sum = 0;
+        switch (l) {
+        case 1: sum = s[a]; break;
+        case 2: sum = s[a] + s[a + 1]; break;
+        case 3: sum = s[a] + s[a + 1] + s[a + 2]; break;
+        case 4: sum = s[a] + s[a + 1] + s[a + 2] + s[a + 3]; break;
+        case 0: break;
+        default:
+            for (int k = a; k < e; k++) sum += s[k];
+            break;
+        }
+        fin_sums[i] = sum;
+    }
+    /* phase 3: the three warp sums through one more 32-lane tree */
+    double v[32];
+    for (int i = 0; i < 32; i++) v[i] = i < 3 ? wsum[i] : 0.0;
+    fin_sums[li] = warp32_lane0(v);
+    /* phase 4: rows whose sum is 0.0 are not written */
+    for (int i = 0; i < n; i++) {
+        if (fin_sums[i] == 0.0) continue;
+        sim_put(t, t->start + i, fin_sums[i]);
+    }
+}
+
+/* calculate_vector_size<128>, :394-405 */
+static int sim_vector_size(int n)
+{
+    if (n >= SIM_BLOCK) return 2;
+    const unsigned avg = (unsigned)SIM_BLOCK / (unsigned)n;
+    unsigned p2 = 1;
+    while (p2 * 2 <= avg) p2 *= 2;
+    return p2 > 32 ? 32 : (p2 < 2 ? 2 : (int)p2);
+}
+
+int oracle_prefree_sim_code_f64(const double *val, const int *row_ptr, const int *col, const double *x, double *y,
+                                int m, int nnz, int code, int p_nnz, int faithful_sentinel, int reverse_tiles,
+                                int *plain, int *atomics)
+{
+    if (code < 1 || code > 5 || (p_nnz != 4 && p_nnz != 8))
+        return -1;
     if (nnz <= 0 || m <= 0)
-        return;
-    const int G = (nnz + SIM_TILE - 1) / SIM_TILE;
+        return 0;
+    const int T = SIM_BLOCK * p_nnz;
+    const int G = (nnz + T - 1) / T;
     int *start_row = (int *)malloc(sizeof(int) * (size_t)(G + 1));
-    oracle_pre_start_row(row_ptr, m, SIM_TILE, start_row, G);
-    double s[SIM_TILE];
+    oracle_pre_start_row(row_ptr, m, T, start_row, G);
+    double s[SIM_TILE_MAX];
     const int last = row_ptr[m] - 1; /* :410 */
     for (int bi = 0; bi < G; bi++) {
         const int b = reverse_tiles ? G - 1 - bi : bi;
-        const int base = b * SIM_TILE;
-        for (int k = 0; k < SIM_TILE; k++) { /* :416-428 */
+        const int base = b * T;
+        for (int k = 0; k < T; k++) { /* :416-428 */
             int g = base + k;
             if (g > last) g = last;
             s[k] = val[g] * x[col[g]];
         }
-        int start, end;
-        oracle_tile_row_range(row_ptr, m, SIM_TILE, start_row, G, b, faithful_sentinel, &start, &end);
-        const int n = end - start;
-        if (n > SIM_BLOCK / 4) {
-            /* red_row_thread, :71-98 */
-            for (int r = start; r < end; r++) {
-                int a = row_ptr[r] - base; if (a < 0) a = 0;
-                int e = row_ptr[r + 1] - base; if (e > SIM_TILE) e = SIM_TILE;
-                double sum = 0;
-                for (int i = a; i < e; i++) sum += s[i];
-                if (r == start || r == end - 1) y[r] += sum; else y[r] = sum;
-            }
-        } else if (n == 1) {
-            /* red_row_block, :30-69 */
-            const int r = start;
-            int a = row_ptr[r] - base; if (a < 0) a = 0;
-            int e = row_ptr[r + 1] - base; if (e > SIM_TILE) e = SIM_TILE;
-            double th[SIM_BLOCK];
-            for (int t = 0; t < SIM_BLOCK; t++) {
-                double acc = 0;
-                for (int j = a + t; j < e; j += SIM_BLOCK) acc += s[j];
-                th[t] = acc;
-            }
-            double fin = 0;
-            for (int w = 0; w < SIM_BLOCK / 32; w++) fin += warp32_lane0(th + 32 * w);
-            y[r] += fin;
-        } else if (n > 0) {
-            /* red_row_vector<VECTOR_SIZE=4>, :116-150 */
-            for (int r = start; r < end; r++) {
-                int a = row_ptr[r] - base; if (a < 0) a = 0;
-                int e = row_ptr[r + 1] - base; if (e > SIM_TILE) e = SIM_TILE;
-                double l[4];
-                for (int q = 0; q < 4; q++) {
-                    double acc = 0;
-                    for (int i = a + q; i < e; i += 4) acc += s[i];
-                    l[q] = acc;
-                }
-                const double sum = (l[0] + l[2]) + (l[1] + l[3]);
-                if (r == start || r == end - 1) y[r] += sum; else y[r] = sum;
-            }
+        sim_tile t = {row_ptr, s, y, plain, atomics, base, T, 0, 0};
+        oracle_tile_row_range(row_ptr, m, T, start_row, G, b, faithful_sentinel, &t.start, &t.end);
+        const int n = t.end - t.start;
+        switch (code) {
+        case 1:
+            sim_thread(&t);
+            break;
+        case 2:
+            if (n == 1) sim_block(&t); else sim_thread(&t);
+            break;
+        case 3:
+            if (n > SIM_BLOCK / 4) sim_thread(&t);
+            else if (n == 1) sim_block(&t);
+            else sim_vector(&t, 4);
+            break;
+        case 4:
+            if (n > SIM_BLOCK / 4) sim_thread(&t);
+            else if (n == 1) sim_block(&t);
+            else if (sim_imbalanced(&t)) sim_long_short(&t);
+            else sim_vector(&t, 4);
+            break;
+        case 5:
+            if (n > SIM_BLOCK) sim_thread(&t);
+            else if (n == 1) sim_block(&t);
+            else if (n > 0) sim_vector(&t, sim_vector_size(n));
+            break;
         }
     }
     free(start_row);
+    return 0;
 }
+
+void oracle_prefree_sim_f64(const double *val, const int *row_ptr, const int *col,
+                            const double *x, double *y, int m, int nnz, int faithful_sentinel,
+                            int reverse_tiles)
+{
+    oracle_prefree_sim_code_f64(val, row_ptr, col, x, y, m, nnz, 3, 4, faithful_sentinel, reverse_tiles, NULL, NULL);
+}
+
+int oracle_prefree_vector_size(int n) { return n > 0 ? sim_vector_size(n) : 0; }
 
 /* ---- eQcheck, test/test_cdspmv.cpp:22-54 ---------------------------------- */
 

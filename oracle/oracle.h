@@ -61,6 +61,14 @@ void oracle_tile_row_range(const int *row_ptr, int m, int tile, const int *start
 void oracle_prefree_sim_f64(const double *val, const int *row_ptr, const int *col,
                             const double *x, double *y, int m, int nnz, int faithful_sentinel,
                             int reverse_tiles);
+/* preFreeSpMV_kernel<p_nnz,128> with reduction ladder `code` (1..5, the tuner's
+ * TEST_CODE_VERSION), p_nnz 4 or 8; plain / atomics (optional, m ints) count each
+ * row's plain stores and atomic adds.  Returns -1 for an unknown code or p_nnz. */
+int oracle_prefree_sim_code_f64(const double *val, const int *row_ptr, const int *col, const double *x, double *y,
+                                int m, int nnz, int code, int p_nnz, int faithful_sentinel, int reverse_tiles,
+                                int *plain, int *atomics);
+/* calculate_vector_size<128> (preFreeSpMV.cu:394-405) for n rows, 0 for n <= 0. */
+int oracle_prefree_vector_size(int n);
 
 /* eQcheck, test/test_cdspmv.cpp:22-54 (fp64 branch): number of i with
  * |a-b|/max(|a|,|b|) > tol (a NaN comparison counts as a pass, as there). */

@@ -60,7 +60,7 @@ class PlanInfo(ctypes.Structure):
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
                 ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
-                ("chunk_nnz", ctypes.c_longlong)]
+                ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -92,7 +92,9 @@ class SpmvArgs(ctypes.Structure):
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong), ("head_slot", ctypes.c_void_p), ("tail_slot", ctypes.c_void_p),
                 ("owner_row", ctypes.c_void_p), ("err_flag", ctypes.c_void_p), ("row_map", ctypes.c_void_p),
                 ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int), ("sched", ctypes.c_void_p),
-                ("sched_cap", ctypes.c_longlong), ("chunk_nnz", ctypes.c_longlong)]
+                ("sched_cap", ctypes.c_longlong), ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int),
+                ("head_bytes", ctypes.c_size_t), ("tail_bytes", ctypes.c_size_t), ("owner_bytes", ctypes.c_size_t),
+                ("row_map_bytes", ctypes.c_size_t), ("sched_bytes", ctypes.c_size_t)]
 
 
 _lib = None
@@ -129,6 +131,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_x_windows, [_vp, _i])
         _sig(L.pf_plan_set_chunk_nnz, [_vp, _ll])
         _sig(L.pf_plan_set_remember_rows, [_vp, _i])
+        _sig(L.pf_plan_set_ladder, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -164,6 +167,10 @@ def klib() -> ctypes.CDLL:
         K = ctypes.CDLL(KLIB_PATH)
         _sig(K.pfk_debug_tile_desc, [_i, _i, ctypes.POINTER(SpmvArgs), _vp, _vp])
         _sig(K.pfk_adaptive_owners, [_i, ctypes.POINTER(SpmvArgs), _vp])
+        _sig(K.pfk_spmv_flat, [_i, ctypes.POINTER(SpmvArgs), _vp])
+        _sig(K.pfk_spmv_adaptive, [_i, ctypes.POINTER(SpmvArgs), _vp])
+        _sig(K.pfk_spmv_fixup, [_i, _i, ctypes.POINTER(SpmvArgs), _vp])
+        _sig(K.pfk_spmv_prefree, [_i, ctypes.POINTER(SpmvArgs), _vp])
         _sig(K.pfk_debug_prefree_rows, [_vp, _i, _i, _i, _vp, _vp])
         _sig(K.pfk_adaptive_long_row_min, [_i, _i])
         _sig(K.pfk_supported_tiles, [_i, _i, ctypes.POINTER(_i), _i])
@@ -283,6 +290,10 @@ class Plan:
     def set_chunk_nnz(self, chunk_nnz):
         _check(lib().pf_plan_set_chunk_nnz(self._h, int(chunk_nnz)), "pf_plan_set_chunk_nnz")
 
+    def set_ladder(self, ladder):
+        """pf_plan_set_ladder: PREFREE reduction ladder 1..5 (the reference tuner's code)."""
+        _check(lib().pf_plan_set_ladder(self._h, int(ladder)), "pf_plan_set_ladder")
+
     def set_remember_rows(self, remember):
         """pf_plan_set_remember_rows: False = every call searches row_ptr (no recorded row map)."""
         _check(lib().pf_plan_set_remember_rows(self._h, int(bool(remember))), "pf_plan_set_remember_rows")
@@ -336,7 +347,8 @@ def adaptive_owners(row_ptr, m, nnz, tile, out, err_flag, dtype="f64", guess_spr
     """pfk_adaptive_owners: split-row owner of every ADAPTIVE tile into `out` (int32[ntiles])."""
     ntiles = max(1, -(-(nnz + m) // tile))
     a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
-                 run_tiles=run_tiles, ntiles=ntiles, owner_row=_p(out), err_flag=_p(err_flag))
+                 run_tiles=run_tiles, ntiles=ntiles, owner_row=_p(out), err_flag=_p(err_flag),
+                 owner_bytes=int(out.numel()) * 4)
     _check(klib().pfk_adaptive_owners(dtype_code(dtype), ctypes.byref(a), _s(stream)), "pfk_adaptive_owners")
     return ntiles
 

@@ -130,4 +130,44 @@ __device__ int wave_search_lt(const int *__restrict__ rp, int m, uint32_t v, lon
     return (int)lo;
 }
 
+// wave_search_lt for row_ptr itself (keys = row_ptr[r]), also returning
+// row_ptr[result + 1]: the final round of the search probes that entry in
+// most cases, and a lane's probe is read back instead of loaded again; only
+// otherwise is it loaded.  Same preconditions; v > 0 and result + 1 <= m.
+__device__ __forceinline__ int wave_search_lt_next(const int *__restrict__ rp, int m, uint32_t v, long long guess,
+                                                   int spread, int lane, int &next_key)
+{
+    long long lo = 0, hi = m;
+    if (spread > 0) {
+        const long long p = guess + (long long)(lane - 32) * spread;
+        const bool valid = p > lo && p < hi;
+        const uint32_t k = valid ? (uint32_t)rp[(int)p] : 0u;
+        const uint64_t okm = __ballot(valid && k < v);
+        const uint64_t badm = __ballot(valid && k >= v);
+        long long nlo = lo, nhi = hi;
+        if (okm) nlo = guess + (long long)(63 - __clzll(okm) - 32) * spread;
+        if (badm) nhi = guess + (long long)(__ffsll((long long)badm) - 1 - 32) * spread;
+        if (nlo < nhi) { lo = nlo; hi = nhi; }
+    }
+    bool have = false;
+    int key = 0;
+    while (hi - lo > 1) {
+        const long long step = (hi - lo + 63) >> 6;
+        const long long p = lo + (long long)lane * step;
+        const bool probe = lane > 0 && p < hi;
+        const int k = probe ? rp[(int)p] : 0;
+        const bool ok = probe && (uint32_t)k < v;
+        const int c = __popcll(__ballot(ok));
+        // lo + (c + 1) * step is the first probe at or past v, if it was made
+        if (step == 1 && c + 1 < kWave && lo + c + 1 < hi) {
+            have = true;
+            key = __builtin_amdgcn_readlane(k, c + 1);
+        }
+        lo += (long long)c * step;
+        hi = (lo + step < hi) ? lo + step : hi;
+    }
+    next_key = have ? key : rp[(int)lo + 1];
+    return (int)lo;
+}
+
 }  // namespace pfdev

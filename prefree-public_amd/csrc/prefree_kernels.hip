@@ -174,6 +174,34 @@ __device__ __forceinline__ long long val_range_bytes(int count)
     return (((long long)count * (long long)sizeof(T)) + 3) & ~3ll;
 }
 
+// Scalar loads through a resource (x gathers, overflow values); an offset
+// outside the resource reads zero.
+constexpr uint32_t kOob = 0xFFFFFFF0u;  // byte offset beyond every resource
+
+__device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, double *)
+{
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ half_t buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, half_t *)
+{
+    return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0));
+}
+
+
+// A resource over a whole array addressed with 32-bit byte offsets (the plan
+// guarantees it stays below 4 GiB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_full(const void *base, long long bytes)
+{
+    const long long b = bytes < 0 ? 0 : (bytes > (long long)kOob ? (long long)kOob : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)(unsigned int)b, kRsrcWord3);
+}
+
 // col and val of the 4 consecutive nnz at 16-byte vector `vec` of a resource pair.
 template <int AUX = kAuxNt>
 __device__ __forceinline__ void load4(__amdgpu_buffer_rsrc_t rc, __amdgpu_buffer_rsrc_t rv, int vec, int (&c)[4],
@@ -368,17 +396,19 @@ __device__ __forceinline__ void issue_cv(const Args<T> &a, int base, int B, int 
             load4(rc, rv, (int)threadIdx.x + k * kBS, c[k], v[k]);
 }
 
-// Gather x (ordinary loads: x stays in L2 / MALL).  Lanes past the tile hold
-// column 0 and gather x[0]; their products are masked later.
+// Gather x (ordinary loads: x stays in L2 / MALL) through a resource over
+// x[0, n): a column outside [0, n) reads zero instead of memory past x.  Lanes
+// past the tile hold column 0 and gather x[0]; their products are masked later.
 template <typename T, int VPT>
 __device__ __forceinline__ void gather_x(const Args<T> &a, int nvec, const int (&c)[VPT][4], T (&xv)[VPT][4])
 {
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
         if (k * kBS < nvec)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                xv[k][j] = a.x[c[k][j]];
+                xv[k][j] = buf_load(rx, (uint32_t)c[k][j] * (uint32_t)sizeof(T), (T *)nullptr);
 }
 
 // val * x, rounded, into LDS (no contraction with the later sums).
@@ -564,7 +594,6 @@ __global__ __launch_bounds__(kBS) void k_tiles(Args<T> a)
 // compiler can then count outstanding operations exactly and waits only for
 // the data it consumes, so the next tiles' loads stay in flight.
 
-constexpr uint32_t kOob = 0xFFFFFFF0u;  // byte offset beyond every resource
 #ifndef PF_STORE_AUX
 #define PF_STORE_AUX 0
 #endif
@@ -599,30 +628,6 @@ __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t o
 {
     const u32x4 v = {__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]), __float_as_uint(w[3])};
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kStoreAux);
-}
-
-__device__ __forceinline__ double buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, double *)
-{
-    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
-}
-
-__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, float *)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
-}
-
-__device__ __forceinline__ half_t buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, half_t *)
-{
-    return __builtin_bit_cast(half_t, __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0));
-}
-
-
-// A resource over a whole array addressed with 32-bit byte offsets (the plan
-// guarantees it stays below 4 GiB).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_full(const void *base, long long bytes)
-{
-    const long long b = bytes < 0 ? 0 : (bytes > (long long)kOob ? (long long)kOob : bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)(unsigned int)b, kRsrcWord3);
 }
 
 __device__ __forceinline__ int rlane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
@@ -1160,6 +1165,7 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
 
     int c[VPT][4];
     T v[VPT][4];
+    T xv[VPT][4];
     if (!DESC) {
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B - kb) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B - kb));
@@ -1173,6 +1179,17 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
                 load4(rc, rv, tid + k * kBS, c[k], v[k]);
             }
         }
+        // The x gathers depend on col only: they are issued before the rows
+        // are known and stay in flight across the row search (or the row map
+        // read) and its barrier, which fences LDS only.  Slots past the tile
+        // read nothing and are never summed.
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                xv[k][j] = buf_load(rx, tile_elem<T>(k, j) < B - kb ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
+                                    (T *)nullptr);
     }
     if (MODE == kFlatMemo) {
         if (tid == 0) {
@@ -1183,18 +1200,20 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     } else if (wave == 2) {  // f: first row with row_ptr >= kb
         if (MODE == kFlatSearch && a.sched && lane == 0)
             sched_record(a.sched, a.sched_cap, t, kb < nnz ? a.col[kb] : 0, a.n);
-        const int f = wave_search_lt<false>(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
-                                            a.guess_spread, lane) + 1;
+        int rpf = 0;
+        const int f = kb == 0 ? (rpf = a.rp[0], 0)
+                              : wave_search_lt_next(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
+                                                    a.guess_spread, lane, rpf) + 1;
         if (lane == 0) {
-            const int rpf = a.rp[f];
             s_info[0] = f; s_info[1] = rpf;
             if (MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(f, rpf);
         }
     } else if (wave == 3) {  // l: first row with row_ptr >= ke (m for the last tile)
-        const int l = last ? m
-                           : wave_search_lt<false>(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane) + 1;
+        int rpl = 0;
+        const int l = last ? (rpl = a.rp[m], m)
+                           : wave_search_lt_next(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane,
+                                                 rpl) + 1;
         if (lane == 0) {
-            const int rpl = a.rp[l];
             s_info[2] = l; s_info[3] = rpl;
             if (MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(l, rpl);
         }
@@ -1227,29 +1246,18 @@ __global__ __launch_bounds__(kBS) void k_flat(Args<T> a, int *__restrict__ map, 
     // Row bounds into LDS (global row_ptr is read directly beyond kRpCap).
     for (int i = tid; i <= nr && i < S::kRpCap; i += kBS)
         s_rp[i] = a.rp[lo_row + i];
-    {
-        const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
 #pragma unroll
-        for (int k = 0; k < VPT; ++k) {
-            if constexpr (strided_layout<T>()) {
+    for (int k = 0; k < VPT; ++k) {
+        if constexpr (strided_layout<T>()) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int e = tile_elem<T>(k, j);
-                    const T xv = buf_load(rx, e < B - kb ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
-                                          (T *)nullptr);
-                    s_prod[e] = P(v[k][j]) * P(xv);  // slots past the tile are never read
-                }
-            } else {
-                const int vec = tid + k * kBS;
-                const bool in = 4 * vec < B - kb;
-                P p[4];
+            for (int j = 0; j < 4; ++j)
+                s_prod[tile_elem<T>(k, j)] = P(v[k][j]) * P(xv[k][j]);
+        } else {
+            P p[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const T xv = buf_load(rx, in ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
-                    p[j] = P(v[k][j]) * P(xv);  // slots past the tile are never read
-                }
-                store4(s_prod + 4 * vec, p);
-            }
+            for (int j = 0; j < 4; ++j)
+                p[j] = P(v[k][j]) * P(xv[k][j]);
+            store4(s_prod + 4 * (tid + k * kBS), p);
         }
     }
     lds_sync();
@@ -1590,19 +1598,21 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     }
     if (MODE != kFlatMemo) {
         if (wave == 2) {  // f: first row with row_ptr >= kb
-            const int ff = wave_search_lt<false>(a.rp, m, (uint32_t)kb, key_guess<false>((uint32_t)kb, m, nnz),
-                                                 a.guess_spread, lane) + 1;
+            int r = 0;
+            const int ff = kb == 0 ? (r = a.rp[0], 0)
+                                   : wave_search_lt_next(a.rp, m, (uint32_t)kb,
+                                                         key_guess<false>((uint32_t)kb, m, nnz), a.guess_spread,
+                                                         lane, r) + 1;
             if (lane == 0) {
-                const int r = a.rp[ff];
                 s_info[0] = ff; s_info[1] = r;
                 if (MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
             }
         } else if (wave == 3) {  // l: first row with row_ptr >= ke (m for the last tile)
-            const int ll = last ? m
-                                : wave_search_lt<false>(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread,
-                                                        lane) + 1;
+            int r = 0;
+            const int ll = last ? (r = a.rp[m], m)
+                                : wave_search_lt_next(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane,
+                                                      r) + 1;
             if (lane == 0) {
-                const int r = a.rp[ll];
                 s_info[2] = ll; s_info[3] = r;
                 if (MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
             }
@@ -1970,14 +1980,229 @@ __device__ __forceinline__ T half_wave_tree(T v)
 template <typename T>
 __device__ __forceinline__ void atomic_add(T *p, T v) { atomicAdd(p, v); }
 
-template <typename T, int P>
+// Sum over the aligned groups of V lanes of each 32-lane half, as lane 0 of a
+// group sees the reference's warpReduceSum<V> (__shfl_down_sync offsets V/2 ..
+// 1, preFreeSpMV.cu:100-114): an xor tree from the largest offset down gives
+// lane 0 the same additions in the same order.
+template <int V, typename T>
+__device__ __forceinline__ T group_tree32(T v)
+{
+    if constexpr (V >= 32) v += swizzle<swizzle_xor_pattern<16>()>(v);
+    if constexpr (V >= 16) v += swizzle<swizzle_xor_pattern<8>()>(v);
+    if constexpr (V >= 8) v += swizzle<swizzle_xor_pattern<4>()>(v);
+    if constexpr (V >= 4) v += dpp<kDppXor2>(v);
+    if constexpr (V >= 2) v += dpp<kDppXor1>(v);
+    return v;
+}
+
+// One tile of the reference algorithm: products in LDS, rows [start, end).
+template <typename T, int TT>
+struct PfTile {
+    const T *s;
+    const int *__restrict__ rp;
+    T *__restrict__ y;
+    int first, start, end;
+
+    __device__ __forceinline__ void range(int r, int &lo, int &hi) const
+    {
+        lo = max(0, rp[r] - first);
+        hi = min(TT, rp[r + 1] - first);
+    }
+    // Tile-boundary rows are shared with a neighbouring tile: atomicAdd;
+    // interior rows are stored (preFreeSpMV.cu:92-96, :139-146).
+    __device__ __forceinline__ void put(int r, T v) const
+    {
+        if (r == start || r == end - 1)
+            atomic_add(y + r, v);
+        else
+            y[r] = v;
+    }
+};
+
+// red_row_thread (preFreeSpMV.cu:71-98): one thread per row, in nnz order.
+template <typename T, int TT>
+__device__ __forceinline__ void pf_red_thread(const PfTile<T, TT> &t)
+{
+    for (int r = t.start + (int)threadIdx.x; r < t.end; r += kPfBS) {
+        int lo, hi;
+        t.range(r, lo, hi);
+        T sum = T(0);
+        for (int i = lo; i < hi; ++i)
+            sum += t.s[i];
+        t.put(r, sum);
+    }
+}
+
+// red_row_block (:30-69): strided lane sums, a 32-lane tree per half wave,
+// then the four half-wave results summed in order by thread 0.
+template <typename T, int TT>
+__device__ __forceinline__ void pf_red_block(const PfTile<T, TT> &t, T *s_warp)
+{
+    const int tid = threadIdx.x;
+    int lo, hi;
+    t.range(t.start, lo, hi);
+    T v = T(0);
+    for (int j = lo + tid; j < hi; j += kPfBS)
+        v += t.s[j];
+    v = half_wave_tree(v);
+    if ((tid & 31) == 0)
+        s_warp[tid >> 5] = v;
+    __syncthreads();
+    if (tid == 0) {
+        T fin = T(0);
+#pragma unroll
+        for (int w = 0; w < kPfBS / 32; ++w)
+            fin += s_warp[w];
+        atomic_add(t.y + t.start, fin);
+    }
+}
+
+// red_row_vector<VS> (:116-150): groups of VS lanes per row, lane 0 of the
+// group ends with warpReduceSum<VS>'s tree.
+template <int VS, typename T, int TT>
+__device__ __forceinline__ void pf_red_vector(const PfTile<T, TT> &t)
+{
+    const int g = threadIdx.x / VS, q = threadIdx.x % VS;
+    for (int r = t.start + g; r < t.end; r += kPfBS / VS) {
+        int lo, hi;
+        t.range(r, lo, hi);
+        T v = T(0);
+        for (int i = lo + q; i < hi; i += VS)
+            v += t.s[i];
+        v = group_tree32<VS>(v);
+        if (q == 0)
+            t.put(r, v);
+    }
+}
+
+// is_imbalanced_warp (:342-373): among the first 32 rows of the range, the
+// longest (whole row length) holds more than 90% of their nnz, compared in
+// float as there.  Integer sums and maxima are exact in any order.
+template <typename T, int TT>
+__device__ __forceinline__ bool pf_imbalanced(const PfTile<T, TT> &t, int *s_flag)
+{
+    const int tid = threadIdx.x;
+    const int n = t.end - t.start;
+    if (tid < 32) {
+        const int len = tid < n ? t.rp[t.start + tid + 1] - t.rp[t.start + tid] : 0;
+        int tot = len, mx = len;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            tot += __shfl_down(tot, o, 32);
+            mx = max(mx, __shfl_down(mx, o, 32));
+        }
+        if (tid == 0) {
+            const float dominance = 0.9f;
+            *s_flag = (n > 1 && tot > 0 && (float)mx > (float)tot * dominance) ? 1 : 0;
+        }
+    }
+    __syncthreads();
+    return *s_flag != 0;
+}
+
+// red_row_long_short_specialized<96> (:152-340), for 2 <= n <= 32 rows: the
+// longest row (a shfl_down max-with-index tree over whole row lengths; a tie
+// keeps the lane's own index) is summed by threads 0..95 in stride 96 with a
+// 32-lane tree per warp and one more tree over the three warp sums; threads
+// 96..127 sum the other rows one each, left to right.  Rows whose sum is 0.0
+// are not written (:326; y is zeroed before the launch).
+template <typename T, int TT>
+__device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_final, T *s_warp, int *s_li)
+{
+    constexpr int kLong = 96;
+    const int tid = threadIdx.x;
+    const int n = t.end - t.start;
+    if (tid < 32) {
+        int len = -1;
+        if (tid < n) {
+            len = t.rp[t.start + tid + 1] - t.rp[t.start + tid];
+            s_final[tid] = T(0);
+        }
+        int ml = len, mi = tid;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            const int rl = __shfl_down(ml, o, 32);
+            const int ri = __shfl_down(mi, o, 32);
+            if (rl > ml) { ml = rl; mi = ri; }
+        }
+        if (tid == 0) *s_li = mi;
+    }
+    __syncthreads();
+    const int li = *s_li;
+    if (tid < kLong) {
+        int lo, hi;
+        t.range(t.start + li, lo, hi);
+        T v = T(0);
+        for (int j = lo + tid; j < hi; j += kLong)
+            v += t.s[j];
+        v = half_wave_tree(v);
+        if ((tid & 31) == 0)
+            s_warp[tid >> 5] = v;
+    } else {
+        for (int i = tid - kLong; i < n; i += kPfBS - kLong) {
+            if (i == li)
+                continue;
+            int lo, hi;
+            t.range(t.start + i, lo, hi);
+            const T *sp = t.s + lo;
+            T sum = T(0);
+            switch (hi - lo) {  // left to right, as the unrolled cases of :293-313
+            case 0: break;
+            case 1: sum = sp[0]; break;
+            case 2: sum = sp[0] + sp[1]; break;
+            case 3: sum = sp[0] + sp[1] + sp[2]; break;
+            case 4: sum = sp[0] + sp[1] + sp[2] + sp[3]; break;
+            default:
+                for (int k = lo; k < hi; ++k)
+                    sum += t.s[k];
+                break;
+            }
+            s_final[i] = sum;
+        }
+    }
+    __syncthreads();
+    if (tid < 32) {
+        T v = tid < kLong / 32 ? s_warp[tid] : T(0);
+        v = half_wave_tree(v);
+        if (tid == 0)
+            s_final[li] = v;
+    }
+    __syncthreads();
+    if (tid < n) {
+        const T fs = s_final[tid];
+        if (fs != T(0))
+            t.put(t.start + tid, fs);
+    }
+}
+
+// calculate_vector_size<128> (:394-405).
+__device__ __forceinline__ int pf_vector_size(int n)
+{
+    if (n >= kPfBS)
+        return 2;
+    const unsigned avg = (unsigned)kPfBS / (unsigned)n;
+    const unsigned p2 = 1u << (31 - __clz((int)avg));
+    return (int)min(32u, max(2u, p2));
+}
+
+// The reference kernel preFreeSpMV_kernel<P, 128> (:407-561) with reduction
+// ladder CODE, the tuner's TEST_CODE_VERSION (scripts/profile_and_generate.py:
+// 109-235): 1 thread per row always (:440-446); 2 block for a single row, else
+// thread (:448-461); 3 thread above 32 rows, block for one, else vector<4>
+// (:466-483, the active ladder); 4 as 3 with the long/short split for
+// imbalanced tiles (:485-511); 5 thread above 128 rows, block for one, else
+// vector<calculate_vector_size> (:513-559).  The tile's first row (the
+// pre-pass map, :3-28) is searched in the kernel.
+template <typename T, int P, int CODE>
 __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
 {
-    constexpr int TT = kPfBS * P;  // 512 nnz for P = 4 (preFreeSpMV.cu:587)
+    constexpr int TT = kPfBS * P;  // 512 nnz for P = 4 (preFreeSpMV.cu:587), 1024 for P = 8
     constexpr int VPT = P / 4;     // 4-nnz vectors per lane
     __shared__ __attribute__((aligned(16))) T s_prod[TT];
     __shared__ int s_rows[2];
     __shared__ T s_warp[kPfBS / 32];
+    __shared__ T s_final[32];
+    __shared__ int s_flag, s_li;
 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
@@ -2001,11 +2226,12 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
         if (lane == 0) s_rows[1] = r;
     }
 
-    // Product stage (:416-428): 16-byte buffer loads of this tile's nnz;
-    // positions past nnz read zeros and give zero products.
+    // Product stage (:416-428): 16-byte buffer loads of this tile's nnz and x
+    // through a range-checked resource; positions past nnz give zero products.
     const int tile_nnz = min(TT, a.nnz - (int)first);
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + first, (long long)tile_nnz * 4);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + first, (long long)tile_nnz * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
     int c[VPT][4];
     T v[VPT][4];
 #pragma unroll
@@ -2017,7 +2243,8 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
         T p[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            p[j] = (off + j < tile_nnz) ? v[k][j] * a.x[c[k][j]] : T(0);
+            p[j] = v[k][j] * buf_load(rx, off + j < tile_nnz ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
+                                      (T *)nullptr);
         store4(s_prod + off, p);
     }
     __syncthreads();
@@ -2028,61 +2255,36 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
     if (a.rp[end] % TT != 0 || end == start)
         end = min(end + 1, m);
     const int nrows = end - start;
+    const PfTile<T, TT> t{s_prod, a.rp, a.y, (int)first, start, end};
 
-    auto range = [&](int r, int &lo, int &hi) {
-        lo = max(0, a.rp[r] - (int)first);
-        hi = min(TT, a.rp[r + 1] - (int)first);
-    };
-    auto put = [&](int r, T s) {
-        if (r == start || r == end - 1)
-            atomic_add(a.y + r, s);
-        else
-            a.y[r] = s;
-    };
-
-    if (nrows > kPfBS / 4) {
-        // red_row_thread (:71-98)
-        for (int r = start + tid; r < end; r += kPfBS) {
-            int lo, hi;
-            range(r, lo, hi);
-            T s = T(0);
-            for (int i = lo; i < hi; ++i)
-                s += s_prod[i];
-            put(r, s);
-        }
-    } else if (nrows == 1) {
-        // red_row_block (:30-69): strided lane sums, a 32-lane tree per half
-        // wave, then the four half-wave results summed in order.
-        int lo, hi;
-        range(start, lo, hi);
-        T s = T(0);
-        for (int j = lo + tid; j < hi; j += kPfBS)
-            s += s_prod[j];
-        s = half_wave_tree(s);
-        if ((lane & 31) == 0)
-            s_warp[tid >> 5] = s;
-        __syncthreads();
-        if (tid == 0) {
-            T fin = T(0);
-#pragma unroll
-            for (int w = 0; w < kPfBS / 32; ++w)
-                fin += s_warp[w];
-            atomic_add(a.y + start, fin);
-        }
+    if constexpr (CODE == 1) {
+        pf_red_thread(t);
+    } else if constexpr (CODE == 2) {
+        if (nrows == 1) pf_red_block(t, s_warp);
+        else pf_red_thread(t);
+    } else if constexpr (CODE == 3) {
+        if (nrows > kPfBS / 4) pf_red_thread(t);
+        else if (nrows == 1) pf_red_block(t, s_warp);
+        else pf_red_vector<4>(t);
+    } else if constexpr (CODE == 4) {
+        if (nrows > kPfBS / 4) pf_red_thread(t);
+        else if (nrows == 1) pf_red_block(t, s_warp);
+        else if (pf_imbalanced(t, &s_flag)) pf_red_long_short(t, s_final, s_warp, &s_li);
+        else pf_red_vector<4>(t);
     } else {
-        // red_row_vector<4> (:116-150): 4 lanes per row; lane 0 of the group
-        // ends with (l0 + l2) + (l1 + l3) as warpReduceSum<4> gives.
-        const int g = tid >> 2, q = tid & 3;
-        for (int r = start + g; r < end; r += kPfBS / 4) {
-            int lo, hi;
-            range(r, lo, hi);
-            T s = T(0);
-            for (int i = lo + q; i < hi; i += 4)
-                s += s_prod[i];
-            s += dpp<kDppXor2>(s);
-            s += dpp<kDppXor1>(s);
-            if (q == 0)
-                put(r, s);
+        static_assert(CODE == 5, "ladder codes 1..5");
+        if (nrows > kPfBS) {
+            pf_red_thread(t);
+        } else if (nrows == 1) {
+            pf_red_block(t, s_warp);
+        } else if (nrows > 0) {
+            switch (pf_vector_size(nrows)) {
+            case 32: pf_red_vector<32>(t); break;
+            case 16: pf_red_vector<16>(t); break;
+            case 8: pf_red_vector<8>(t); break;
+            case 4: pf_red_vector<4>(t); break;
+            default: pf_red_vector<2>(t); break;
+            }
         }
     }
 }
@@ -2322,6 +2524,38 @@ int unsupported_f16(const char *variant)
     return PF_ERR_UNSUPPORTED;
 }
 
+// A workspace buffer of `have` bytes where `need` are touched.
+bool room(const void *p, size_t have, long long need, const char *what)
+{
+    if (need <= 0) return true;
+    if (p && have >= (size_t)need) return true;
+    snprintf(g_err, sizeof g_err, "%s: %zu bytes given, %lld needed", what, p ? have : (size_t)0, need);
+    return false;
+}
+
+// The workspace a launch touches, against the sizes the caller declared.
+// split: head / tail / owner slots are written or read (every tiling but the
+// row-aligned FLAT and PREFREE ones).
+bool ws_ok(int dtype, const pfk_spmv_args *a, bool split)
+{
+    const long long nt = a->ntiles;
+    if (split && !(room(a->head_slot, a->head_bytes, nt * PFK_SLOT_BYTES(dtype), "head slots") &&
+                   room(a->tail_slot, a->tail_bytes, nt * PFK_SLOT_BYTES(dtype), "tail slots") &&
+                   room(a->owner_row, a->owner_bytes, nt * 4, "owner slots")))
+        return false;
+    if (a->row_map && !room(a->row_map, a->row_map_bytes, (nt + 1) * 8, "row map"))
+        return false;
+    if (a->sched) {
+        if (a->sched_cap < (nt + kXcds - 1) / kXcds) {
+            snprintf(g_err, sizeof g_err, "schedule lists of %lld tiles for %lld tiles", a->sched_cap, nt);
+            return false;
+        }
+        if (!room(a->sched, a->sched_bytes, (long long)PFK_SCHED_INTS(nt, a->sched_cap) * 4, "x-window schedule"))
+            return false;
+    }
+    return true;
+}
+
 bool args_ok(const pfk_spmv_args *a, bool need_ws)
 {
     if (!a || !a->row_ptr || !a->y || a->m < 0 || a->n < 0 || a->nnz < 0 || a->ntiles < 1 || !a->err_flag)
@@ -2498,6 +2732,23 @@ int launch_flat_desc(const pfk_spmv_args *a, int *out, void *stream)
     return PF_OK;
 }
 
+template <typename T, int P>
+int launch_prefree(const pfk_spmv_args *a, void *stream)
+{
+    Args<T> r = make_args<T>(a);
+    const dim3 grid((unsigned)(((a->ntiles + kXcds - 1) / kXcds) * kXcds));
+    switch (a->ladder == 0 ? 3 : a->ladder) {
+    case 1: hipLaunchKernelGGL((k_prefree<T, P, 1>), grid, dim3(kPfBS), 0, S(stream), r); break;
+    case 2: hipLaunchKernelGGL((k_prefree<T, P, 2>), grid, dim3(kPfBS), 0, S(stream), r); break;
+    case 3: hipLaunchKernelGGL((k_prefree<T, P, 3>), grid, dim3(kPfBS), 0, S(stream), r); break;
+    case 4: hipLaunchKernelGGL((k_prefree<T, P, 4>), grid, dim3(kPfBS), 0, S(stream), r); break;
+    case 5: hipLaunchKernelGGL((k_prefree<T, P, 5>), grid, dim3(kPfBS), 0, S(stream), r); break;
+    default: return PF_ERR_INVALID;
+    }
+    PFK_LAUNCHED("k_prefree");
+    return PF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2506,15 +2757,16 @@ int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream)
 {
     if (dtype == PF_F16) return unsupported_f16("ADAPTIVE");
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
-    if (!args_ok(a, true)) return PF_ERR_INVALID;
+    if (!args_ok(a, true) || !ws_ok(dtype, a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_adaptive<double>(a, stream)
          : dtype == PF_F32 ? dispatch_adaptive<float>(a, stream) : PF_ERR_INVALID;
 }
 
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
 {
-    if (a && a->m == 0 && a->nnz == 0) return PF_OK;
-    if (!args_ok(a, true)) return PF_ERR_INVALID;
+    if (!a) return PF_ERR_INVALID;
+    if (a->m == 0 && a->nnz == 0) return PF_OK;
+    if (!args_ok(a, !a->row_aligned) || !ws_ok(dtype, a, !a->row_aligned)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream)
          : dtype == PF_F16 ? dispatch_flat<half_t>(a, stream) : PF_ERR_INVALID;
@@ -2559,6 +2811,7 @@ int pfk_adaptive_resident_waves(int dtype, int tile, long long *waves)
 int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream)
 {
     if (!a || !a->row_ptr || !a->owner_row || !a->err_flag || a->m <= 0 || a->ntiles < 1) return PF_ERR_INVALID;
+    if (!room(a->owner_row, a->owner_bytes, a->ntiles * 4, "owner slots")) return PF_ERR_INVALID;
     // The descriptors depend on (K, LMAX) only; the double instantiation serves both value types.
 #define PF_OWNERS(TT, DT, KK) \
     if (dtype == DT && a->tile == KK) return launch_stream<double, KK, adaptive_lmax(KK), true>(a, nullptr, stream);
@@ -2571,7 +2824,7 @@ int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream)
 int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream)
 {
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
-    if (!args_ok(a, true) || a->tile <= 0) return PF_ERR_INVALID;
+    if (!args_ok(a, true) || a->tile <= 0 || !ws_ok(dtype, a, true)) return PF_ERR_INVALID;
     const unsigned grid = (unsigned)((a->ntiles + kBS - 1) / kBS);
     if (dtype == PF_F64) {
         Args<double> r = make_args<double>(a);
@@ -2597,25 +2850,16 @@ int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream)
     if (dtype != PF_F64 && dtype != PF_F32) return PF_ERR_INVALID;  // before y is sized from it
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, false)) return PF_ERR_INVALID;
+    if (a->ladder < 0 || a->ladder > 5) {
+        snprintf(g_err, sizeof g_err, "reduction ladder %d: the reference has codes 1..5", a->ladder);
+        return PF_ERR_INVALID;
+    }
+    if (a->tile != 512 && a->tile != 1024) return PF_ERR_UNSUPPORTED;
     const size_t ybytes = (size_t)a->m * (dtype == PF_F64 ? 8 : 4);
     int st = pfk_fill_zero(a->y, ybytes, stream);  // the reference memsets y, preFreeSpMV.cu:644
     if (st != PF_OK || a->nnz == 0) return st;
-    const long long grid = ((a->ntiles + kXcds - 1) / kXcds) * kXcds;
-    if (dtype == PF_F64) {
-        Args<double> r = make_args<double>(a);
-        if (a->tile == 512) hipLaunchKernelGGL((k_prefree<double, 4>), dim3((unsigned)grid), dim3(kPfBS), 0, S(stream), r);
-        else if (a->tile == 1024) hipLaunchKernelGGL((k_prefree<double, 8>), dim3((unsigned)grid), dim3(kPfBS), 0, S(stream), r);
-        else return PF_ERR_UNSUPPORTED;
-    } else if (dtype == PF_F32) {
-        Args<float> r = make_args<float>(a);
-        if (a->tile == 512) hipLaunchKernelGGL((k_prefree<float, 4>), dim3((unsigned)grid), dim3(kPfBS), 0, S(stream), r);
-        else if (a->tile == 1024) hipLaunchKernelGGL((k_prefree<float, 8>), dim3((unsigned)grid), dim3(kPfBS), 0, S(stream), r);
-        else return PF_ERR_UNSUPPORTED;
-    } else {
-        return PF_ERR_INVALID;
-    }
-    PFK_LAUNCHED("k_prefree");
-    return PF_OK;
+    if (dtype == PF_F64) return a->tile == 512 ? launch_prefree<double, 4>(a, stream) : launch_prefree<double, 8>(a, stream);
+    return a->tile == 512 ? launch_prefree<float, 4>(a, stream) : launch_prefree<float, 8>(a, stream);
 }
 
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)

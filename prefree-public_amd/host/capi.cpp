@@ -325,6 +325,7 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
         r.needs_fixup = 0;
         r.workspace_bytes = 256;
+        r.ladder = 3;  // the reference's active ladder, preFreeSpMV.cu:466-483
     } else {
         return fail(PF_ERR_INVALID, "unknown variant");
     }
@@ -349,6 +350,8 @@ struct pf_plan {
     int *sched = nullptr;    // split-row FLAT 1024/2048: x-window schedule, recorded with the map
     long long sched_cap = 0;
     bool remember_rows = true;  // false: every call searches row_ptr (no row map, no schedule)
+    // bytes of the workspace behind each array (passed to the kernel layer, which checks them)
+    size_t head_bytes = 0, tail_bytes = 0, owner_bytes = 0, row_map_bytes = 0, sched_bytes = 0;
 };
 
 namespace {
@@ -390,20 +393,27 @@ void plan_carve(pf_plan *p, void *w0)
 {
     const pf_plan_info &info = p->info;
     char *w = static_cast<char *>(w0);
+    const size_t total = info.workspace_bytes;
     p->ws = w0;
     p->err = reinterpret_cast<int *>(w);
     if (info.variant != PF_PREFREE) {
         const size_t vb = (size_t)slot_bytes(info.dtype);
         const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
+        const size_t owner_at = 256 + 2 * slots;
         p->head = w + 256;
         p->tail = w + 256 + slots;
-        p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
+        p->owner = reinterpret_cast<int *>(w + owner_at);
+        p->head_bytes = p->tail_bytes = slots;
+        p->owner_bytes = total - owner_at;
         if (uses_row_map(info.variant, info.tile)) {
             const size_t owners = ((size_t)info.ntiles * 4 + 255) & ~(size_t)255;
             const size_t map = ((size_t)(info.ntiles + 1) * 8 + 255) & ~(size_t)255;
-            p->row_map = reinterpret_cast<int *>(w + 256 + 2 * slots + owners);
-            p->sched = reinterpret_cast<int *>(w + 256 + 2 * slots + owners + map);
+            p->row_map = reinterpret_cast<int *>(w + owner_at + owners);
+            p->sched = reinterpret_cast<int *>(w + owner_at + owners + map);
             p->sched_cap = sched_cap(info.ntiles);
+            p->owner_bytes = owners;
+            p->row_map_bytes = map;
+            p->sched_bytes = total - (owner_at + owners + map);
         }
     }
 }
@@ -429,6 +439,7 @@ int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
         a.run_tiles = info.run_tiles;
         a.ntiles = info.ntiles;
         a.owner_row = p->owner;
+        a.owner_bytes = p->owner_bytes;
         a.err_flag = p->err;
         rc = pfk_adaptive_owners(info.dtype, &a, stream);
     }
@@ -656,6 +667,14 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz)
     return PF_OK;
 }
 
+int pf_plan_set_ladder(pf_plan *plan, int ladder)
+{
+    if (!plan || ladder < 1 || ladder > 5) return fail(PF_ERR_INVALID, "ladder must be 1..5");
+    if (plan->info.variant != PF_PREFREE) return fail(PF_ERR_UNSUPPORTED, "reduction ladders are for PREFREE plans");
+    plan->info.ladder = ladder;
+    return PF_OK;
+}
+
 int pf_plan_set_remember_rows(pf_plan *plan, int remember)
 {
     if (!plan || (remember != 0 && remember != 1)) return fail(PF_ERR_INVALID, "remember must be 0 or 1");
@@ -703,6 +722,12 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.sched = (plan->remember_rows && plan->info.x_windows && plan->sched) ? plan->sched : nullptr;
     a.sched_cap = plan->sched_cap;
     a.chunk_nnz = plan->info.chunk_nnz;
+    a.ladder = plan->info.ladder;
+    a.head_bytes = plan->head_bytes;
+    a.tail_bytes = plan->tail_bytes;
+    a.owner_bytes = plan->owner_bytes;
+    a.row_map_bytes = plan->row_map_bytes;
+    a.sched_bytes = plan->sched_bytes;
     if (a.sched && !plan->map_ready)  // the recording call starts from empty lists
         PF_TRY(pfk_fill_zero(a.sched, 16 * sizeof(int), stream), "schedule reset");
     const int dt = plan->info.dtype;
@@ -957,6 +982,11 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
         std::swap(plan->map_ready, best_plan->map_ready);
         std::swap(plan->sched, best_plan->sched);
         std::swap(plan->sched_cap, best_plan->sched_cap);
+        std::swap(plan->head_bytes, best_plan->head_bytes);
+        std::swap(plan->tail_bytes, best_plan->tail_bytes);
+        std::swap(plan->owner_bytes, best_plan->owner_bytes);
+        std::swap(plan->row_map_bytes, best_plan->row_map_bytes);
+        std::swap(plan->sched_bytes, best_plan->sched_bytes);
         pf_plan_destroy(best_plan);
     }
     // y = A x with the chosen configuration, so that the caller's y is defined.

@@ -233,3 +233,67 @@ def test_noalloc_rejects_oversized_workspace_before_launch():
     st = f(0x1000, 0x1000, 0x1000, 0x1000, 0x1000, 1, 1, 300_000_000, pf.F64, pf.FLAT, None)
     assert st == 5  # PF_ERR_UNSUPPORTED
     assert b"scratch" in L.pf_last_error()
+
+
+# ---- the thin HIP layer checks the workspace sizes it is given (no launch happens) ----
+
+def _args(ntiles=100, **kw):
+    fake = 0x10000  # never dereferenced: every case below is refused on the host
+    a = dict(row_ptr=fake, col=fake, val=fake, x=fake, y=fake, m=1000, n=1000, nnz=100 * 1024, tile=1024,
+             ntiles=ntiles, head_slot=fake, tail_slot=fake, owner_row=fake, err_flag=fake,
+             head_bytes=ntiles * 8, tail_bytes=ntiles * 8, owner_bytes=ntiles * 4)
+    a.update(kw)
+    return pf.SpmvArgs(**a)
+
+
+@pytest.mark.parametrize("field,value", [("head_bytes", 99 * 8), ("tail_bytes", 100 * 8 - 1), ("owner_bytes", 396),
+                                         ("head_slot", None)])
+def test_flat_split_rejects_small_slots(field, value):
+    K = pf.klib()
+    a = _args(**{field: value})
+    assert K.pfk_spmv_flat(pf.F64, ctypes.byref(a), None) == 1  # PF_ERR_INVALID
+    assert K.pfk_spmv_fixup(pf.F64, 0, ctypes.byref(a), None) == 1
+    assert K.pfk_spmv_adaptive(pf.F64, ctypes.byref(_args(tile=512, **{field: value})), None) == 1
+
+
+def test_fp16_slots_are_fp32():
+    # fp16 partial sums are fp32: 2-byte slots per tile are too small.
+    K = pf.klib()
+    a = _args(head_bytes=100 * 2, tail_bytes=100 * 2)
+    assert K.pfk_spmv_flat(pf.F16, ctypes.byref(a), None) == 1
+    assert b"head slots" in K.pfk_last_error()
+
+
+def test_row_map_and_schedule_sizes_checked():
+    K = pf.klib()
+    fake = 0x20000
+    assert K.pfk_spmv_flat(pf.F64, ctypes.byref(_args(row_map=fake, row_map_bytes=100 * 8)), None) == 1
+    assert b"row map" in K.pfk_last_error()
+    cap = 13  # ceil(100 / 8)
+    ints = 16 + 8 * cap + 100
+    a = _args(row_map=fake, row_map_bytes=101 * 8, sched=fake, sched_cap=cap, sched_bytes=ints * 4 - 4)
+    assert K.pfk_spmv_flat(pf.F64, ctypes.byref(a), None) == 1
+    assert b"schedule" in K.pfk_last_error()
+    a = _args(row_map=fake, row_map_bytes=101 * 8, sched=fake, sched_cap=12, sched_bytes=1 << 20)
+    assert K.pfk_spmv_flat(pf.F64, ctypes.byref(a), None) == 1  # lists shorter than an even share
+
+
+def test_adaptive_owner_table_size_checked():
+    K = pf.klib()
+    a = _args(tile=512, owner_bytes=10)
+    assert K.pfk_adaptive_owners(pf.F64, ctypes.byref(a), None) == 1
+
+
+def test_prefree_ladder_range_checked():
+    K = pf.klib()
+    K.pfk_spmv_prefree.argtypes = [ctypes.c_int, ctypes.POINTER(pf.SpmvArgs), ctypes.c_void_p]
+    for bad in (-1, 6):
+        a = _args(tile=512, ladder=bad)
+        assert K.pfk_spmv_prefree(pf.F64, ctypes.byref(a), None) == 1
+        assert b"ladder" in K.pfk_last_error()
+
+
+def test_plan_info_layout_has_ladder():
+    s = pf.RowStats(m=1000, nnz=5000, max_row_len=7, min_row_len=3)
+    assert pf.select(s, "f64", "prefree").ladder == 3
+    assert pf.select(s, "f64", "flat").ladder == 0

@@ -221,3 +221,98 @@ def test_initvec():
     v = oracle.initvec(40)
     assert list(v[:16]) == [float(i % 15) for i in range(16)]
     assert np.array_equal(oracle.initvec(40, np.float32), v.astype(np.float32))
+
+
+# ---- every reduction ladder of the reference kernel (preFreeSpMV.cu:440-559) ----
+
+LADDERS = [(code, p) for code in (1, 2, 3, 4, 5) for p in (4, 8)]
+
+
+@pytest.mark.parametrize("code,p_nnz", LADDERS, ids=[f"code{c}-p{p}" for c, p in LADDERS])
+def test_prefree_sim_ladders_exact_on_kat(code, p_nnz):
+    # initVec values: every product and row sum is an exact integer, so any
+    # summation tree and any order of the boundary-row atomics give the serial sum.
+    for name, rp, col, n in edge_cases():
+        val, x = oracle.initvec(len(col)), oracle.initvec(n)
+        ref = oracle.spmv_serial(rp, col, val, x)
+        for rev in (False, True):
+            got = oracle.prefree_sim(rp, col, val, x, code=code, p_nnz=p_nnz, reverse_tiles=rev)
+            assert np.array_equal(got, ref), (name, code, p_nnz, rev)
+
+
+@pytest.mark.parametrize("code,p_nnz", LADDERS, ids=[f"code{c}-p{p}" for c, p in LADDERS])
+def test_prefree_sim_ladders_random_within_tolerance(code, p_nnz):
+    rng = np.random.default_rng(code * 10 + p_nnz)
+    for name, rp, col, n in edge_cases(11):
+        val = rng.uniform(-1, 1, len(col))
+        x = rng.uniform(-1, 1, n)
+        y, plain, atomics = oracle.prefree_sim(rp, col, val, x, code=code, p_nnz=p_nnz, counts=True)
+        err, zb, _ = oracle.rownorm_maxerr(rp, col, val, x, oracle.spmv_serial(rp, col, val, x), y)
+        assert err <= 1e-14 and zb == 0, (name, code, p_nnz)
+        # every non-empty row is written: by exactly one plain store, or by atomic adds alone
+        lens = np.diff(rp)
+        ok = ((plain == 1) & (atomics == 0)) | ((plain == 0) & (atomics >= 1))
+        if code == 4:  # the long/short split skips rows whose sum is exactly zero
+            ok |= (plain == 0) & (atomics == 0) & (y == 0)
+        assert np.all(ok[lens > 0]), (name, code, p_nnz)
+
+
+def test_prefree_sim_thread_ladder_is_sequential():
+    # Code 1 sums every row with one thread in nnz order (red_row_thread): a row
+    # inside one tile, stored plainly, is bit-identical to spmv_serial even where
+    # cancellation makes other summation orders round differently.
+    rng = np.random.default_rng(3)
+    lengths = rng.integers(1, 12, size=4000)
+    rp, col = csr_from_lengths(lengths, 3000, rng)
+    val = rng.uniform(-1, 1, len(col)) * 10.0 ** rng.integers(-8, 9, size=len(col))
+    x = rng.uniform(-1, 1, 3000)
+    ref = oracle.spmv_serial(rp, col, val, x)
+    for p_nnz in (4, 8):
+        y, plain, _ = oracle.prefree_sim(rp, col, val, x, code=1, p_nnz=p_nnz, counts=True)
+        assert plain.sum() > 3000
+        assert np.array_equal(y[plain == 1], ref[plain == 1])
+
+
+def test_prefree_vector_size_table():
+    # calculate_vector_size<128> (preFreeSpMV.cu:394-405): 2^floor(log2(128 // n)) clamped to [2, 32],
+    # 2 from 128 rows on; values worked by hand.
+    want = {1: 32, 2: 32, 3: 32, 4: 32, 5: 16, 8: 16, 9: 8, 16: 8, 17: 4, 32: 4, 33: 2, 42: 2, 43: 2, 64: 2,
+            65: 2, 127: 2, 128: 2, 500: 2}
+    for n, vs in want.items():
+        assert oracle.prefree_vector_size(n) == vs, n
+
+
+def test_prefree_sim_long_short_split():
+    # One 512-nnz tile holding rows of 2, 3, 500 and 7 nnz: the 500-nnz row holds
+    # 97.7% of the tile, so ladder 4 takes red_row_long_short_specialized
+    # (:485-511).  Row 1 (interior) sums to exactly zero: ladder 4 never writes
+    # it (:326), ladder 3 stores the zero.  Row 0 opens the tile (atomic add of
+    # its two-term sum, left to right).
+    rng = np.random.default_rng(5)
+    lengths = [2, 3, 500, 7, 4, 600]
+    rp, col = csr_from_lengths(lengths, 2000, rng)
+    val = rng.uniform(-1, 1, len(col))
+    x = rng.uniform(-1, 1, 2000)
+    val[rp[1]:rp[2]] = [1.0, 1.0, -2.0]
+    x[col[rp[1]:rp[2]]] = 1.0
+    ref = oracle.spmv_serial(rp, col, val, x)
+    sentinel = np.full(len(lengths), 7.0)
+    y4 = oracle.prefree_sim(rp, col, val, x, code=4, y=sentinel)
+    y3 = oracle.prefree_sim(rp, col, val, x, code=3, y=sentinel)
+    assert y4[1] == 7.0 and y3[1] == 0.0
+    assert y4[0] == 7.0 + (val[0] * x[col[0]] + val[1] * x[col[1]])
+    # the long row (interior, stored plainly) is within rounding of the serial sum
+    r2 = slice(rp[2], rp[3])
+    assert y4[2] != 7.0 and abs(y4[2] - ref[2]) <= 1e-14 * np.abs(val[r2] * x[col[r2]]).sum()
+    kat_v, kat_x = oracle.initvec(len(col)), oracle.initvec(2000)
+    assert np.array_equal(oracle.prefree_sim(rp, col, kat_v, kat_x, code=4),
+                          oracle.spmv_serial(rp, col, kat_v, kat_x))
+
+
+def test_prefree_sim_rejects_unknown_ladder():
+    rp, col = csr_from_lengths([3, 3], 4, np.random.default_rng(0))
+    v = oracle.initvec(6)
+    with pytest.raises(ValueError):
+        oracle.prefree_sim(rp, col, v, oracle.initvec(4), code=6)
+    with pytest.raises(ValueError):
+        oracle.prefree_sim(rp, col, v, oracle.initvec(4), code=3, p_nnz=16)
