@@ -11,13 +11,17 @@
  * x, runs 200 warm-up and 4000 timed SpMVs, writes the mean kernel time per
  * SpMV in ms to *cdTime, computes Y_val = A·x (overwritten) and frees
  * everything.  Differences, all deliberate:
- *   - *cdPre is the one-time analysis cost in ms (row statistics, variant
- *     selection, workspace) — the kernels need no per-call pre-pass;
+ *   - *cdPre is what finding the tiles' rows costs per SpMV in ms: there is
+ *     no pre-pass kernel, the SpMV kernel's first call searches row_ptr and
+ *     records the rows, later calls read them; cdPre is the event-timed mean of
+ *     calls that search every time minus *cdTime (0 for variants that always
+ *     search: PREFREE, ADAPTIVE);
  *   - exactly rowA+1 row_ptr entries are read (the reference copies rowA+2);
  *   - fatal errors print one line to stderr and exit(EXIT_FAILURE), as the
  *     reference's CUDA_CHECK_ERROR (include/common.h:49-58) does.
  * Environment knobs (all optional): PREFREE_VARIANT=auto|prefree|adaptive|flat,
- * PREFREE_TILE=<keys per tile>, PREFREE_WARMUP=<n> (200), PREFREE_ITERS=<n> (4000).
+ * PREFREE_TILE=<keys per tile>, PREFREE_WARMUP=<n> (200), PREFREE_ITERS=<n> (4000),
+ * PREFREE_PRE_ITERS=<n> (ITERS/10, at least 20), PREFREE_VERBOSE=1 (planning time to stderr).
  *
  * valT is double (the reference's default -Dfp64 build).  Defining
  * PREFREE_VALT_FLOAT before including this header selects the float overload,

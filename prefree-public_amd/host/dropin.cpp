@@ -1,8 +1,8 @@
 // dropin.cpp — the reference's one-call API, preFreeSpMV (include/PreFree.h),
 // on top of the C ABI.  Restates the host orchestration of
-// src/spmv_kernel/preFreeSpMV.cu:563-662: allocate, copy in, analyse (the
-// reference's pre-pass slot), time 200 warm-up + 4000 SpMVs with events on one
-// stream, compute the checked y, copy out, free.
+// src/spmv_kernel/preFreeSpMV.cu:563-662: allocate, copy in, analyse, time 200
+// warm-up + 4000 SpMVs with events on one stream, time the rows' search (the
+// reference's pre-pass slot, cdPre), compute the checked y, copy out, free.
 #include "PreFree.h"
 #include "prefree_c.h"
 #include "prefree_kernels.h"
@@ -66,32 +66,51 @@ void run(T *csrVal, int *csrRowPtr, int *csrColInd, T *X_val, T *Y_val, int rowA
     check(pf_memcpy_h2d(d_x, X_val, sizeof(T) * (size_t)colA, stream), "copy x");
     check(pf_stream_synchronize(stream), "copy");
 
-    // One-time analysis (row statistics + selection + workspace), timed as cdPre.
+    // One-time analysis (row statistics + selection + workspace); its wall time
+    // is printed with PREFREE_VERBOSE=1.
     const auto t0 = std::chrono::steady_clock::now();
     pf_plan *plan = nullptr;
     check(pf_plan_create_tuned(&plan, static_cast<int *>(d_rp), static_cast<int *>(d_col), rowA, colA, nnzA, dtype,
                                env_variant(), env_int("PREFREE_TILE", 0), stream),
           "plan");
     const auto t1 = std::chrono::steady_clock::now();
-    *cdPre = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    const double plan_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
 
     const int warm = env_int("PREFREE_WARMUP", 200), iters = env_int("PREFREE_ITERS", 4000);
     auto spmv = [&]() {
         check(pf_plan_execute(plan, static_cast<int *>(d_rp), static_cast<int *>(d_col), d_val, d_x, d_y, stream),
               "spmv");
     };
-    for (int i = 0; i < warm; ++i) spmv();
-    check(pf_stream_synchronize(stream), "warm-up");
     void *e0 = nullptr, *e1 = nullptr;
     check(pfk_event_create(&e0), "event");
     check(pfk_event_create(&e1), "event");
-    check(pfk_event_record(e0, stream), "event record");
-    for (int i = 0; i < iters; ++i) spmv();
-    check(pfk_event_record(e1, stream), "event record");
-    check(pfk_event_sync(e1), "event sync");
-    float ms = 0.f;
-    check(pfk_event_elapsed_ms(&ms, e0, e1), "event time");
-    *cdTime = iters > 0 ? (double)ms / iters : 0.0;
+    auto timed = [&](int n) {  // mean event-timed ms per SpMV over n back-to-back calls
+        check(pfk_event_record(e0, stream), "event record");
+        for (int i = 0; i < n; ++i) spmv();
+        check(pfk_event_record(e1, stream), "event record");
+        check(pfk_event_sync(e1), "event sync");
+        float ms = 0.f;
+        check(pfk_event_elapsed_ms(&ms, e0, e1), "event time");
+        return n > 0 ? (double)ms / n : 0.0;
+    };
+    for (int i = 0; i < warm; ++i) spmv();
+    check(pf_stream_synchronize(stream), "warm-up");
+    *cdTime = timed(iters);
+
+    // cdPre: what finding the tiles' rows costs per call.  The reference times
+    // its separate pre-pass kernel (preFreeSpMV.cu:604-622); here the rows are
+    // found inside the SpMV kernel, by its first call (later calls read what it
+    // recorded), so cdPre is the mean time of calls that search on every call
+    // minus cdTime.  Variants that always search report 0: their search is in cdTime.
+    const int pre_iters = env_int("PREFREE_PRE_ITERS", iters / 10 > 20 ? iters / 10 : 20);
+    check(pf_plan_set_remember_rows(plan, 0), "search mode");
+    for (int i = 0; i < 5; ++i) spmv();
+    const double search_ms = timed(pre_iters);
+    check(pf_plan_set_remember_rows(plan, 1), "search mode");
+    *cdPre = search_ms > *cdTime ? search_ms - *cdTime : 0.0;
+    if (env_int("PREFREE_VERBOSE", 0))
+        std::fprintf(stderr, "preFreeSpMV: plan %.3f ms, %.6f ms per SpMV, %.6f ms per SpMV searching rows\n", plan_ms,
+                     *cdTime, search_ms);
 
     // The checked result: a fresh y, one SpMV (preFreeSpMV.cu:644-645).
     check(pfk_fill_zero(d_y, sizeof(T) * (size_t)rowA, stream), "zero y");

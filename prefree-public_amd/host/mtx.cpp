@@ -16,6 +16,7 @@
 // indices out of range, short files) is reported instead of read past.
 #include "prefree_c.h"
 
+#include <algorithm>
 #include <cctype>
 #include <cerrno>
 #include <cstdio>
@@ -119,8 +120,14 @@ int pf_mtx_read(const char *path, int *m, int *n, int *nnz, int *is_symmetric, i
     if (M < 0 || N < 0 || Z < 0 || M > 0x7FFFFFFF - 1 || N > 0x7FFFFFFF || Z > 0x7FFFFFFF)
         return mtx_fail("size out of range");
 
-    std::vector<int> ri((size_t)Z), ci((size_t)Z);
-    std::vector<double> vi((size_t)Z);
+    // The entry arrays grow as entries are read: a header's count alone (up to
+    // 2^31 - 1) never decides an allocation.
+    std::vector<int> ri, ci;
+    std::vector<double> vi;
+    const size_t first_reserve = (size_t)std::min<long long>(Z, 1 << 20);
+    ri.reserve(first_reserve);
+    ci.reserve(first_reserve);
+    vi.reserve(first_reserve);
     long long got = 0;
     while (got < Z) {
         if (!r.line(ln)) return mtx_fail("file ends after " + std::to_string(got) + " of " + std::to_string(Z) + " entries");
@@ -138,9 +145,9 @@ int pf_mtx_read(const char *path, int *m, int *n, int *nnz, int *is_symmetric, i
         if (k != 3) return mtx_fail("bad entry line: " + ln);
         if (i < 1 || i > M || j < 1 || j > N) return mtx_fail("entry index out of range: " + ln);
         if (mirror && j > M) return mtx_fail("symmetric entry outside a square matrix: " + ln);
-        ri[(size_t)got] = (int)(i - 1);
-        ci[(size_t)got] = (int)(j - 1);
-        vi[(size_t)got] = v;
+        ri.push_back((int)(i - 1));
+        ci.push_back((int)(j - 1));
+        vi.push_back(v);
         ++got;
     }
 

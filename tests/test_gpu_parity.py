@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 import prefree_amd as pf
-from csr_cases import edge_cases
+from csr_cases import csr_from_lengths, edge_cases
 from gpu_util import NP, assert_parity, gpu_spmv, kat_exact_possible
 
 pytestmark = pytest.mark.gpu
@@ -367,3 +367,48 @@ def test_malformed_csr_rejected_at_planning():
     with pytest.raises(pf.PrefreeError) as e:          # row_ptr[m] != nnz
         pf.Plan(dev(rp), dev(col), 2, 3, 3, "f64")
     assert e.value.status == 6
+
+
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_kernel_error_flag_on_changed_row_ptr(tile):
+    # A row-aligned FLAT plan accepts rows of at most 256 nnz.  A different but
+    # valid row_ptr (same m and nnz, monotone, row 0 at 0, row m at nnz, every
+    # column in range) with one row of 400 nnz makes a tile's last row overflow
+    # it: the search sets the plan's error flag (every access stays clamped to
+    # the tile), pf_plan_check reports PF_ERR_KERNEL once and clears the flag,
+    # and the next call on the planned row_ptr is clean and exact.
+    import torch
+
+    m, n = 4000, 4000
+    rng = np.random.default_rng(tile)
+    rp, col = csr_from_lengths([5] * m, n, rng)
+    lengths = np.full(m, 5)
+    r = tile - 20                   # starts at 5r = 5 tile - 100: runs 300 nnz into the next tile
+    lengths[r] = 400
+    lengths[r + 1:r + 1 + 395] = 4  # nnz unchanged
+    assert lengths.sum() == 5 * m
+    rp_bad = np.zeros(m + 1, dtype=np.int32)
+    np.cumsum(lengths, out=rp_bad[1:])
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    d_rp, d_bad, d_col = (torch.from_numpy(a).cuda() for a in (rp, rp_bad, col))
+    d_val, d_x = torch.from_numpy(val).cuda(), torch.from_numpy(x).cuda()
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device="cuda")
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "flat", tile) as p:
+        assert p.info.row_aligned
+        p.execute(d_rp, d_col, d_val, d_x, y)       # records the row map
+        p.check()
+        p.set_remember_rows(False)                  # every call searches row_ptr
+        p.execute(d_bad, d_col, d_val, d_x, y)
+        with pytest.raises(pf.PrefreeError) as e:
+            p.check()
+        assert e.value.status == 7  # PF_ERR_KERNEL
+        p.check()                                   # the flag was cleared
+        y.fill_(float("nan"))
+        p.execute(d_rp, d_col, d_val, d_x, y)
+        p.check()
+        assert np.array_equal(y.cpu().numpy(), oracle.spmv_serial(rp, col, val, x))
+        p.set_remember_rows(True)                   # records the map again on this call
+        y.fill_(float("nan"))
+        p.execute(d_rp, d_col, d_val, d_x, y)
+        p.check()
+        assert np.array_equal(y.cpu().numpy(), oracle.spmv_serial(rp, col, val, x))
