@@ -68,6 +68,7 @@ typedef struct pf_row_stats {
     long long row_ptr_last;   /* row_ptr[m] (must be nnz) */
     long long n_bad_cols;     /* col[j] outside [0,n); -1 when columns were not checked */
     long long hist_log2[33];  /* [0]: empty rows; [k]: rows with 2^(k-1) <= len < 2^k */
+    long long n_long_rows;    /* rows longer than 256 nnz (the longest a row-aligned tile takes) */
 } pf_row_stats;
 
 /* Launch configuration chosen for a matrix. */
@@ -91,6 +92,12 @@ typedef struct pf_plan_info {
     long long chunk_nnz;  /* FLAT 1024/2048 without x windows: tiles dealt to the 8 XCDs in chunks of
                              consecutive tiles of about this many nnz (0 = one chunk per XCD) */
     int ladder;           /* PREFREE: the reduction ladder 1..5 (see pf_plan_set_ladder); 0 otherwise */
+    int hybrid;           /* 1: rows of at least a few thousand nnz with sorted columns ("dense rows") are summed
+                             by x windows staged in LDS, shared by 128 rows at a time, and the other rows (at
+                             most 256 nnz each) in row-aligned tiles; chosen at planning (PF_AUTO or PF_FLAT
+                             with the default tile, columns given) for split-row FLAT matrices of that shape
+                             (pf_plan_set_hybrid switches it) */
+    long long dense_rows; /* hybrid plans: rows summed by x windows */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -145,6 +152,9 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
  *   5 thread per row above 128 rows, block for one row, else groups of 128/rows lanes (2..32) per row.
  * The tile size (pf_plan_create_tuned: 512 or 1024 nnz) is the reference's P_NNZ 4 or 8. */
 int pf_plan_set_ladder(pf_plan *plan, int ladder);
+/* Plans that PF_AUTO made hybrid (pf_plan_info.hybrid): 0 = split-row FLAT tiles instead, 1 = back to
+ * hybrid.  Both give y within rounding of each other (the dense rows' partial sums differ in order). */
+int pf_plan_set_hybrid(pf_plan *plan, int hybrid);
 /* FLAT 1024/2048: 1 (default) = the first call records each tile's first row and later calls read it;
  * 0 = every call searches row_ptr inside the tile kernel (no recorded map, tiles dealt to XCDs by
  * position).  Both give the same y.  The reference times its own row map as a separate pre-pass

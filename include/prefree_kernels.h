@@ -71,10 +71,38 @@ typedef struct pfk_spmv_args {
     size_t owner_bytes;
     size_t row_map_bytes;
     size_t sched_bytes;
+    /* Hybrid plans (pfk_spmv_hybrid) only.  Dense rows (sorted columns) are summed by x windows of
+     * PFK_DENSE_WINDOW(dtype) columns; the rows between them form runs, each cut into row-aligned
+     * tiles of `tile` nnz (every run row holds at most PFK_ALIGN_ROW_MAX nnz).  ntiles counts the tiles
+     * of all runs. */
+    const int *dense_rows;   /* [n_dense] row indices, ascending */
+    int n_dense;
+    int n_win;               /* ceil(n / PFK_DENSE_WINDOW(dtype)) */
+    int n_runs;
+    const int *runs;         /* [5 * (n_runs + 1)]: tile_begin[n_runs + 1] (the last = ntiles), then row_begin,
+                                row_end, nnz_begin, nnz_end [n_runs + 1 each, the last unused] */
+    int *run_map;            /* [8 * ntiles] ints: per tile (f, row_ptr[f], l, row_ptr[l], kb, B0, last, 0) */
+    int *dense_seg;          /* [n_dense * (n_win + 1)] first nnz of each dense row in each window */
+    void *dense_part;        /* [n_dense * n_win] window partial sums, PFK_SLOT_BYTES(dtype) each */
+    size_t runs_bytes, run_map_bytes, dense_seg_bytes, dense_part_bytes;
 } pfk_spmv_args;
 
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
 #define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
+
+/* Columns per x window of a hybrid plan's dense-row kernel (64 KB of LDS), and dense rows per workgroup. */
+#define PFK_DENSE_WINDOW(dtype) ((dtype) == 0 ? 8192 : 16384)
+#define PFK_DENSE_GROUP 128
+
+/* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums and
+ * their combine, three launches.  map_ready 0: the call searches rows and segment bounds (and records them
+ * when run_map / dense_seg are given); 1: it reads them. */
+int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream);
+/* Planning scan of a hybrid plan: every row of at least dmin nnz as (row, row_ptr[row], row_ptr[row+1]) into
+ * list[3 * cap] in no particular order; counters[0] = such rows (may exceed cap: then the list is partial),
+ * counters[1] = listed rows whose columns decrease somewhere.  counters must be zero on entry. */
+int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *list, int cap, int *counters,
+                   void *stream);
 
 /* Ints of an x-window schedule. */
 #define PFK_SCHED_INTS(ntiles, cap) (16 + 8 * (cap) + (ntiles))

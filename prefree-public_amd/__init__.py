@@ -46,7 +46,7 @@ class RowStats(ctypes.Structure):
                 ("min_row_len", ctypes.c_longlong), ("n_empty_rows", ctypes.c_longlong),
                 ("n_decreasing", ctypes.c_longlong), ("row_ptr_first", ctypes.c_longlong),
                 ("row_ptr_last", ctypes.c_longlong), ("n_bad_cols", ctypes.c_longlong),
-                ("hist_log2", ctypes.c_longlong * 33)]
+                ("hist_log2", ctypes.c_longlong * 33), ("n_long_rows", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_ if k != "hist_log2"}
@@ -60,7 +60,8 @@ class PlanInfo(ctypes.Structure):
                 ("run_tiles", ctypes.c_int), ("keep_cached", ctypes.c_int), ("ntiles", ctypes.c_longlong),
                 ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
-                ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int)]
+                ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int), ("hybrid", ctypes.c_int),
+                ("dense_rows", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -94,7 +95,12 @@ class SpmvArgs(ctypes.Structure):
                 ("map_ready", ctypes.c_int), ("row_aligned", ctypes.c_int), ("sched", ctypes.c_void_p),
                 ("sched_cap", ctypes.c_longlong), ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int),
                 ("head_bytes", ctypes.c_size_t), ("tail_bytes", ctypes.c_size_t), ("owner_bytes", ctypes.c_size_t),
-                ("row_map_bytes", ctypes.c_size_t), ("sched_bytes", ctypes.c_size_t)]
+                ("row_map_bytes", ctypes.c_size_t), ("sched_bytes", ctypes.c_size_t),
+                ("dense_rows", ctypes.c_void_p), ("n_dense", ctypes.c_int), ("n_win", ctypes.c_int),
+                ("n_runs", ctypes.c_int), ("runs", ctypes.c_void_p), ("run_map", ctypes.c_void_p),
+                ("dense_seg", ctypes.c_void_p), ("dense_part", ctypes.c_void_p), ("runs_bytes", ctypes.c_size_t),
+                ("run_map_bytes", ctypes.c_size_t), ("dense_seg_bytes", ctypes.c_size_t),
+                ("dense_part_bytes", ctypes.c_size_t)]
 
 
 _lib = None
@@ -132,6 +138,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_chunk_nnz, [_vp, _ll])
         _sig(L.pf_plan_set_remember_rows, [_vp, _i])
         _sig(L.pf_plan_set_ladder, [_vp, _i])
+        _sig(L.pf_plan_set_hybrid, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -293,6 +300,10 @@ class Plan:
     def set_ladder(self, ladder):
         """pf_plan_set_ladder: PREFREE reduction ladder 1..5 (the reference tuner's code)."""
         _check(lib().pf_plan_set_ladder(self._h, int(ladder)), "pf_plan_set_ladder")
+
+    def set_hybrid(self, hybrid):
+        """pf_plan_set_hybrid: switch a hybrid plan to split-row tiles (False) and back (True)."""
+        _check(lib().pf_plan_set_hybrid(self._h, int(bool(hybrid))), "pf_plan_set_hybrid")
 
     def set_remember_rows(self, remember):
         """pf_plan_set_remember_rows: False = every call searches row_ptr (no recorded row map)."""

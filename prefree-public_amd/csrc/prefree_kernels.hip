@@ -1542,8 +1542,32 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
     }
 }
 
-template <typename T, int K, int MODE, bool PRIO = false>
-__global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, int *__restrict__ dbg)
+// Runs of a hybrid plan: the rows between two dense rows (or a matrix end), each
+// cut into row-aligned tiles of its own; `runs` holds, with R = nruns + 1,
+// tile_begin[R] then row_begin, row_end, nnz_begin, nnz_end [R each].
+struct RunTable {
+    const int *__restrict__ runs;
+    int nruns;
+};
+
+// The run holding run tile t: the largest i < nruns with tile_begin[i] <= t (a
+// wave-cooperative search; every probe stays inside the table).
+__device__ __forceinline__ int run_of_tile(const RunTable &rt, long long t, int lane)
+{
+    long long lo = 0, hi = rt.nruns;  // tile_begin[lo] <= t < tile_begin[hi] (tile_begin[nruns] = total)
+    while (hi - lo > 1) {
+        const long long step = (hi - lo + 63) >> 6;
+        const long long p = lo + (long long)lane * step;
+        const bool ok = lane > 0 && p < hi && (long long)rt.runs[p] <= t;
+        lo += (long long)__popcll(__ballot(ok)) * step;
+        hi = (lo + step < hi) ? lo + step : hi;
+    }
+    return (int)lo;
+}
+
+template <typename T, int K, int MODE, bool PRIO = false, bool RUNS = false>
+__global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, int *__restrict__ dbg,
+                                              RunTable rt = RunTable{nullptr, 0})
 {
     using S = RowsShape<T, K>;
     constexpr int VPT = S::kVPT;
@@ -1569,13 +1593,39 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     if (t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping
     const int m = a.m, nnz = a.nnz;
-    const bool last = t == a.ntiles - 1;
-    const int kb = (int)(t * K);
-    const int B0 = last ? nnz : kb + K;                // nominal nnz range [kb, B0)
-    const uint32_t ke = last ? (uint32_t)nnz + 1u : (uint32_t)(kb + K);
-
+    // Tile t's nominal nnz range [kb, B0); its rows end at row `lend` with
+    // row_ptr `nend` when it is the last tile (of the matrix, or of its run).
+    bool last = t == a.ntiles - 1;
+    int kb = (int)(t * K);
+    int B0 = last ? nnz : kb + K;
+    int lend = m, nend = nnz;
     int f = 0, rpf = 0, l = 0, rpl = 0;
-    if (MODE == kFlatMemo) {
+    if constexpr (RUNS) {
+        if (MODE == kFlatMemo) {  // recorded by the call that searched: (f, rpf, l, rpl), (kb, B0, last)
+            const int4 *mp = reinterpret_cast<const int4 *>(map);
+            const int4 e0 = mp[2 * t], e1 = mp[2 * t + 1];
+            f = e0.x; rpf = e0.y; l = e0.z; rpl = e0.w;
+            kb = e1.x; B0 = e1.y; last = e1.z != 0;
+            lend = l; nend = rpl;
+        } else {
+            const int i = run_of_tile(rt, t, lane);
+            const int R = rt.nruns + 1;
+            const int nb = rt.runs[3 * R + i], ne = rt.runs[4 * R + i];
+            kb = nb + (int)(t - rt.runs[i]) * K;
+            last = ne - kb <= K;
+            B0 = last ? ne : kb + K;
+            lend = rt.runs[2 * R + i];
+            nend = ne;
+        }
+    }
+    if constexpr (RUNS) {  // keep every load of the tile inside [0, nnz) and rows inside [0, m] whatever the tables hold
+        kb = min(max(kb, 0), nnz);
+        B0 = min(max(B0, kb), min(nnz, kb + K));
+        lend = min(max(lend, 0), m);
+    }
+    const uint32_t ke = last ? (uint32_t)nend + 1u : (uint32_t)(kb + K);
+
+    if (!RUNS && MODE == kFlatMemo) {
         const int2 *mp = reinterpret_cast<const int2 *>(map);
         const int2 e0 = mp[t], e1 = mp[t + 1];
         f = e0.x; rpf = e0.y; l = e1.x; rpl = e1.y;
@@ -1605,28 +1655,33 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
                                                          lane, r) + 1;
             if (lane == 0) {
                 s_info[0] = ff; s_info[1] = r;
-                if (MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
+                if (!RUNS && MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
             }
-        } else if (wave == 3) {  // l: first row with row_ptr >= ke (m for the last tile)
+        } else if (wave == 3) {  // l: first row with row_ptr >= ke (the run's or matrix's end for a last tile)
             int r = 0;
-            const int ll = last ? (r = a.rp[m], m)
+            const int ll = last ? (r = a.rp[lend], lend)
                                 : wave_search_lt_next(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane,
                                                       r) + 1;
             if (lane == 0) {
                 s_info[2] = ll; s_info[3] = r;
-                if (MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
+                if (!RUNS && MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
             }
         }
         lds_sync();
         f = s_info[0]; rpf = s_info[1]; l = s_info[2]; rpl = s_info[3];
+        if (RUNS && MODE == kFlatSearch && map && tid == 0) {
+            int4 *mp = reinterpret_cast<int4 *>(map);
+            mp[2 * t] = make_int4(f, rpf, l, rpl);
+            mp[2 * t + 1] = make_int4(kb, B0, last ? 1 : 0, 0);
+        }
     }
     if (tid == 0) { L.nw = 0; L.nb = 0; }
 
     // The tile's rows [f, l) and nnz [rpf, rpl); everything read below is
     // bounded by these checks even if row_ptr changed after planning.
     const int ovf = last ? 0 : rpl - (int)ke;  // nnz of the last row past the nominal range
-    const bool ok = f >= 0 && l >= f && l <= m && rpf >= kb && rpf <= rpl && rpl <= nnz &&
-                    (last ? (l == m && rpl == nnz) : (ovf >= 0 && ovf < kAlignRowMax));
+    const bool ok = f >= 0 && l >= f && l <= m && kb >= 0 && B0 >= kb && B0 <= nnz && rpf >= kb && rpf <= rpl &&
+                    rpl <= nnz && (last ? (l == lend && rpl == nend && rpl == B0) : (ovf >= 0 && ovf < kAlignRowMax));
     if (!ok && tid == 0) atomicOr(a.err, 1);
     const int f0 = ok ? f : 0;
     const int nr = ok ? l - f : 0;
@@ -1654,6 +1709,168 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     // instead of 32.55 (fp16); non-temporal in the short-row mode, where y is
     // a sixth of the bytes and device scope took C4 from 320 to 357 us.
     rows_reduce<T, K, PRIO ? kAuxNt : kAuxDev>(a, d, s_prod, s_rp, L);
+}
+
+// ---- k_dense: dense rows by x windows staged in LDS (hybrid plans) -----------
+//
+// A dense row (at least the plan's dense_min nnz, columns sorted) sweeps all of
+// x.  Summed tile by tile, each of its tiles drags its whole x span from L2
+// into a CU's L1 for a few nnz per line.  Here a workgroup stages one window
+// of W consecutive x entries in LDS and sums, for each of G dense rows, the
+// segment of the row whose columns fall in the window: x is read once per
+// G rows instead of once per row.  Workgroup (window w, group g) is dealt so
+// that an XCD takes a contiguous eighth of the windows (its x entries stay in
+// its L2).  Each (row, window) partial sum goes to part[row][w]; k_dense_sum
+// adds them in window order.  Segment bounds: MODE kFlatSearch finds them by
+// a wave search of the row's columns and records them in seg; kFlatMemo reads
+// them.  C5 (1000 rows of 50k-500k nnz, 280M nnz): 584 us against 742 us for
+// the same rows in split-row tiles with the x-window schedule.
+
+template <typename T>
+struct DenseShape {
+    static constexpr int kW = sizeof(T) == 8 ? 8192 : 16384;  // x window: 64 KB of LDS
+    static constexpr int kG = 128;                            // dense rows per workgroup
+    static constexpr int kU = 8;                              // loads in flight per lane
+};
+
+struct DenseArgs {
+    const int *__restrict__ rows;  // dense rows, ascending
+    int nd;
+    int nwin;
+    int ngroups;
+    int *__restrict__ seg;         // [nd][nwin + 1] first nnz of each window (recorded / read)
+    void *__restrict__ part;       // [nd][nwin] partial sums (accumulation type)
+};
+
+// First j in [a, b) with col[j] >= v (b if none); col sorted in [a, b).  One wave.
+__device__ __forceinline__ int wave_lower_bound(const int *__restrict__ col, int a, int b, int v, int lane)
+{
+    int lo = a - 1, hi = b;  // col[lo] < v, col[hi] >= v, both virtual at the ends
+    while (hi - lo > 1) {
+        const int step = (hi - lo + 63) >> 6;
+        const int p = lo + lane * step;
+        const bool ok = lane > 0 && p < hi && col[p] < v;
+        lo += __popcll(__ballot(ok)) * step;
+        hi = min(lo + step, hi);
+    }
+    return hi;
+}
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
+{
+    using P = acc_t<T>;
+    constexpr int W = DenseShape<T>::kW, G = DenseShape<T>::kG, U = DenseShape<T>::kU;
+    __shared__ __attribute__((aligned(16))) T sx[W];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
+    const int wper = (d.nwin + kXcds - 1) / kXcds;
+    const int w = xcd * wper + q % wper, g = q / wper;
+    if (w >= d.nwin || g >= d.ngroups)
+        return;
+    const int m = a.m, nnz = a.nnz;
+    const int c0 = w * W;
+    {  // the window x[c0, c0 + W) into LDS, 16 bytes per lane and load; zeros past n
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + c0, (long long)min(W, a.n - c0) * (long long)sizeof(T));
+        constexpr int kPer = 16 / (int)sizeof(T);
+#pragma unroll 4
+        for (int i = tid; i < W / kPer; i += kBS)
+            *reinterpret_cast<u32x4 *>(sx + i * kPer) = __builtin_amdgcn_raw_buffer_load_b128(rx, i * 16, 0, 0);
+    }
+    lds_sync();
+    const int i_end = min(d.nd, (g + 1) * G);
+    for (int i = g * G + wave; i < i_end; i += kWaves) {
+        const int r = d.rows[i];
+        if (r < 0 || r >= m) {  // a table entry that is not a row: skip it, report it
+            if (lane == 0) atomicOr(a.err, 1);
+            continue;
+        }
+        const int a0 = min(max(a.rp[r], 0), nnz);
+        const int a1 = min(max(a.rp[r + 1], a0), nnz);
+        int s, e;
+        int *sg = d.seg + (long long)i * (d.nwin + 1);
+        if (MODE == kFlatMemo) {
+            s = min(max(sg[w], a0), a1);
+            e = min(max(sg[w + 1], s), a1);
+        } else {
+            s = wave_lower_bound(a.col, a0, a1, c0, lane);
+            e = w == d.nwin - 1 ? a1 : wave_lower_bound(a.col, s, a1, c0 + W, lane);
+            if (MODE == kFlatSearch && d.seg && lane == 0) {
+                sg[w] = s;
+                if (w == d.nwin - 1) sg[d.nwin] = e;
+            }
+        }
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
+        P acc = P(0);
+        for (int j = 0; j < e - s; j += kWave * U) {
+            int c[U];
+            T v[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k)
+                load1(rc, rv, j + k * kWave + lane, c[k], v[k]);
+#pragma unroll
+            for (int k = 0; k < U; ++k) {  // no product for slots past the segment (x may hold inf or NaN)
+                const T xv = sx[(c[k] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
+                if (j + k * kWave + lane < e - s)
+                    acc += P(v[k]) * P(xv);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) static_cast<P *>(d.part)[(long long)i * d.nwin + w] = acc;
+    }
+}
+
+// y of each dense row: its window partial sums in window order.
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_dense_sum(Args<T> a, DenseArgs d)
+{
+    using P = acc_t<T>;
+    const int i = blockIdx.x * kBS + threadIdx.x;
+    if (i >= d.nd)
+        return;
+    const int r = d.rows[i];
+    if (r < 0 || r >= a.m)
+        return;
+    const P *pp = static_cast<const P *>(d.part) + (long long)i * d.nwin;
+    P sum = P(0);
+    for (int w = 0; w < d.nwin; ++w)
+        sum += pp[w];
+    a.y[r] = T(sum);
+}
+
+// Planning scan of a hybrid plan: every row of at least `dmin` nnz goes to the
+// list as (row, row_ptr[row], row_ptr[row + 1]) (in no particular order; the
+// host sorts it), and counters[1] counts the decreasing column pairs inside
+// the listed rows (a hybrid plan needs sorted columns).
+__global__ __launch_bounds__(kBS) void k_dense_scan(const int *__restrict__ rp, int m, int dmin, int *__restrict__ list,
+                                                    int cap, int *__restrict__ counters)
+{
+    for (long long r = (long long)blockIdx.x * kBS + threadIdx.x; r < m; r += (long long)gridDim.x * kBS) {
+        const int a0 = rp[r], a1 = rp[r + 1];
+        if (a1 - a0 >= dmin) {
+            const int k = atomicAdd(counters, 1);
+            if (k < cap) {
+                list[3 * k] = (int)r;
+                list[3 * k + 1] = a0;
+                list[3 * k + 2] = a1;
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBS) void k_dense_sorted(const int *__restrict__ col, const int *__restrict__ list,
+                                                      int cap, int *__restrict__ counters)
+{
+    const int nk = min(cap, counters[0]);
+    int bad = 0;
+    for (int k = blockIdx.y; k < nk; k += gridDim.y) {
+        const int a0 = list[3 * k + 1], a1 = list[3 * k + 2];
+        for (long long j = a0 + (long long)blockIdx.x * kBS + threadIdx.x; j + 1 < a1; j += (long long)gridDim.x * kBS)
+            bad += col[j] > col[j + 1];
+    }
+    if (__ballot(bad != 0) && (threadIdx.x & (kWave - 1)) == 0)
+        atomicAdd(counters + 1, 1);
 }
 
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
@@ -2355,7 +2572,7 @@ __global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ id
 // Layout of the statistics block (unsigned long long):
 enum StatSlot {
     kStMax = 0, kStMin = 1, kStEmpty = 2, kStDec = 3, kStFirst = 4, kStLast = 5, kStBadCol = 6,
-    kStHist = 7, kStCount = 44
+    kStHist = 7, kStOverAlign = 40, kStCount = 44
 };
 
 __global__ void k_stats_init(unsigned long long *out)
@@ -2369,12 +2586,12 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
                                                    unsigned long long *__restrict__ out)
 {
     __shared__ unsigned int s_hist[33];
-    __shared__ unsigned int s_max, s_min, s_empty, s_dec;
+    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over;
     const int tid = threadIdx.x;
     if (tid < 33) s_hist[tid] = 0;
-    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; }
+    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; }
     __syncthreads();
-    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0;
+    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0;
     for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
         int len = rp[r + 1] - rp[r];
         if (len < 0) { ++ldec; len = 0; }
@@ -2382,12 +2599,14 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         lmax = max(lmax, u);
         lmin = min(lmin, u);
         lempty += (u == 0);
+        lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
         atomicAdd(&s_hist[u == 0 ? 0 : 32 - __clz(u)], 1u);
     }
     atomicMax(&s_max, lmax);
     atomicMin(&s_min, lmin);
     atomicAdd(&s_empty, lempty);
     atomicAdd(&s_dec, ldec);
+    atomicAdd(&s_over, lover);
     __syncthreads();
     if (tid < 33 && s_hist[tid]) atomicAdd(out + kStHist + tid, (unsigned long long)s_hist[tid]);
     if (tid == 0) {
@@ -2395,6 +2614,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         atomicMin(out + kStMin, (unsigned long long)s_min);
         atomicAdd(out + kStEmpty, (unsigned long long)s_empty);
         atomicAdd(out + kStDec, (unsigned long long)s_dec);
+        atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
         if (blockIdx.x == 0) {
             out[kStFirst] = (unsigned long long)(long long)rp[0];
             out[kStLast] = (unsigned long long)(long long)rp[m];
@@ -2749,6 +2969,39 @@ int launch_prefree(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
+// A hybrid plan's call: run tiles (k_rows over the run table), the dense rows'
+// window sums (k_dense), their combine (k_dense_sum).
+template <typename T, int K>
+int launch_hybrid(const pfk_spmv_args *a, void *stream)
+{
+    Args<T> r = make_args<T>(a);
+    if (r.ntiles > 0) chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8);
+    const RunTable rt{a->runs, a->n_runs};
+    const bool memo = a->map_ready && a->run_map && a->dense_seg;
+    const bool prio = (long long)a->nnz < 4LL * a->m;
+    const dim3 rgrid((unsigned)(r.g8 * kXcds));
+    if (a->ntiles == 0)  // every row is dense
+        ;
+    else if (memo && prio)
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+    else if (memo)
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+    else
+        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+    if (a->ntiles > 0) PFK_LAUNCHED("k_rows (runs)");
+    const int ngroups = (a->n_dense + PFK_DENSE_GROUP - 1) / PFK_DENSE_GROUP;
+    const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, a->dense_seg, a->dense_part};
+    const unsigned dgrid = (unsigned)(kXcds * ((a->n_win + kXcds - 1) / kXcds) * ngroups);
+    if (memo)
+        hipLaunchKernelGGL((k_dense<T, kFlatMemo>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
+    else
+        hipLaunchKernelGGL((k_dense<T, kFlatSearch>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
+    PFK_LAUNCHED("k_dense");
+    hipLaunchKernelGGL((k_dense_sum<T>), dim3((unsigned)((a->n_dense + kBS - 1) / kBS)), dim3(kBS), 0, S(stream), r, d);
+    PFK_LAUNCHED("k_dense_sum");
+    return PF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2770,6 +3023,49 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream)
          : dtype == PF_F16 ? dispatch_flat<half_t>(a, stream) : PF_ERR_INVALID;
+}
+
+int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
+{
+    if (!a) return PF_ERR_INVALID;
+    if (dtype != PF_F64 && dtype != PF_F32) {
+        snprintf(g_err, sizeof g_err, "hybrid plans are fp64 or fp32");
+        return PF_ERR_UNSUPPORTED;
+    }
+    if (a->m == 0 && a->nnz == 0) return PF_OK;
+    pfk_spmv_args v = *a;  // a hybrid plan may have no run tiles (every row dense)
+    v.ntiles = a->ntiles > 0 ? a->ntiles : 1;
+    if (a->ntiles < 0 || !args_ok(&v, false) || a->n_dense < 1 || a->n_runs < 1 || !a->dense_rows || !a->runs ||
+        !a->dense_part ||
+        (a->tile != 1024 && a->tile != 2048)) {
+        snprintf(g_err, sizeof g_err, "hybrid call: missing tables or tile %d", a->tile);
+        return PF_ERR_INVALID;
+    }
+    const long long win = PFK_DENSE_WINDOW(dtype);
+    if (a->n_win != (int)((a->n + win - 1) / win) || a->n_win < 1) {
+        snprintf(g_err, sizeof g_err, "hybrid call: %d x windows for n = %d", a->n_win, a->n);
+        return PF_ERR_INVALID;
+    }
+    const long long nd = a->n_dense, nw = a->n_win;
+    if (!room(a->runs, a->runs_bytes, 5LL * (a->n_runs + 1) * 4, "run table") ||
+        !room(a->dense_part, a->dense_part_bytes, nd * nw * PFK_SLOT_BYTES(dtype), "dense partial sums") ||
+        (a->run_map && !room(a->run_map, a->run_map_bytes, a->ntiles * 32, "run tile map")) ||
+        (a->dense_seg && !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")))
+        return PF_ERR_INVALID;
+    if (dtype == PF_F64) return a->tile == 1024 ? launch_hybrid<double, 1024>(a, stream) : launch_hybrid<double, 2048>(a, stream);
+    return a->tile == 1024 ? launch_hybrid<float, 1024>(a, stream) : launch_hybrid<float, 2048>(a, stream);
+}
+
+int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *list, int cap, int *counters, void *stream)
+{
+    if (!row_ptr || !col || !list || !counters || m < 1 || dmin < 1 || cap < 1) return PF_ERR_INVALID;
+    hipLaunchKernelGGL(k_dense_scan, dim3(grid_for(m, kBS, 2048)), dim3(kBS), 0, S(stream), row_ptr, m, dmin, list,
+                       cap, counters);
+    PFK_LAUNCHED("k_dense_scan");
+    hipLaunchKernelGGL(k_dense_sorted, dim3(64, (unsigned)std::min(cap, 4096)), dim3(kBS), 0, S(stream), col, list,
+                       cap, counters);
+    PFK_LAUNCHED("k_dense_sorted");
+    return PF_OK;
 }
 
 long long pfk_flat_grid(long long ntiles, int tile, long long chunk_nnz)

@@ -352,6 +352,15 @@ struct pf_plan {
     bool remember_rows = true;  // false: every call searches row_ptr (no row map, no schedule)
     // bytes of the workspace behind each array (passed to the kernel layer, which checks them)
     size_t head_bytes = 0, tail_bytes = 0, owner_bytes = 0, row_map_bytes = 0, sched_bytes = 0;
+    // hybrid plans: dense rows by x windows, the rows between them in runs of row-aligned tiles
+    bool hybrid = false;     // the hybrid path is in use (it can be switched off: the split-row layout stays)
+    void *ws_hyb = nullptr;  // its tables: dense rows, runs, run tile map, segment bounds, partial sums
+    int n_dense = 0, n_runs = 0, n_win = 0, run_tile = 0;
+    long long run_tiles = 0, run_chunk = 0;
+    int *dense_rows = nullptr, *runs = nullptr, *run_map = nullptr, *dense_seg = nullptr;
+    void *dense_part = nullptr;
+    size_t runs_bytes = 0, run_map_bytes = 0, dense_seg_bytes = 0, dense_part_bytes = 0;
+    bool hyb_map_ready = false;
 };
 
 namespace {
@@ -446,11 +455,132 @@ int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
     return rc;
 }
 
+// Dense-row threshold of a hybrid plan: a power of two at least 4096 and at
+// least 256 n / W, so that a dense row averages 256 or more nnz per x window.
+long long dense_min(long long n, int dtype)
+{
+    const long long want = std::max(4096LL, (256LL * n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
+    long long t = 4096;
+    while (t < want) t <<= 1;
+    return t;
+}
+
+// Rows of at least 2^j nnz, from the log2 histogram (bucket k: 2^(k-1) <= len < 2^k).
+long long rows_at_least_pow2(const pf_row_stats &s, int j)
+{
+    long long c = 0;
+    for (int k = j + 1; k < 33; ++k) c += s.hist_log2[k];
+    return c;
+}
+
+// A hybrid plan fits matrices whose long rows (over 256 nnz) are all dense
+// (dense_min or more) and whose columns are checked (the scan needs col).
+bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_plan_info &info, const int *d_col)
+{
+    if (!d_col || (dtype != PF_F64 && dtype != PF_F32) || info.variant != PF_FLAT || info.row_aligned ||
+        !uses_row_map(info.variant, info.tile) || s.n_long_rows < 1)
+        return false;
+    const long long t = dense_min(n, dtype);
+    int j = 0;
+    while ((1LL << j) < t) ++j;
+    if (rows_at_least_pow2(s, j) != s.n_long_rows) return false;
+    const long long nwin = (n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype);
+    return s.n_long_rows * (nwin + 1) <= (64LL << 20);  // segment table under 256 MB
+}
+
+// Adds the hybrid path to a split-row FLAT plan when its long rows have sorted
+// columns: lists them (a planning scan), cuts the rows between them into runs
+// of row-aligned tiles and allocates the tables.  Leaves the plan as it is
+// (split-row tiles) otherwise.
+int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
+{
+    const int dtype = p->info.dtype;
+    const long long cap = p->stats.n_long_rows;
+    const int dmin = (int)dense_min(p->n, dtype);
+    int *tmp = nullptr;
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&tmp), (size_t)(2 + 3 * cap) * sizeof(int)), "dense scan buffer");
+    std::vector<int> list((size_t)(3 * cap));
+    int cnt[2] = {0, 0};
+    int st = pfk_fill_zero(tmp, 2 * sizeof(int), stream);
+    if (st == PF_OK) st = pfk_dense_scan(d_row_ptr, d_col, p->m, dmin, tmp + 2, (int)cap, tmp, stream);
+    if (st == PF_OK) st = pfk_memcpy_d2h(cnt, tmp, sizeof cnt, stream);
+    if (st == PF_OK) st = pfk_memcpy_d2h(list.data(), tmp + 2, list.size() * sizeof(int), stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream);
+    pfk_free(tmp);
+    if (st != PF_OK) return from_kernel_layer(st, "dense scan");
+    if (cnt[0] != cap || cnt[1] != 0) return PF_OK;  // unsorted columns in a long row: stay split-row
+
+    // Dense rows ascending, and the runs of rows between them.
+    std::vector<int> order((size_t)cap);
+    for (long long k = 0; k < cap; ++k) order[(size_t)k] = (int)k;
+    std::sort(order.begin(), order.end(), [&](int x, int y) { return list[3 * (size_t)x] < list[3 * (size_t)y]; });
+    const int nd = (int)cap, nruns = nd + 1, R = nruns + 1;
+    std::vector<int> rows((size_t)nd), runs((size_t)5 * R, 0);
+    long long short_rows = 0, short_nnz = 0;
+    for (int i = 0; i < nruns; ++i) {
+        const int rb = i == 0 ? 0 : list[3 * (size_t)order[(size_t)i - 1]] + 1;
+        const int re = i == nd ? p->m : list[3 * (size_t)order[(size_t)i]];
+        const int nb = i == 0 ? 0 : list[3 * (size_t)order[(size_t)i - 1] + 2];
+        const int ne = i == nd ? p->nnz : list[3 * (size_t)order[(size_t)i] + 1];
+        runs[(size_t)R + i] = rb;
+        runs[(size_t)2 * R + i] = re;
+        runs[(size_t)3 * R + i] = nb;
+        runs[(size_t)4 * R + i] = ne;
+        if (i < nd) rows[(size_t)i] = list[3 * (size_t)order[(size_t)i]];
+        short_rows += re - rb;
+        short_nnz += ne - nb;
+    }
+    // Run tiles: the FLAT rule for the short rows alone.
+    const int K = (dtype == PF_F64 && short_nnz >= 4 * short_rows) ? 1024 : 2048;
+    long long tiles = 0;
+    for (int i = 0; i < nruns; ++i) {
+        runs[(size_t)i] = (int)tiles;
+        const long long rr = runs[(size_t)2 * R + i] - runs[(size_t)R + i];
+        const long long nz = runs[(size_t)4 * R + i] - runs[(size_t)3 * R + i];
+        tiles += rr > 0 ? std::max(1LL, (nz + K - 1) / K) : 0;
+    }
+    runs[(size_t)nruns] = (int)tiles;  // 0 when every row is dense: only the dense kernels run
+    const int nwin = (int)((p->n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
+    auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t b_rows = up((size_t)nd * 4), b_runs = up((size_t)5 * R * 4), b_map = up((size_t)tiles * 32),
+                 b_seg = up((size_t)nd * (nwin + 1) * 4), b_part = up((size_t)nd * nwin * slot_bytes(dtype));
+    void *w = nullptr;
+    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part), "hybrid tables");
+    char *c = static_cast<char *>(w);
+    p->ws_hyb = w;
+    p->dense_rows = reinterpret_cast<int *>(c);
+    p->runs = reinterpret_cast<int *>(c + b_rows);
+    p->run_map = reinterpret_cast<int *>(c + b_rows + b_runs);
+    p->dense_seg = reinterpret_cast<int *>(c + b_rows + b_runs + b_map);
+    p->dense_part = c + b_rows + b_runs + b_map + b_seg;
+    p->runs_bytes = b_runs;
+    p->run_map_bytes = b_map;
+    p->dense_seg_bytes = b_seg;
+    p->dense_part_bytes = b_part;
+    p->n_dense = nd;
+    p->n_runs = nruns;
+    p->n_win = nwin;
+    p->run_tile = K;
+    p->run_tiles = tiles;
+    p->run_chunk = short_nnz < 4 * short_rows ? 0 : kChunkNnz;
+    st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
+    if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream);
+    if (st != PF_OK) return from_kernel_layer(st, "hybrid tables");
+    p->hybrid = true;
+    p->info.hybrid = 1;
+    p->info.dense_rows = nd;
+    return PF_OK;
+}
+
 // The plan for a validated matrix with known statistics (shared by plan
 // creation and the tuner's candidates): workspace allocated and initialised.
+// With columns given, PF_AUTO and PF_FLAT plans of the default tile also try
+// the hybrid path.
 int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
-               void *stream, pf_plan **plan)
+               void *stream, pf_plan **plan, const int *d_col = nullptr)
 {
+    const bool want_hybrid = (variant == PF_AUTO || variant == PF_FLAT) && tile <= 0;
     pf_plan_info info;
     const int st = plan_info(s, n, dtype, variant, tile, &info);
     if (st != PF_OK) return st;
@@ -469,6 +599,15 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     plan_carve(p, w);
     rc = plan_init(p, d_row_ptr, stream);
     if (rc == PF_OK) rc = pfk_stream_sync(stream);
+    if (rc == PF_OK && want_hybrid && hybrid_candidate(s, n, dtype, p->info, d_col)) {
+        rc = try_hybrid(p, d_row_ptr, d_col, stream);
+        if (rc != PF_OK) {
+            pfk_free(p->ws_hyb);
+            pfk_free(p->ws);
+            delete p;
+            return rc;
+        }
+    }
     if (rc != PF_OK) {
         pfk_free(p->ws);
         delete p;
@@ -516,6 +655,7 @@ int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int
     out->row_ptr_last = (long long)h[5];
     out->n_bad_cols = (d_col && nnz > 0) ? (long long)h[6] : (nnz > 0 ? -1 : 0);
     for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
+    out->n_long_rows = (long long)h[40];
     return PF_OK;
 }
 
@@ -601,7 +741,7 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
         st = check_csr_stats(s, nnz);
         if (st != PF_OK) return st;
     }
-    return plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan);
+    return plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan, d_col);
 }
 
 int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz, int dtype,
@@ -667,6 +807,16 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz)
     return PF_OK;
 }
 
+int pf_plan_set_hybrid(pf_plan *plan, int hybrid)
+{
+    if (!plan || (hybrid != 0 && hybrid != 1)) return fail(PF_ERR_INVALID, "hybrid must be 0 or 1");
+    if (hybrid && !plan->ws_hyb)
+        return fail(PF_ERR_UNSUPPORTED, "this plan has no hybrid tables (no dense rows with sorted columns)");
+    plan->hybrid = hybrid != 0;
+    plan->info.hybrid = hybrid;
+    return PF_OK;
+}
+
 int pf_plan_set_ladder(pf_plan *plan, int ladder)
 {
     if (!plan || ladder < 1 || ladder > 5) return fail(PF_ERR_INVALID, "ladder must be 1..5");
@@ -678,7 +828,10 @@ int pf_plan_set_ladder(pf_plan *plan, int ladder)
 int pf_plan_set_remember_rows(pf_plan *plan, int remember)
 {
     if (!plan || (remember != 0 && remember != 1)) return fail(PF_ERR_INVALID, "remember must be 0 or 1");
-    if (remember && !plan->remember_rows) plan->map_ready = false;  // the next call records the map afresh
+    if (remember && !plan->remember_rows) {  // the next call records the map afresh
+        plan->map_ready = false;
+        plan->hyb_map_ready = false;
+    }
     plan->remember_rows = remember != 0;
     return PF_OK;
 }
@@ -728,9 +881,33 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.owner_bytes = plan->owner_bytes;
     a.row_map_bytes = plan->row_map_bytes;
     a.sched_bytes = plan->sched_bytes;
+    const int dt = plan->info.dtype;
+    if (plan->hybrid) {
+        a.ntiles = plan->run_tiles;
+        a.tile = plan->run_tile;
+        a.row_aligned = 1;
+        a.chunk_nnz = plan->run_chunk;
+        a.row_map = nullptr;
+        a.sched = nullptr;
+        a.dense_rows = plan->dense_rows;
+        a.n_dense = plan->n_dense;
+        a.n_win = plan->n_win;
+        a.n_runs = plan->n_runs;
+        a.runs = plan->runs;
+        a.runs_bytes = plan->runs_bytes;
+        a.run_map = plan->remember_rows ? plan->run_map : nullptr;
+        a.run_map_bytes = plan->run_map_bytes;
+        a.dense_seg = plan->remember_rows ? plan->dense_seg : nullptr;
+        a.dense_seg_bytes = plan->dense_seg_bytes;
+        a.dense_part = plan->dense_part;
+        a.dense_part_bytes = plan->dense_part_bytes;
+        a.map_ready = (plan->remember_rows && plan->hyb_map_ready) ? 1 : 0;
+        PF_TRY(pfk_spmv_hybrid(dt, &a, stream), "hybrid kernels");
+        if (plan->remember_rows) plan->hyb_map_ready = true;  // later calls read what this one recorded
+        return PF_OK;
+    }
     if (a.sched && !plan->map_ready)  // the recording call starts from empty lists
         PF_TRY(pfk_fill_zero(a.sched, 16 * sizeof(int), stream), "schedule reset");
-    const int dt = plan->info.dtype;
     switch (plan->info.variant) {
     case PF_ADAPTIVE:
         PF_TRY(pfk_spmv_adaptive(dt, &a, stream), "adaptive kernel");
@@ -765,7 +942,11 @@ int pf_plan_check(pf_plan *plan, void *stream)
 int pf_plan_destroy(pf_plan *plan)
 {
     if (!plan) return PF_OK;
-    const int st = pfk_free(plan->ws);
+    int st = pfk_free(plan->ws);
+    if (plan->ws_hyb) {
+        const int st2 = pfk_free(plan->ws_hyb);
+        if (st == PF_OK) st = st2;
+    }
     delete plan;
     return st == PF_OK ? PF_OK : from_kernel_layer(st, "free workspace");
 }
@@ -972,21 +1153,7 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
         }
     }
     if (best_plan) {  // move the winner into the caller's plan
-        std::swap(plan->info, best_plan->info);
-        std::swap(plan->ws, best_plan->ws);
-        std::swap(plan->head, best_plan->head);
-        std::swap(plan->tail, best_plan->tail);
-        std::swap(plan->owner, best_plan->owner);
-        std::swap(plan->err, best_plan->err);
-        std::swap(plan->row_map, best_plan->row_map);
-        std::swap(plan->map_ready, best_plan->map_ready);
-        std::swap(plan->sched, best_plan->sched);
-        std::swap(plan->sched_cap, best_plan->sched_cap);
-        std::swap(plan->head_bytes, best_plan->head_bytes);
-        std::swap(plan->tail_bytes, best_plan->tail_bytes);
-        std::swap(plan->owner_bytes, best_plan->owner_bytes);
-        std::swap(plan->row_map_bytes, best_plan->row_map_bytes);
-        std::swap(plan->sched_bytes, best_plan->sched_bytes);
+        std::swap(*plan, *best_plan);  // the same matrix: every field is the winner's
         pf_plan_destroy(best_plan);
     }
     // y = A x with the chosen configuration, so that the caller's y is defined.

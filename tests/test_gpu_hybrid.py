@@ -1,0 +1,153 @@
+"""Hybrid plans on the GPU: dense rows by x windows, the rows between them in runs of row-aligned tiles.
+
+PF_AUTO makes a split-row FLAT plan hybrid when every row longer than 256 nnz
+is dense (at least the plan's threshold, 4096 nnz or more) and those rows'
+columns are sorted.  Checked through the C ABI against the CPU oracle:
+known-answer values bit for bit, U[-1,1] values within 1e-12 (f64) / 1e-5
+(f32) per row normalised by sum |a_ij x_j|, the first call (which searches rows
+and window bounds and records them) and later calls (which read them)
+bit-identical, the split-row path of the same plan within tolerance, and
+edge shapes: dense first and last rows, adjacent dense rows, empty rows and
+empty runs between them, rectangular matrices, duplicate columns.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import prefree_amd as pf
+from csr_cases import csr_from_lengths
+from gpu_util import NP, TORCH, assert_parity, dev, gpu_spmv, kat_exact_possible
+
+pytestmark = pytest.mark.gpu
+
+
+def _lengths(pattern, rng, dense_len=(9000, 30000), short=(0, 60)):
+    out = []
+    for p in pattern:
+        if p == "D":
+            out.append(int(rng.integers(*dense_len)))
+        elif p == "E":
+            out.append(0)
+        else:
+            out += [int(v) for v in rng.integers(short[0], short[1] + 1, size=int(p))]
+    return out
+
+
+SHAPES = {
+    "dense_first_and_last": "D 300 D 500 D",
+    "adjacent_dense": "40 D D D 200 D D 10",
+    "empty_runs": "E E D E D E E E D 100 D E",
+    "only_dense": "D D D",
+    "single_dense_middle": "1000 D 1000",
+    "many_short_runs": " ".join(["D 3"] * 60),
+}
+
+
+def _case(name, n=60000, seed=3):
+    rng = np.random.default_rng(seed)
+    lengths = _lengths(SHAPES[name].split(), rng)
+    rp, col = csr_from_lengths(lengths, n, rng)
+    return rp, col, n
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_hybrid_shapes(name, dtype):
+    rp, col, n = _case(name)
+    rng = np.random.default_rng(1)
+    kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
+    y, info = gpu_spmv(rp, col, kv, kx, "flat", dtype=dtype)
+    assert info["hybrid"] == 1 and info["dense_rows"] == int(np.sum(np.diff(rp) > 256)), info
+    assert_parity(rp, col, kv, kx, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"{name}/kat")
+    val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+    x = rng.uniform(-1, 1, n).astype(NP[dtype])
+    y, _ = gpu_spmv(rp, col, val, x, "flat", dtype=dtype)
+    assert_parity(rp, col, val, x, y, dtype, what=f"{name}/random")
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+def test_hybrid_scaled_c5(dtype):
+    rp, col, v = pf.synth_csr(5, seed=9, scale_n=200000, dtypes=(dtype,))
+    x = pf.synth_x(5, len(rp) - 1, seed=9, dtypes=(dtype,))[dtype]
+    y, info = gpu_spmv(rp, col, v[dtype], x, "auto", dtype=dtype)
+    assert info["hybrid"] == 1 and info["dense_rows"] == 200
+    assert_parity(rp, col, v[dtype], x, y, dtype, what="C5/200000")
+    kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(len(x), NP[dtype])
+    ky, _ = gpu_spmv(rp, col, kv, kx, "auto", dtype=dtype)
+    assert_parity(rp, col, kv, kx, ky, dtype, exact=kat_exact_possible(rp, dtype), what="C5/200000/kat")
+
+
+def test_hybrid_rectangular_and_duplicates():
+    rng = np.random.default_rng(7)
+    lengths = _lengths("500 D 20 D 800".split(), rng)
+    # n = 100000 columns for 1.3k rows: several x windows; duplicate (non-decreasing) columns in dense rows
+    rp, col = csr_from_lengths(lengths, 100000, rng, distinct=False)
+    for r in np.flatnonzero(np.diff(rp) > 256):
+        assert np.all(np.diff(col[rp[r]:rp[r + 1]]) >= 0)
+    val, x = oracle.initvec(len(col)), oracle.initvec(100000)
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["hybrid"] == 1
+    assert_parity(rp, col, val, x, y, "f64", exact=True, what="rectangular")
+
+
+def test_hybrid_refused_for_unsorted_or_medium_rows():
+    rng = np.random.default_rng(8)
+    lengths = _lengths("300 D 300 D".split(), rng)
+    rp, col = csr_from_lengths(lengths, 50000, rng, sorted_cols=False)
+    val, x = oracle.initvec(len(col)), oracle.initvec(50000)
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["hybrid"] == 0  # unsorted columns in the dense rows: split-row tiles
+    assert_parity(rp, col, val, x, y, "f64", exact=True, what="unsorted")
+    rp2, col2 = csr_from_lengths(lengths + [700], 50000, rng)  # a 700-nnz row is long but not dense
+    val2 = oracle.initvec(len(col2))
+    y2, info2 = gpu_spmv(rp2, col2, val2, x, "flat")
+    assert info2["hybrid"] == 0
+    assert_parity(rp2, col2, val2, x, y2, "f64", exact=True, what="medium row")
+
+
+def test_hybrid_switch_and_search_modes():
+    rp, col, n = _case("adjacent_dense", seed=11)
+    rng = np.random.default_rng(12)
+    val = rng.uniform(-1, 1, len(col))
+    x = rng.uniform(-1, 1, n)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    m = len(rp) - 1
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    outs = {}
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "flat") as p:
+        assert p.info.hybrid == 1
+        for label, setup in (("first", None), ("memo", None), ("split", lambda: p.set_hybrid(False)),
+                             ("back", lambda: p.set_hybrid(True)), ("search", lambda: p.set_remember_rows(False)),
+                             ("rerecord", lambda: p.set_remember_rows(True)), ("memo2", None)):
+            if setup:
+                setup()
+            y.fill_(float("nan"))
+            p.execute(d_rp, d_col, d_val, d_x, y)
+            p.check()
+            outs[label] = y.cpu().numpy()
+    for label in ("memo", "back", "search", "rerecord", "memo2"):
+        assert np.array_equal(outs[label], outs["first"]), label
+    assert_parity(rp, col, val, x, outs["first"], "f64", what="hybrid")
+    assert_parity(rp, col, val, x, outs["split"], "f64", what="split-row")
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "flat", 2048) as p:  # explicit tile: never hybrid
+        assert p.info.hybrid == 0
+        with pytest.raises(pf.PrefreeError):
+            p.set_hybrid(True)
+
+
+def test_hybrid_special_values():
+    # NaN and infinities in x and val propagate exactly as in the serial sum (integer values otherwise),
+    # including x entries next to a segment's end, whose products must not be formed.
+    rp, col, n = _case("dense_first_and_last", seed=5)
+    rng = np.random.default_rng(6)
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    for arr in (val, x):
+        idx = rng.choice(len(arr), size=max(1, len(arr) // 700), replace=False)
+        arr[idx] = rng.choice([np.nan, np.inf, -np.inf], size=len(idx))
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["hybrid"] == 1
+    ref = oracle.spmv_serial(rp, col, val, x)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(y[ok], ref[ok])
