@@ -73,6 +73,8 @@ def cfg_name(cfg, dt):
 def kernel_name(info):
     """The dominant kernel of a plan's step (prefree-public_amd/csrc/prefree_kernels.hip)."""
     v = info["variant_name"]
+    if info.get("hybrid"):
+        return "k_dense + k_rows (runs)"
     if v == "adaptive":
         return "k_wave"
     if v == "prefree":
@@ -230,6 +232,10 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
             p.set_chunk_nnz(args.chunk_nnz)
         if args.ladder and p.info.variant == pf.PREFREE:
             p.set_ladder(args.ladder)
+        if args.hybrid == 0 and p.info.hybrid:
+            p.set_hybrid(False)
+        if args.x_halves >= 0 and p.info.hybrid:
+            p.set_x_halves(args.x_halves)
         return p
 
     t_plan = time.perf_counter()
@@ -263,7 +269,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
     gbs = bytes_eff / (ev_ms * 1e6)
     key = f"C{cfg}-{dt}-{info['variant_name']}-{info['tile']}" + (
         f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
-        "-rows" if info["row_aligned"] else "")
+        "-rows" if info["row_aligned"] else "") + ("-hybrid" if info["hybrid"] else "")
     traffic = traffic_from_profiles(key)
     rec = {
         "workload": WORKLOADS[cfg] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
@@ -273,8 +279,10 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         "run_tiles": info["run_tiles"] if info["variant_name"] == "adaptive" else None,
         "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
         "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
-        "split_row_combine": bool(info["needs_fixup"]), "plan_ms": round(t_plan, 3),
+        "split_row_combine": bool(info["needs_fixup"]) and not info["hybrid"], "plan_ms": round(t_plan, 3),
         "ladder": info["ladder"] if info["variant_name"] == "prefree" else None,
+        "hybrid": bool(info["hybrid"]), "dense_rows": info["dense_rows"] if info["hybrid"] else None,
+        "x_halves": bool(info["x_halves"]) if info["hybrid"] else None,
         "steps": steps, "warmup": warmup,
         "launch": ("one captured HIP graph of the timed steps" if use_graph else "eager launches from Python")
                   + f"; eager warm-up step {warm_us:.1f} us",
@@ -288,7 +296,9 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
                      "launch_ms": round(ev_ms, 6), "algorithmic_bytes": bytes_eff,
                      "traffic_gbps": round(traffic / (ev_ms * 1e6), 1) if traffic else None,
                      "traffic_key": key,
-                     "note": ("step = tile kernel + split-row combine kernel; launch_ms covers both"
+                     "note": ("step = k_rows over the runs of short rows + k_dense over the dense rows' x windows "
+                              "+ k_dense_sum; launch_ms covers all three" if info["hybrid"] else
+                              "step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
     }
 
@@ -476,6 +486,10 @@ def main():
                     help="split-row FLAT: force the x-window tile schedule off (0) or on (1); -1 = the plan's choice")
     ap.add_argument("--chunk-nnz", type=int, default=-1,
                     help="FLAT 1024/2048: nnz per XCD chunk of tiles (0 = one chunk per XCD); -1 = the plan's choice")
+    ap.add_argument("--hybrid", type=int, default=-1, choices=[-1, 0, 1],
+                    help="plans with dense rows: 0 = split-row tiles instead of the hybrid path; -1 = the plan's choice")
+    ap.add_argument("--x-halves", type=int, default=-1, choices=[-1, 0, 1],
+                    help="hybrid plans: run tiles once per half of x (1) or once (0); -1 = the plan's choice")
     ap.add_argument("--ladder", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
                     help="PREFREE: the reference's reduction ladder 1..5 (0 = its active ladder, 3)")
     ap.add_argument("--seed", type=int, default=1)
@@ -554,7 +568,7 @@ def main():
                  f"{h['cfg']}: {h['values']}"),
         "config": {k: h[k] for k in ("workload", "cfg", "rows", "cols", "nnz", "seed", "variant", "tile", "tiles",
                                      "run_tiles", "row_aligned", "x_windows", "xcd_chunk_nnz", "split_row_combine",
-                                     "plan_ms")},
+                                     "hybrid", "dense_rows", "x_halves", "plan_ms")},
         "gbps_effective": h["gbps_effective"],
         "pct_peak_hbm": h["pct_peak_hbm"],
         "bytes_model": h["bytes_model"],

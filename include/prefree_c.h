@@ -98,6 +98,8 @@ typedef struct pf_plan_info {
                              with the default tile, columns given) for split-row FLAT matrices of that shape
                              (pf_plan_set_hybrid switches it) */
     long long dense_rows; /* hybrid plans: rows summed by x windows */
+    int x_halves;         /* hybrid plans: 1 = the runs' tiles are processed once per half of x, by XCDs 0-3 and
+                             4-7, so each XCD's random gathers fall in half of x (chosen when x is 4-24 MB) */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -155,6 +157,8 @@ int pf_plan_set_ladder(pf_plan *plan, int ladder);
 /* Plans that PF_AUTO made hybrid (pf_plan_info.hybrid): 0 = split-row FLAT tiles instead, 1 = back to
  * hybrid.  Both give y within rounding of each other (the dense rows' partial sums differ in order). */
 int pf_plan_set_hybrid(pf_plan *plan, int hybrid);
+/* Hybrid plans: 1 = run tiles per half of x (see pf_plan_info.x_halves), 0 = once each. */
+int pf_plan_set_x_halves(pf_plan *plan, int x_halves);
 /* FLAT 1024/2048: 1 (default) = the first call records each tile's first row and later calls read it;
  * 0 = every call searches row_ptr inside the tile kernel (no recorded map, tiles dealt to XCDs by
  * position).  Both give the same y.  The reference times its own row map as a separate pre-pass

@@ -85,6 +85,11 @@ typedef struct pfk_spmv_args {
     int *dense_seg;          /* [n_dense * (n_win + 1)] first nnz of each dense row in each window */
     void *dense_part;        /* [n_dense * n_win] window partial sums, PFK_SLOT_BYTES(dtype) each */
     size_t runs_bytes, run_map_bytes, dense_seg_bytes, dense_part_bytes;
+    int x_halves;            /* 1: each run tile is processed twice, by XCDs 0-3 for the columns in the first half
+                                of x and by XCDs 4-7 for the second, whose row sums go to half_part and are added
+                                to y in that order (each XCD's random gathers then fall in half of x) */
+    void *half_part;         /* [m] values of dtype */
+    size_t half_part_bytes;
 } pfk_spmv_args;
 
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */

@@ -61,7 +61,7 @@ class PlanInfo(ctypes.Structure):
                 ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
                 ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int), ("hybrid", ctypes.c_int),
-                ("dense_rows", ctypes.c_longlong)]
+                ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -100,7 +100,8 @@ class SpmvArgs(ctypes.Structure):
                 ("n_runs", ctypes.c_int), ("runs", ctypes.c_void_p), ("run_map", ctypes.c_void_p),
                 ("dense_seg", ctypes.c_void_p), ("dense_part", ctypes.c_void_p), ("runs_bytes", ctypes.c_size_t),
                 ("run_map_bytes", ctypes.c_size_t), ("dense_seg_bytes", ctypes.c_size_t),
-                ("dense_part_bytes", ctypes.c_size_t)]
+                ("dense_part_bytes", ctypes.c_size_t), ("x_halves", ctypes.c_int), ("half_part", ctypes.c_void_p),
+                ("half_part_bytes", ctypes.c_size_t)]
 
 
 _lib = None
@@ -139,6 +140,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_remember_rows, [_vp, _i])
         _sig(L.pf_plan_set_ladder, [_vp, _i])
         _sig(L.pf_plan_set_hybrid, [_vp, _i])
+        _sig(L.pf_plan_set_x_halves, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
@@ -304,6 +306,10 @@ class Plan:
     def set_hybrid(self, hybrid):
         """pf_plan_set_hybrid: switch a hybrid plan to split-row tiles (False) and back (True)."""
         _check(lib().pf_plan_set_hybrid(self._h, int(bool(hybrid))), "pf_plan_set_hybrid")
+
+    def set_x_halves(self, x_halves):
+        """pf_plan_set_x_halves: hybrid plans' run tiles once per half of x (True) or once (False)."""
+        _check(lib().pf_plan_set_x_halves(self._h, int(bool(x_halves))), "pf_plan_set_x_halves")
 
     def set_remember_rows(self, remember):
         """pf_plan_set_remember_rows: False = every call searches row_ptr (no recorded row map)."""

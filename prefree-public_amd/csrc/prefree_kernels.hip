@@ -105,6 +105,7 @@ struct Args {
     int *__restrict__ err;
     int *__restrict__ sched;      // split-row FLAT x-window schedule (see k_flat), or null
     long long sched_cap;          // tiles per XCD list
+    T *__restrict__ y2;           // x-halves runs: the second half's row sums (k_rows_halves_add adds them to y)
 };
 
 // Long-row threshold of ADAPTIVE for tile size K (keys per wave tile).  A
@@ -134,6 +135,20 @@ __device__ __forceinline__ long long xcd_tile(long long xch)
     const uint32_t c = (uint32_t)xch;
     const uint32_t r = q / c;
     return (long long)r * (kXcds * (long long)c) + (long long)(b % kXcds) * c + (q - r * c);
+}
+
+// x-halves tiling (row-aligned runs of hybrid plans): every tile is processed
+// twice, by a workgroup on XCDs 0-3 that gathers only the columns in the first
+// half of x and one on XCDs 4-7 for the second half, so each XCD's random x
+// gathers fall in half of x.  The tiles are chunked over the four XCDs of a
+// half as xcd_tile chunks them over eight.
+__device__ __forceinline__ long long xcd_tile_half(long long xch)
+{
+    const uint32_t b = blockIdx.x;
+    const uint32_t q = b / kXcds;
+    const uint32_t c = (uint32_t)xch;
+    const uint32_t r = q / c;
+    return (long long)r * ((kXcds / 2) * (long long)c) + (long long)((b % kXcds) & (kXcds / 2 - 1)) * c + (q - r * c);
 }
 
 // ---- 16-byte streaming loads through buffer resources ----------------------
@@ -1314,6 +1329,7 @@ struct RowsShape {
 // products of nnz [A, B), nov overflow nnz past kb + K, cnt row bounds staged.
 struct RowsDesc {
     int kb, B0, f0, nr, nov, A, B, cnt;
+    int clo, chi;  // x-halves: the columns this workgroup gathers, [clo, chi)
 };
 
 // The tile's loads after its col / val: the overflow col / val, the x gathers
@@ -1330,10 +1346,10 @@ struct RowsDesc {
 //     also covers some of them (the compiler cannot count loads a wave may
 //     skip).  C4: 310.5 instead of 320.4 us (fp64), 224.3 instead of 227.9
 //     (fp32); on C2 it costs 0.5-0.7 us in fp32 / fp16, hence the split.
-template <typename T, int K, bool EARLY_RP>
+template <typename T, int K, bool EARLY_RP, bool HALVES = false>
 __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, const int (&c)[RowsShape<T, K>::kVPT][4],
                                            T (&xv)[RowsShape<T, K>::kVPT][4], T &ov, T &xo,
-                                           int (&rr)[RowsShape<T, K>::kRpPer])
+                                           int (&rr)[RowsShape<T, K>::kRpPer], int &oc)
 {
     using S = RowsShape<T, K>;
     const int tid = threadIdx.x;
@@ -1351,7 +1367,7 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
     // read only by lanes below nov.
     constexpr bool kSkipOvf = S::kVPT == 1 && !EARLY_RP;
     const bool ovw = !kSkipOvf || wave * kWave < d.nov;  // wave-uniform
-    int oc;
+    oc = -1;
     if (ovw) {
         oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
         ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
@@ -1375,38 +1391,45 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int g = d.kb + tile_elem<T>(k, j);
-            const bool use = g >= d.A && g < d.B && g < d.B0;  // slots outside [A, B) are never read
+            const bool use = g >= d.A && g < d.B && g < d.B0 &&  // slots outside [A, B) are never read
+                             (!HALVES || (c[k][j] >= d.clo && c[k][j] < d.chi));
             xv[k][j] = buf_load(rx, use ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
         }
     }
-    if (ovw) xo = buf_load(rx, tid < d.nov ? (uint32_t)oc * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    if (ovw)
+        xo = buf_load(rx, tid < d.nov && (!HALVES || (oc >= d.clo && oc < d.chi)) ? (uint32_t)oc * (uint32_t)sizeof(T)
+                                                                                   : kOob, (T *)nullptr);
     if constexpr (!EARLY_RP) rp_loads();
 }
 
 // Products and row bounds of a row-aligned tile into LDS.
-template <typename T, int K>
-__device__ __forceinline__ void rows_stage(const RowsDesc &d, const T (&v)[RowsShape<T, K>::kVPT][4],
-                                           const T (&xv)[RowsShape<T, K>::kVPT][4], T ov, T xo,
+// x-halves: a column outside this workgroup's half gives the product 0 (not
+// v * 0, which is NaN for an infinite v); its half's workgroup forms it.
+template <typename T, int K, bool HALVES = false>
+__device__ __forceinline__ void rows_stage(const RowsDesc &d, const int (&c)[RowsShape<T, K>::kVPT][4],
+                                           const T (&v)[RowsShape<T, K>::kVPT][4],
+                                           const T (&xv)[RowsShape<T, K>::kVPT][4], int oc, T ov, T xo,
                                            const int (&rr)[RowsShape<T, K>::kRpPer], acc_t<T> *s_prod, int *s_rp)
 {
     using S = RowsShape<T, K>;
     using P = acc_t<T>;
     const int tid = threadIdx.x;
+    const auto mine = [&](int col) { return !HALVES || (col >= d.clo && col < d.chi); };
 #pragma unroll
     for (int k = 0; k < S::kVPT; ++k) {
         if constexpr (strided_layout<T>()) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                s_prod[tile_elem<T>(k, j)] = P(v[k][j]) * P(xv[k][j]);
+                s_prod[tile_elem<T>(k, j)] = mine(c[k][j]) ? P(v[k][j]) * P(xv[k][j]) : P(0);
         } else {
             P p[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                p[j] = P(v[k][j]) * P(xv[k][j]);
+                p[j] = mine(c[k][j]) ? P(v[k][j]) * P(xv[k][j]) : P(0);
             store4(s_prod + 4 * (tid + k * kBS), p);
         }
     }
-    if (tid < d.nov) s_prod[K + tid] = P(ov) * P(xo);
+    if (tid < d.nov) s_prod[K + tid] = mine(oc) ? P(ov) * P(xo) : P(0);
 #pragma unroll
     for (int q = 0; q < S::kRpPer; ++q)
         if (tid + q * kBS < d.cnt) s_rp[tid + q * kBS] = rr[q];
@@ -1565,7 +1588,7 @@ __device__ __forceinline__ int run_of_tile(const RunTable &rt, long long t, int 
     return (int)lo;
 }
 
-template <typename T, int K, int MODE, bool PRIO = false, bool RUNS = false>
+template <typename T, int K, int MODE, bool PRIO = false, bool RUNS = false, bool HALVES = false>
 __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, int *__restrict__ dbg,
                                               RunTable rt = RunTable{nullptr, 0})
 {
@@ -1589,7 +1612,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const long long t = xcd_tile(a.xch);
+    const long long t = HALVES ? xcd_tile_half(a.xch) : xcd_tile(a.xch);
     if (t >= a.ntiles)
         return;  // whole workgroup: padding of the XCD mapping
     const int m = a.m, nnz = a.nnz;
@@ -1669,7 +1692,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         }
         lds_sync();
         f = s_info[0]; rpf = s_info[1]; l = s_info[2]; rpl = s_info[3];
-        if (RUNS && MODE == kFlatSearch && map && tid == 0) {
+        if (RUNS && MODE == kFlatSearch && map && tid == 0 && (!HALVES || blockIdx.x % kXcds < kXcds / 2)) {
             int4 *mp = reinterpret_cast<int4 *>(map);
             mp[2 * t] = make_int4(f, rpf, l, rpl);
             mp[2 * t + 1] = make_int4(kb, B0, last ? 1 : 0, 0);
@@ -1696,13 +1719,16 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         return;
     }
 
-    const RowsDesc d{kb, B0, f0, nr, nov, A, B, min(nr + 1, S::kRpCap)};
+    const bool second = HALVES && blockIdx.x % kXcds >= kXcds / 2;  // the second half of x, rows into y2
+    const int hx = (a.n + 1) / 2;
+    const RowsDesc d{kb, B0, f0, nr, nov, A, B, min(nr + 1, S::kRpCap), second ? hx : 0, second ? a.n : hx};
     T xv[VPT][4], ov, xo;
-    int rr[S::kRpPer];
-    rows_loads<T, K, PRIO>(a, d, c, xv, ov, xo, rr);
+    int rr[S::kRpPer], oc;
+    rows_loads<T, K, PRIO, HALVES>(a, d, c, xv, ov, xo, rr, oc);
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
-    rows_stage<T, K>(d, v, xv, ov, xo, rr, s_prod, s_rp);
+    rows_stage<T, K, HALVES>(d, c, v, xv, oc, ov, xo, rr, s_prod, s_rp);
     lds_sync();
+    if (second) a.y = a.y2;
 
     // y stores: device scope (written through to memory) in general, C2:
     // 55.25 instead of 55.6 us (fp64), 36.0 instead of 36.5 (fp32), 31.9
@@ -1871,6 +1897,14 @@ __global__ __launch_bounds__(kBS) void k_dense_sorted(const int *__restrict__ co
     }
     if (__ballot(bad != 0) && (threadIdx.x & (kWave - 1)) == 0)
         atomicAdd(counters + 1, 1);
+}
+
+// x-halves runs: y = (first half's row sum) + (second half's), in that order.
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_rows_halves_add(T *__restrict__ y, const T *__restrict__ y2, int m)
+{
+    for (long long r = (long long)blockIdx.x * kBS + threadIdx.x; r < m; r += (long long)gridDim.x * kBS)
+        y[r] = T(acc_t<T>(y[r]) + acc_t<T>(y2[r]));
 }
 
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
@@ -2701,9 +2735,10 @@ inline unsigned grid_for(long long work, long long per_block, long long cap)
 // nnz, or one chunk of ceil(ntiles / 8) tiles per XCD when chunk_nnz is 0.
 // The rounds are balanced: every XCD gets the same number of chunks, of
 // ceil(g / rounds) tiles, so the last round does not fall on a few XCDs.
-void chunk_shape(long long ntiles, long long tile_nnz, long long chunk_nnz, long long &xch, long long &g8)
+void chunk_shape(long long ntiles, long long tile_nnz, long long chunk_nnz, long long &xch, long long &g8,
+                 int nx = kXcds)
 {
-    const long long g = (ntiles + kXcds - 1) / kXcds;
+    const long long g = (ntiles + nx - 1) / nx;
     long long target = chunk_nnz > 0 ? chunk_nnz / tile_nnz : g;
     if (target < 1) target = 1;
     const long long rounds = (g + target - 1) / target;
@@ -2735,6 +2770,7 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.err = a->err_flag;
     r.sched = a->sched;
     r.sched_cap = a->sched_cap;
+    r.y2 = static_cast<T *>(a->half_part);
     return r;
 }
 
@@ -2975,13 +3011,18 @@ template <typename T, int K>
 int launch_hybrid(const pfk_spmv_args *a, void *stream)
 {
     Args<T> r = make_args<T>(a);
-    if (r.ntiles > 0) chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8);
+    const bool halves = a->x_halves && a->half_part;
+    if (r.ntiles > 0) chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8, halves ? kXcds / 2 : kXcds);
     const RunTable rt{a->runs, a->n_runs};
     const bool memo = a->map_ready && a->run_map && a->dense_seg;
     const bool prio = (long long)a->nnz < 4LL * a->m;
     const dim3 rgrid((unsigned)(r.g8 * kXcds));
     if (a->ntiles == 0)  // every row is dense
         ;
+    else if (halves && memo)
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+    else if (halves)
+        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
     else if (memo && prio)
         hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
     else if (memo)
@@ -2989,6 +3030,11 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     else
         hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
     if (a->ntiles > 0) PFK_LAUNCHED("k_rows (runs)");
+    if (a->ntiles > 0 && halves) {
+        hipLaunchKernelGGL((k_rows_halves_add<T>), dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream), r.y, r.y2,
+                           a->m);
+        PFK_LAUNCHED("k_rows_halves_add");
+    }
     const int ngroups = (a->n_dense + PFK_DENSE_GROUP - 1) / PFK_DENSE_GROUP;
     const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, a->dense_seg, a->dense_part};
     const unsigned dgrid = (unsigned)(kXcds * ((a->n_win + kXcds - 1) / kXcds) * ngroups);
@@ -3050,7 +3096,9 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
     if (!room(a->runs, a->runs_bytes, 5LL * (a->n_runs + 1) * 4, "run table") ||
         !room(a->dense_part, a->dense_part_bytes, nd * nw * PFK_SLOT_BYTES(dtype), "dense partial sums") ||
         (a->run_map && !room(a->run_map, a->run_map_bytes, a->ntiles * 32, "run tile map")) ||
-        (a->dense_seg && !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")))
+        (a->dense_seg && !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")) ||
+        (a->x_halves && !room(a->half_part, a->half_part_bytes, (long long)a->m * (dtype == PF_F64 ? 8 : 4),
+                              "x-halves row sums")))
         return PF_ERR_INVALID;
     if (dtype == PF_F64) return a->tile == 1024 ? launch_hybrid<double, 1024>(a, stream) : launch_hybrid<double, 2048>(a, stream);
     return a->tile == 1024 ? launch_hybrid<float, 1024>(a, stream) : launch_hybrid<float, 2048>(a, stream);

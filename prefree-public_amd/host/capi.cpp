@@ -361,6 +361,9 @@ struct pf_plan {
     void *dense_part = nullptr;
     size_t runs_bytes = 0, run_map_bytes = 0, dense_seg_bytes = 0, dense_part_bytes = 0;
     bool hyb_map_ready = false;
+    bool x_halves = false;       // run tiles processed per half of x (see pfk_spmv_args.x_halves)
+    void *half_part = nullptr;   // [m] second-half row sums
+    size_t half_part_bytes = 0;
 };
 
 namespace {
@@ -543,9 +546,10 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     const int nwin = (int)((p->n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const size_t b_rows = up((size_t)nd * 4), b_runs = up((size_t)5 * R * 4), b_map = up((size_t)tiles * 32),
-                 b_seg = up((size_t)nd * (nwin + 1) * 4), b_part = up((size_t)nd * nwin * slot_bytes(dtype));
+                 b_seg = up((size_t)nd * (nwin + 1) * 4), b_part = up((size_t)nd * nwin * slot_bytes(dtype)),
+                 b_half = up((size_t)p->m * value_bytes(dtype));
     void *w = nullptr;
-    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part), "hybrid tables");
+    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_half), "hybrid tables");
     char *c = static_cast<char *>(w);
     p->ws_hyb = w;
     p->dense_rows = reinterpret_cast<int *>(c);
@@ -553,6 +557,8 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     p->run_map = reinterpret_cast<int *>(c + b_rows + b_runs);
     p->dense_seg = reinterpret_cast<int *>(c + b_rows + b_runs + b_map);
     p->dense_part = c + b_rows + b_runs + b_map + b_seg;
+    p->half_part = c + b_rows + b_runs + b_map + b_seg + b_part;
+    p->half_part_bytes = b_half;
     p->runs_bytes = b_runs;
     p->run_map_bytes = b_map;
     p->dense_seg_bytes = b_seg;
@@ -563,7 +569,14 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     p->run_tile = K;
     p->run_tiles = tiles;
     p->run_chunk = short_nnz < 4 * short_rows ? 0 : kChunkNnz;
+    // The runs' random x gathers fall in half of x per XCD when x exceeds one
+    // XCD's 4 MB L2 but a half of it nearly fits (x up to 24 MB).
+    const long long xb = (long long)p->n * value_bytes(dtype);
+    p->x_halves = xb > kXcdL2Bytes && xb <= 6 * kXcdL2Bytes;
+    p->info.x_halves = p->x_halves ? 1 : 0;
     st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
+    // rows the runs never write (the dense rows) keep a zero second-half sum
+    if (st == PF_OK) st = pfk_fill_zero(p->half_part, b_half, stream);
     if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
     if (st == PF_OK) st = pfk_stream_sync(stream);
     if (st != PF_OK) return from_kernel_layer(st, "hybrid tables");
@@ -814,6 +827,16 @@ int pf_plan_set_hybrid(pf_plan *plan, int hybrid)
         return fail(PF_ERR_UNSUPPORTED, "this plan has no hybrid tables (no dense rows with sorted columns)");
     plan->hybrid = hybrid != 0;
     plan->info.hybrid = hybrid;
+    plan->info.x_halves = hybrid ? (plan->x_halves ? 1 : 0) : plan->info.x_halves;
+    return PF_OK;
+}
+
+int pf_plan_set_x_halves(pf_plan *plan, int x_halves)
+{
+    if (!plan || (x_halves != 0 && x_halves != 1)) return fail(PF_ERR_INVALID, "x_halves must be 0 or 1");
+    if (!plan->ws_hyb) return fail(PF_ERR_UNSUPPORTED, "x halves are for the runs of hybrid plans");
+    plan->x_halves = x_halves != 0;
+    plan->info.x_halves = x_halves;
     return PF_OK;
 }
 
@@ -901,6 +924,9 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         a.dense_seg_bytes = plan->dense_seg_bytes;
         a.dense_part = plan->dense_part;
         a.dense_part_bytes = plan->dense_part_bytes;
+        a.x_halves = plan->x_halves ? 1 : 0;
+        a.half_part = plan->half_part;
+        a.half_part_bytes = plan->half_part_bytes;
         a.map_ready = (plan->remember_rows && plan->hyb_map_ready) ? 1 : 0;
         PF_TRY(pfk_spmv_hybrid(dt, &a, stream), "hybrid kernels");
         if (plan->remember_rows) plan->hyb_map_ready = true;  // later calls read what this one recorded

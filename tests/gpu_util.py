@@ -25,7 +25,7 @@ def dev(a, min_len=4):
 
 
 def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("nan"), repeat=2, row_aligned=None,
-             x_windows=None, chunk_nnz=None, ladder=None):
+             x_windows=None, chunk_nnz=None, ladder=None, x_halves=None):
     """y = A·x on the GPU through pf_plan_create / pf_plan_execute; returns (y, plan info).
 
     The plan executes `repeat` times, y refilled with `fill` before each call,
@@ -35,7 +35,7 @@ def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("n
     (up to atomic ordering for the reference's PREFREE algorithm).
     row_aligned (FLAT 1024/2048): force row-aligned (1) or split-row (0) tiles; x_windows (split-row
     FLAT): force the x-window schedule on (1) or off (0); chunk_nnz (FLAT 1024/2048): the XCD chunk;
-    ladder (PREFREE): the reduction ladder 1..5."""
+    ladder (PREFREE): the reduction ladder 1..5; x_halves (hybrid plans): run tiles per half of x."""
     m, n, nnz = len(rp) - 1, len(x), len(col)
     d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
     y = torch.full((max(m, 1),), fill, dtype=TORCH[dtype], device=DEV)
@@ -50,6 +50,8 @@ def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("n
             p.set_chunk_nnz(chunk_nnz)
         if ladder is not None:
             p.set_ladder(ladder)
+        if x_halves is not None:
+            p.set_x_halves(x_halves)
         for k in range(repeat):
             y.fill_(fill)
             p.execute(d_rp, d_col, d_val, d_x, y, stream=stream)

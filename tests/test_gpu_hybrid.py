@@ -151,3 +151,45 @@ def test_hybrid_special_values():
     assert np.array_equal(np.isnan(y), np.isnan(ref))
     ok = ~np.isnan(ref)
     assert np.array_equal(y[ok], ref[ok])
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_hybrid_x_halves(name, dtype):
+    # Run tiles processed once per half of x (XCDs 0-3 and 4-7), the halves' row sums added in order.
+    rp, col, n = _case(name, seed=21)
+    rng = np.random.default_rng(22)
+    kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
+    y, info = gpu_spmv(rp, col, kv, kx, "flat", dtype=dtype, x_halves=True)
+    assert info["hybrid"] == 1 and info["x_halves"] == 1
+    assert_parity(rp, col, kv, kx, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"{name}/halves/kat")
+    val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+    x = rng.uniform(-1, 1, n).astype(NP[dtype])
+    y, _ = gpu_spmv(rp, col, val, x, "flat", dtype=dtype, x_halves=True)
+    assert_parity(rp, col, val, x, y, dtype, what=f"{name}/halves/random")
+
+
+def test_hybrid_x_halves_special_values():
+    # A column outside a workgroup's half must not multiply its value (inf * 0 would be NaN).
+    rp, col, n = _case("many_short_runs", seed=23)
+    rng = np.random.default_rng(24)
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    for arr in (val, x):
+        idx = rng.choice(len(arr), size=max(1, len(arr) // 500), replace=False)
+        arr[idx] = rng.choice([np.nan, np.inf, -np.inf], size=len(idx))
+    y, info = gpu_spmv(rp, col, val, x, "flat", x_halves=True)
+    assert info["x_halves"] == 1
+    ref = oracle.spmv_serial(rp, col, val, x)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(y[ok], ref[ok])
+
+
+def test_full_c5_plan_choice():
+    # C5 as bench.py measures it: hybrid with x halves (x = 8 MB), and the same y as the split-row plan
+    # within rounding.
+    rp, col, v = pf.synth_csr(5, seed=1, dtypes=("f64",))
+    x = pf.synth_x(5, len(rp) - 1, seed=1)["f64"]
+    y, info = gpu_spmv(rp, col, v["f64"], x, "auto")
+    assert info["hybrid"] == 1 and info["x_halves"] == 1 and info["dense_rows"] == 1000
+    assert_parity(rp, col, v["f64"], x, y, "f64", what="C5 hybrid")
