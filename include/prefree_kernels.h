@@ -95,9 +95,8 @@ typedef struct pfk_spmv_args {
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
 #define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
 
-/* Columns per x window of a hybrid plan's dense-row kernel (64 KB of LDS), and dense rows per workgroup. */
+/* Columns per x window of a hybrid plan's dense-row kernel (64 KB of LDS). */
 #define PFK_DENSE_WINDOW(dtype) ((dtype) == 0 ? 8192 : 16384)
-#define PFK_DENSE_GROUP 128
 
 /* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums and
  * their combine, three launches.  map_ready 0: the call searches rows and segment bounds (and records them

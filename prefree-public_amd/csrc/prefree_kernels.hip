@@ -1747,16 +1747,25 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
 // G rows instead of once per row.  Workgroup (window w, group g) is dealt so
 // that an XCD takes a contiguous eighth of the windows (its x entries stay in
 // its L2).  Each (row, window) partial sum goes to part[row][w]; k_dense_sum
-// adds them in window order.  Segment bounds: MODE kFlatSearch finds them by
+// adds them up.  Segment bounds: MODE kFlatSearch finds them by
 // a wave search of the row's columns and records them in seg; kFlatMemo reads
-// them.  C5 (1000 rows of 50k-500k nnz, 280M nnz): 584 us against 742 us for
-// the same rows in split-row tiles with the x-window schedule.
+// them.  C5 (1000 rows of 50k-500k nnz, 280M nnz): 558 us against 742 us for
+// the same rows in split-row tiles with the x-window schedule.  16 loads in
+// flight per lane and 128 rows per workgroup were the best of U = 4-16 and
+// G = 64-256 (C5 fp64 whole step 896-1015 us, fp32 598-942).
 
+#ifndef PF_DENSE_G
+#define PF_DENSE_G 128
+#endif
+#ifndef PF_DENSE_U
+#define PF_DENSE_U 16
+#endif
 template <typename T>
 struct DenseShape {
     static constexpr int kW = sizeof(T) == 8 ? 8192 : 16384;  // x window: 64 KB of LDS
-    static constexpr int kG = 128;                            // dense rows per workgroup
-    static constexpr int kU = 8;                              // loads in flight per lane
+    static constexpr int kG = PF_DENSE_G;                     // dense rows per workgroup
+    static constexpr int kU = PF_DENSE_U;                     // loads in flight per lane
+    static_assert(kW == PFK_DENSE_WINDOW(sizeof(T) == 8 ? PF_F64 : PF_F32), "window of the C ABI");
 };
 
 struct DenseArgs {
@@ -1847,22 +1856,27 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
     }
 }
 
-// y of each dense row: its window partial sums in window order.
+// y of each dense row from its window partial sums: one wave per row, lane j
+// adding windows j, j + 64, ... in order, then the wave's DPP tree (a fixed
+// order: deterministic).  One thread per row walking 123 windows took 34 us
+// on C5; a wave per row takes a few.
 template <typename T>
 __global__ __launch_bounds__(kBS) void k_dense_sum(Args<T> a, DenseArgs d)
 {
     using P = acc_t<T>;
-    const int i = blockIdx.x * kBS + threadIdx.x;
+    const int i = blockIdx.x * kWaves + (int)threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
     if (i >= d.nd)
-        return;
+        return;  // whole wave
     const int r = d.rows[i];
     if (r < 0 || r >= a.m)
-        return;
+        return;  // whole wave
     const P *pp = static_cast<const P *>(d.part) + (long long)i * d.nwin;
     P sum = P(0);
-    for (int w = 0; w < d.nwin; ++w)
+    for (int w = lane; w < d.nwin; w += kWave)
         sum += pp[w];
-    a.y[r] = T(sum);
+    sum = wave_sum(sum);
+    if (lane == 0) a.y[r] = T(sum);
 }
 
 // Planning scan of a hybrid plan: every row of at least `dmin` nnz goes to the
@@ -3035,7 +3049,7 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
                            a->m);
         PFK_LAUNCHED("k_rows_halves_add");
     }
-    const int ngroups = (a->n_dense + PFK_DENSE_GROUP - 1) / PFK_DENSE_GROUP;
+    const int ngroups = (a->n_dense + DenseShape<T>::kG - 1) / DenseShape<T>::kG;
     const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, a->dense_seg, a->dense_part};
     const unsigned dgrid = (unsigned)(kXcds * ((a->n_win + kXcds - 1) / kXcds) * ngroups);
     if (memo)
@@ -3043,7 +3057,7 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     else
         hipLaunchKernelGGL((k_dense<T, kFlatSearch>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense");
-    hipLaunchKernelGGL((k_dense_sum<T>), dim3((unsigned)((a->n_dense + kBS - 1) / kBS)), dim3(kBS), 0, S(stream), r, d);
+    hipLaunchKernelGGL((k_dense_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense_sum");
     return PF_OK;
 }
