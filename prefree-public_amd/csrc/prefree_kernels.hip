@@ -1791,6 +1791,84 @@ __device__ __forceinline__ int wave_lower_bound(const int *__restrict__ col, int
     return hi;
 }
 
+// The recorded-bounds call (kFlatMemo): each wave reads the window bounds of
+// all its rows (one load per lane) before the window is staged, and streams
+// its rows' segments as one sequence of batches of U loads per lane, double
+// buffered: the next batch (of the same row or the next one) is in flight
+// while the current one is summed, so neither a row change nor a row's last
+// partial batch leaves the wave without loads in flight.
+template <typename T>
+__device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const DenseArgs &d, const T *sx, int w,
+                                                    int c0, int i0, int nk)
+{
+    using P = acc_t<T>;
+    constexpr int W = DenseShape<T>::kW, U = DenseShape<T>::kU;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nnz = a.nnz;
+    // lane k: the segment [ms, me) of row i0 + kWaves k in window w
+    int ms = 0, me = 0;
+    if (lane < nk) {
+        const int *sg = d.seg + (long long)(i0 + kWaves * lane) * (d.nwin + 1) + w;
+        ms = min(max(sg[0], 0), nnz);
+        me = min(max(sg[1], ms), nnz);
+        if (me == ms) static_cast<P *>(d.part)[(long long)(i0 + kWaves * lane) * d.nwin + w] = P(0);
+    }
+    const uint64_t todo = __ballot(lane < nk && me > ms);
+    int cA[U], cB[U];
+    T vA[U], vB[U];
+    P acc = P(0);
+    const auto issue = [&](int k, int j, int (&c)[U], T (&v)[U]) {
+        const int s = __builtin_amdgcn_readlane(ms, k), e = __builtin_amdgcn_readlane(me, k);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            load1(rc, rv, j + u * kWave + lane, c[u], v[u]);
+    };
+    const auto consume = [&](int k, int j, const int (&c)[U], const T (&v)[U]) {
+        const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ms, k);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {  // no product for slots past the segment (x may hold inf or NaN)
+            const T xv = sx[(c[u] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
+            if (j + u * kWave + lane < len)
+                acc += P(v[u]) * P(xv);
+        }
+        if (j + kWave * U >= len) {  // the row's last batch
+            acc = wave_sum(acc);
+            if (lane == 0) static_cast<P *>(d.part)[(long long)(i0 + kWaves * k) * d.nwin + w] = acc;
+            acc = P(0);
+        }
+    };
+    const auto advance = [&](int &k, int &j) {  // the batch after (k, j); false at the end
+        const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ms, k);
+        j += kWave * U;
+        if (j < len) return true;
+        const uint64_t rest = todo & ~((2ull << k) - 1ull);
+        if (!rest) return false;
+        k = __ffsll((long long)rest) - 1;
+        j = 0;
+        return true;
+    };
+    if (!todo) return;
+    int k = __ffsll((long long)todo) - 1, j = 0;
+    issue(k, j, cA, vA);
+    for (;;) {
+        int k2 = k, j2 = j;
+        bool more = advance(k2, j2);
+        if (more) issue(k2, j2, cB, vB);
+        consume(k, j, cA, vA);
+        if (!more) break;
+        k = k2;
+        j = j2;
+        more = advance(k2, j2);
+        if (more) issue(k2, j2, cA, vA);
+        consume(k, j, cB, vB);
+        if (!more) break;
+        k = k2;
+        j = j2;
+    }
+}
+
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
 {
@@ -1805,6 +1883,7 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
         return;
     const int m = a.m, nnz = a.nnz;
     const int c0 = w * W;
+    const int i_end = min(d.nd, (g + 1) * G);
     {  // the window x[c0, c0 + W) into LDS, 16 bytes per lane and load; zeros past n
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + c0, (long long)min(W, a.n - c0) * (long long)sizeof(T));
         constexpr int kPer = 16 / (int)sizeof(T);
@@ -1813,7 +1892,12 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
             *reinterpret_cast<u32x4 *>(sx + i * kPer) = __builtin_amdgcn_raw_buffer_load_b128(rx, i * 16, 0, 0);
     }
     lds_sync();
-    const int i_end = min(d.nd, (g + 1) * G);
+    if constexpr (MODE == kFlatMemo) {
+        static_assert(G / kWaves <= kWave, "one lane per row of a wave");
+        const int i0 = g * G + wave;
+        dense_rows_recorded<T>(a, d, sx, w, c0, i0, i0 < i_end ? (i_end - i0 + kWaves - 1) / kWaves : 0);
+        return;
+    }
     for (int i = g * G + wave; i < i_end; i += kWaves) {
         const int r = d.rows[i];
         if (r < 0 || r >= m) {  // a table entry that is not a row: skip it, report it
@@ -1822,18 +1906,12 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
         }
         const int a0 = min(max(a.rp[r], 0), nnz);
         const int a1 = min(max(a.rp[r + 1], a0), nnz);
-        int s, e;
         int *sg = d.seg + (long long)i * (d.nwin + 1);
-        if (MODE == kFlatMemo) {
-            s = min(max(sg[w], a0), a1);
-            e = min(max(sg[w + 1], s), a1);
-        } else {
-            s = wave_lower_bound(a.col, a0, a1, c0, lane);
-            e = w == d.nwin - 1 ? a1 : wave_lower_bound(a.col, s, a1, c0 + W, lane);
-            if (MODE == kFlatSearch && d.seg && lane == 0) {
-                sg[w] = s;
-                if (w == d.nwin - 1) sg[d.nwin] = e;
-            }
+        const int s = wave_lower_bound(a.col, a0, a1, c0, lane);
+        const int e = w == d.nwin - 1 ? a1 : wave_lower_bound(a.col, s, a1, c0 + W, lane);
+        if (MODE == kFlatSearch && d.seg && lane == 0) {
+            sg[w] = s;
+            if (w == d.nwin - 1) sg[d.nwin] = e;
         }
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
