@@ -283,6 +283,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         "ladder": info["ladder"] if info["variant_name"] == "prefree" else None,
         "hybrid": bool(info["hybrid"]), "dense_rows": info["dense_rows"] if info["hybrid"] else None,
         "x_halves": bool(info["x_halves"]) if info["hybrid"] else None,
+        "tuning_table": os.path.relpath(os.path.realpath(pf.tuning_table()), REPO) if pf.tuning_table() else None,
         "steps": steps, "warmup": warmup,
         "launch": ("one captured HIP graph of the timed steps" if use_graph else "eager launches from Python")
                   + f"; eager warm-up step {warm_us:.1f} us",
@@ -568,7 +569,7 @@ def main():
                  f"{h['cfg']}: {h['values']}"),
         "config": {k: h[k] for k in ("workload", "cfg", "rows", "cols", "nnz", "seed", "variant", "tile", "tiles",
                                      "run_tiles", "row_aligned", "x_windows", "xcd_chunk_nnz", "split_row_combine",
-                                     "hybrid", "dense_rows", "x_halves", "plan_ms")},
+                                     "hybrid", "dense_rows", "x_halves", "plan_ms", "tuning_table")},
         "gbps_effective": h["gbps_effective"],
         "pct_peak_hbm": h["pct_peak_hbm"],
         "bytes_model": h["bytes_model"],

@@ -180,10 +180,12 @@ int pf_plan_destroy(pf_plan *plan);
 /* ---- tuning ------------------------------------------------------------------
  * pf_plan_autotune times every compiled configuration for the plan's dtype on
  * the caller's matrix and vectors (ADAPTIVE tiles x run lengths 1..16, FLAT
- * tiles; PREFREE and the ordinary-load cache policy when asked by `flags`), each
- * as the best of two batches of `reps` back-to-back SpMVs, and switches the plan
- * to the fastest.  d_y holds A·x on return.  Synchronises `stream`; allocates
- * temporary plans.  The online counterpart of the reference tuner
+ * tiles and XCD chunks; PREFREE tiles x its five reduction ladders and the
+ * ordinary-load cache policy when asked by `flags`), each as the best of two
+ * batches of `reps` back-to-back SpMVs, and switches the plan to the fastest.
+ * The plan's own configuration (a hybrid plan included) is the first candidate.
+ * d_y holds A·x on return.  Synchronises `stream`; allocates temporary plans.
+ * The online counterpart of the reference tuner
  * (scripts/profile_and_generate.py:319-418), which compiled and timed each
  * candidate as a separate program. */
 enum { PF_TUNE_PREFREE = 1, PF_TUNE_KEEP_CACHED = 2 };
@@ -193,18 +195,30 @@ typedef struct pf_tune_result {
     double us;          /* microseconds per SpMV of the chosen configuration */
     double default_us;  /* of the configuration the plan had before tuning */
     long long chunk_nnz; /* FLAT 1024/2048: XCD chunk of the chosen configuration (see pf_plan_info) */
+    int ladder;         /* PREFREE: the chosen reduction ladder 1..5; 0 otherwise */
+    int hybrid;         /* 1 if the chosen configuration is the plan's own hybrid one */
 } pf_tune_result;
 int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x,
                      void *d_y, int reps, int flags, void *stream, pf_tune_result *result);
 
-/* Size-class table for PF_AUTO, as written by the offline tuner
- * (prefree-public_amd/tune/autotune.py).  Text, one row per line:
- *   <class> <nnz_upper | -1> <f64|f32|f16> <adaptive|flat|prefree> <tile> <run_tiles | 0> <keep_cached>
- * The first row whose dtype matches and whose bound exceeds the matrix's nnz
- * decides (run 0: the built-in run rule).  NULL clears the table.  Without a
- * call, $PREFREE_TUNING_TABLE is read once if set.  Plans made before the call
- * are unaffected. */
+/* Table for PF_AUTO, as written by the offline tuner (prefree-public_amd/tune/autotune.py).
+ * Text, one row per line ('#' starts a comment):
+ *   <class> <nnz_upper | -1> <rows> <f64|f32|f16> <adaptive|flat|prefree|auto> <tile> <run_tiles | 0>
+ *   <keep_cached> <ladder | 0> <hybrid 0|1>
+ * (variant auto, tile 0: the matrices of that row keep PF_AUTO's built-in rules)
+ * rows: the matrix's row-length class from its statistics — short (no row over 256 nnz, under 4 nnz
+ * per row on average), regular (no row over 256 nnz), skewed (longer rows, under 16 nnz per row on
+ * average), dense (longer rows, 16 or more on average) — or any.  The first row whose dtype and row
+ * class match and whose bound exceeds the matrix's nnz decides (run 0: the built-in run rule; ladder
+ * 0: the default ladder; hybrid 0: a FLAT plan stays split-row even with dense rows).  Rows of the
+ * older form <class> <nnz_upper> <dtype> <variant> <tile> <run> <keep> match any row class.
+ * NULL clears the table.  Without a call, the table named by $PREFREE_TUNING_TABLE is read once (an
+ * empty value: none) or, when that is unset, tune/mi355x_tuning_table.txt beside the lib/ directory
+ * of this library (the table measured on MI355X that ships with it).  Plans made before the call are
+ * unaffected. */
 int pf_set_tuning_table(const char *path);
+/* Path of the table PF_AUTO consults ("" when none). */
+const char *pf_tuning_table(void);
 
 /* One-shot y = A·x: plan, execute, synchronise, destroy. */
 int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,

@@ -73,7 +73,8 @@ class TuneResult(ctypes.Structure):
     """pf_tune_result, include/prefree_c.h."""
     _fields_ = [("variant", ctypes.c_int), ("tile", ctypes.c_int), ("run_tiles", ctypes.c_int),
                 ("keep_cached", ctypes.c_int), ("candidates", ctypes.c_int), ("us", ctypes.c_double),
-                ("default_us", ctypes.c_double), ("chunk_nnz", ctypes.c_longlong)]
+                ("default_us", ctypes.c_double), ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int),
+                ("hybrid", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -143,6 +144,7 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_set_x_halves, [_vp, _i])
         _sig(L.pf_plan_autotune, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, ctypes.POINTER(TuneResult)])
         _sig(L.pf_set_tuning_table, [ctypes.c_char_p])
+        _sig(L.pf_tuning_table, [], ctypes.c_char_p)
         _sig(L.pf_plan_get_stats, [_vp, ctypes.POINTER(RowStats)])
         _sig(L.pf_plan_execute, [_vp, _vp, _vp, _vp, _vp, _vp, _vp])
         _sig(L.pf_plan_check, [_vp, _vp])
@@ -413,8 +415,13 @@ def synth_dims(cfg, seed=1, scale_n=0):
 
 
 def set_tuning_table(path):
-    """pf_set_tuning_table: size-class table for PF_AUTO (None clears it)."""
+    """pf_set_tuning_table: the table PF_AUTO consults (None clears it)."""
     _check(lib().pf_set_tuning_table(None if path is None else os.fsencode(path)), "pf_set_tuning_table")
+
+
+def tuning_table():
+    """pf_tuning_table: path of the table PF_AUTO consults ('' when none)."""
+    return os.fsdecode(lib().pf_tuning_table() or b"")
 
 
 def mtx_read(path):

@@ -8,9 +8,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <dlfcn.h>
 #include <fstream>
 #include <mutex>
 #include <sstream>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -111,19 +113,42 @@ int choose_run(int tile, long long ntiles, long long resident)
 
 // ---- tuning table (written by the offline tuner, prefree-public_amd/tune) ----
 //
-// One row per (size class, value type): nnz below `nnz_upper` (-1: no bound)
-// selects (variant, tile, run_tiles, keep_cached).  Loaded by
-// pf_set_tuning_table or, once, from $PREFREE_TUNING_TABLE; consulted by
-// PF_AUTO before the built-in rules.  This replaces the reference tuner's
-// generated size-class dispatch (templates/preFreeSpMV_template.cu.j2:845-1003).
+// One row per (size class, row-length class, value type): nnz below
+// `nnz_upper` (-1: no bound) and the matrix's row-length class select
+// (variant, tile, run_tiles, keep_cached, ladder, hybrid), or variant "auto"
+// (tile 0): the built-in rules.  The row-length
+// classes are the cuts of the built-in rules below: "short" (every row <= 256
+// nnz, under 4 nnz per row on average), "regular" (every row <= 256 nnz),
+// "skewed" (longer rows, under 16 nnz per row on average), "dense" (longer
+// rows, 16 or more on average); "any" matches every matrix.  Loaded by
+// pf_set_tuning_table, else from $PREFREE_TUNING_TABLE (an empty value: no
+// table), else from tune/mi355x_tuning_table.txt beside this library's lib/
+// directory; consulted by PF_AUTO before the built-in rules.  This replaces
+// the reference tuner's generated size-class dispatch
+// (templates/preFreeSpMV_template.cu.j2:845-1003).
+enum RowClass { kRowsAny = -1, kRowsShort = 0, kRowsRegular, kRowsSkewed, kRowsDense };
+
+int row_class(const pf_row_stats &s)
+{
+    if (s.max_row_len <= PFK_ALIGN_ROW_MAX) return s.nnz < 4LL * s.m ? kRowsShort : kRowsRegular;
+    return s.nnz < 16LL * s.m ? kRowsSkewed : kRowsDense;
+}
+
+int parse_rows(const std::string &v)
+{
+    return v == "any" ? kRowsAny : v == "short" ? kRowsShort : v == "regular" ? kRowsRegular
+         : v == "skewed" ? kRowsSkewed : v == "dense" ? kRowsDense : -2;
+}
+
 struct TableRow {
     std::string name;
     long long nnz_upper;
-    int dtype, variant, tile, run, keep;
+    int rows, dtype, variant, tile, run, keep, ladder, hybrid;
 };
 
 std::mutex g_table_mu;
 std::vector<TableRow> g_table;
+std::string g_table_path;
 bool g_table_env_done = false;
 
 int parse_dtype(const std::string &s)
@@ -132,9 +157,13 @@ int parse_dtype(const std::string &s)
 }
 int parse_variant(const std::string &s)
 {
-    return s == "adaptive" ? PF_ADAPTIVE : s == "flat" ? PF_FLAT : s == "prefree" ? PF_PREFREE : -1;
+    return s == "adaptive" ? PF_ADAPTIVE : s == "flat" ? PF_FLAT : s == "prefree" ? PF_PREFREE
+         : s == "auto" ? PF_AUTO : -1;
 }
 
+// Rows: `class nnz_upper rows dtype variant tile run keep ladder hybrid`, or
+// the older `class nnz_upper dtype variant tile run keep` (rows "any", the
+// default ladder, hybrid allowed).
 int load_table(const char *path, std::vector<TableRow> &out, std::string &why)
 {
     std::ifstream f(path);
@@ -150,48 +179,102 @@ int load_table(const char *path, std::vector<TableRow> &out, std::string &why)
         const size_t hash = line.find('#');
         if (hash != std::string::npos) line.resize(hash);
         std::istringstream in(line);
+        std::vector<std::string> w;
+        for (std::string t; in >> t;) w.push_back(t);
+        if (w.empty()) continue;  // blank or comment
+        const auto bad = [&](const char *what) {
+            why = std::string(path) + ":" + std::to_string(lineno) + ": " + what;
+            return PF_ERR_IO;
+        };
+        if (w.size() != 7 && w.size() != 10)
+            return bad("expected 'class nnz_upper rows dtype variant tile run keep ladder hybrid'");
+        const bool v2 = w.size() == 10;
+        const size_t o = v2 ? 1 : 0;
         TableRow r;
-        std::string dt, var;
-        if (!(in >> r.name)) continue;  // blank or comment
-        if (!(in >> r.nnz_upper >> dt >> var >> r.tile >> r.run >> r.keep)) {
-            why = std::string(path) + ":" + std::to_string(lineno) + ": expected 'class nnz_upper dtype variant tile run keep'";
-            return PF_ERR_IO;
+        r.name = w[0];
+        r.rows = v2 ? parse_rows(w[2]) : kRowsAny;
+        r.dtype = parse_dtype(w[2 + o]);
+        r.variant = parse_variant(w[3 + o]);
+        try {
+            size_t used = 0;
+            const auto num = [&](const std::string &t) {
+                const long long v = std::stoll(t, &used);
+                if (used != t.size()) throw std::invalid_argument(t);
+                return v;
+            };
+            r.nnz_upper = num(w[1]);
+            r.tile = (int)num(w[4 + o]);
+            r.run = (int)num(w[5 + o]);
+            r.keep = (int)num(w[6 + o]);
+            r.ladder = v2 ? (int)num(w[8]) : 0;
+            r.hybrid = v2 ? (int)num(w[9]) : 1;
+        } catch (const std::exception &) {
+            return bad("not a number");
         }
-        r.dtype = parse_dtype(dt);
-        r.variant = parse_variant(var);
-        if (r.dtype < 0 || r.variant < 0 || r.tile <= 0 || r.run < 0 || r.run > 256 || r.keep < 0 || r.keep > 1) {
-            why = std::string(path) + ":" + std::to_string(lineno) + ": bad value";
-            return PF_ERR_IO;
-        }
+        if (r.rows < -1 || r.dtype < 0 || r.variant < 0 || (r.variant == PF_AUTO ? r.tile != 0 : r.tile <= 0) ||
+            r.run < 0 || r.run > 256 || r.keep < 0 ||
+            r.keep > 1 || r.ladder < 0 || r.ladder > 5 || (r.ladder != 0 && r.variant != PF_PREFREE) ||
+            r.hybrid < 0 || r.hybrid > 1)
+            return bad("bad value");
         out.push_back(r);
     }
     return PF_OK;
 }
 
+// tune/mi355x_tuning_table.txt beside the lib/ directory holding this library.
+std::string default_table_path()
+{
+    Dl_info di;
+    if (!dladdr(reinterpret_cast<void *>(&default_table_path), &di) || !di.dli_fname) return std::string();
+    std::string lib(di.dli_fname);
+    const size_t slash = lib.rfind('/');
+    const std::string dir = slash == std::string::npos ? std::string(".") : lib.substr(0, slash);
+    return dir + "/../tune/mi355x_tuning_table.txt";
+}
+
+// Loads the table once per process unless pf_set_tuning_table chose one.
+// Caller holds g_table_mu.
+void table_init_locked()
+{
+    if (g_table_env_done) return;
+    g_table_env_done = true;
+    const char *env = std::getenv("PREFREE_TUNING_TABLE");
+    const std::string path = env ? std::string(env) : default_table_path();
+    std::string why;
+    if (!path.empty() && load_table(path.c_str(), g_table, why) == PF_OK) {
+        g_table_path = path;
+    } else {
+        g_table.clear();
+        g_table_path.clear();
+    }
+}
+
 bool tile_supported(int variant, int dtype, int tile);
 
 // Decision of PF_AUTO: variant and tile, plus the run length and cache
-// policy when a tuning-table row fixes them (run 0 / keep -1: not fixed).
+// policy when a tuning-table row fixes them (run 0 / keep -1: not fixed), the
+// PREFREE ladder (0: the default) and whether FLAT may turn hybrid.
 struct Choice {
-    int variant = PF_ADAPTIVE, tile = 0, run = 0, keep = -1;
+    int variant = PF_ADAPTIVE, tile = 0, run = 0, keep = -1, ladder = 0;
+    bool hybrid = true;
 };
 
 bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
 {
     std::lock_guard<std::mutex> lock(g_table_mu);
-    if (!g_table_env_done) {
-        g_table_env_done = true;
-        const char *env = std::getenv("PREFREE_TUNING_TABLE");
-        std::string why;
-        if (env && *env && load_table(env, g_table, why) != PF_OK) g_table.clear();
-    }
+    table_init_locked();
+    const int rc = row_class(s);
     for (const TableRow &r : g_table) {
         if (r.dtype != dtype || (r.nnz_upper >= 0 && s.nnz >= r.nnz_upper)) continue;
+        if (r.rows != kRowsAny && r.rows != rc) continue;
+        if (r.variant == PF_AUTO) return false;  // this class keeps the built-in rules
         if (!tile_supported(r.variant, dtype, r.tile)) continue;
         c.variant = r.variant;
         c.tile = r.tile;
         c.run = r.run;
         c.keep = r.keep;
+        c.ladder = r.ladder;
+        c.hybrid = r.hybrid != 0;
         return true;
     }
     return false;
@@ -262,9 +345,11 @@ void set_grid(pf_plan_info &r)
     }
 }
 
-// A tuning-table row may fix the run length and cache policy of ADAPTIVE.
+// A tuning-table row may fix the run length and cache policy of ADAPTIVE and
+// the reduction ladder of PREFREE.
 void apply_overrides(const Choice &c, pf_plan_info &info)
 {
+    if (info.variant == PF_PREFREE && c.ladder > 0) info.ladder = c.ladder;
     if (info.variant != PF_ADAPTIVE) return;
     if (c.run > 0) {
         info.run_tiles = c.run;
@@ -371,11 +456,16 @@ namespace {
 // Launch configuration of a plan for a validated matrix with known statistics
 // (host only, apart from occupancy queries): variant and tile (PF_AUTO
 // resolved), run length, x windows, workspace size.
-int plan_info(const pf_row_stats &s, int n, int dtype, int variant, int tile, pf_plan_info *out)
+// `allow_hybrid` (optional) tells whether a FLAT plan of PF_AUTO may turn
+// hybrid: always, unless a tuning-table row says otherwise.
+int plan_info(const pf_row_stats &s, int n, int dtype, int variant, int tile, pf_plan_info *out,
+              bool *allow_hybrid = nullptr)
 {
     Choice c;
+    if (allow_hybrid) *allow_hybrid = true;
     if (variant == PF_AUTO) {  // an explicit tile is kept only if the chosen variant has it
         c = auto_choice(s, dtype);
+        if (allow_hybrid) *allow_hybrid = c.hybrid;
         variant = c.variant;
         if (tile <= 0 || !tile_supported(variant, dtype, tile)) tile = c.tile;
     }
@@ -593,9 +683,10 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
 int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
                void *stream, pf_plan **plan, const int *d_col = nullptr)
 {
-    const bool want_hybrid = (variant == PF_AUTO || variant == PF_FLAT) && tile <= 0;
+    bool allow_hybrid = true;
     pf_plan_info info;
-    const int st = plan_info(s, n, dtype, variant, tile, &info);
+    const int st = plan_info(s, n, dtype, variant, tile, &info, &allow_hybrid);
+    const bool want_hybrid = (variant == PF_AUTO || variant == PF_FLAT) && tile <= 0 && allow_hybrid;
     if (st != PF_OK) return st;
     pf_plan *p = new pf_plan();
     p->m = m;
@@ -1046,8 +1137,18 @@ int pf_set_tuning_table(const char *path)
     }
     std::lock_guard<std::mutex> lock(g_table_mu);
     g_table.swap(rows);
-    g_table_env_done = true;  // an explicit table (or none) overrides the environment
+    g_table_path = path ? path : "";
+    g_table_env_done = true;  // an explicit table (or none) overrides the environment and the default
     return PF_OK;
+}
+
+const char *pf_tuning_table(void)
+{
+    thread_local std::string path;
+    std::lock_guard<std::mutex> lock(g_table_mu);
+    table_init_locked();
+    path = g_table_path;
+    return path.c_str();
 }
 
 // Times `reps` back-to-back executions (after two warm-up launches) and
@@ -1100,6 +1201,8 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
     best.run_tiles = plan->info.run_tiles;
     best.keep_cached = plan->info.keep_cached;
     best.chunk_nnz = plan->info.chunk_nnz;
+    best.ladder = plan->info.variant == PF_PREFREE ? plan->info.ladder : 0;
+    best.hybrid = plan->info.hybrid;
     best.us = base_us;
     best.default_us = base_us;
     best.candidates = 1;
@@ -1127,33 +1230,40 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
             const bool chunked = uses_row_map(variant, tiles[ti]);
             const int nchunk = chunked ? (int)(sizeof kChunks / sizeof kChunks[0]) : 1;
             const long long rule_chunk = cand->info.chunk_nnz;
-            int cand_run = cand->info.run_tiles, cand_keep = cand->info.keep_cached;
+            // PREFREE: the reference tuner's code axis, its five reduction ladders
+            // (scripts/profile_and_generate.py:109-235)
+            const int nladder = variant == PF_PREFREE ? 5 : 1;
+            int cand_run = cand->info.run_tiles, cand_keep = cand->info.keep_cached, cand_ladder = cand->info.ladder;
             long long cand_chunk = rule_chunk;
             double cand_us = 1e300;
-            for (int ri = 0; ri < nruns; ++ri) {
-                for (int k = 0; k < nkeep; ++k) {
-                    for (int ci = 0; ci < nchunk; ++ci) {
-                        if (ci > 0 && kChunks[ci] == rule_chunk) continue;  // timed as the rule's own
-                        if (walks_runs) {
-                            cand->info.run_tiles = kRuns[ri];
-                            if (variant == PF_ADAPTIVE) cand->info.keep_cached = k;
-                            else cand->info.needs_fixup = cand->info.ntiles > kRuns[ri];
-                        }
-                        if (chunked) cand->info.chunk_nnz = ci == 0 ? rule_chunk : kChunks[ci];
-                        set_grid(cand->info);
-                        double us = 0;
-                        st = time_plan(cand, d_row_ptr, d_col, d_val, d_x, d_y, reps, stream, &us);
-                        if (st != PF_OK) {
-                            pf_plan_destroy(cand);
-                            if (best_plan) pf_plan_destroy(best_plan);
-                            return st;
-                        }
-                        ++best.candidates;
-                        if (us < cand_us) {
-                            cand_us = us;
-                            cand_run = cand->info.run_tiles;
-                            cand_keep = cand->info.keep_cached;
-                            cand_chunk = cand->info.chunk_nnz;
+            for (int li = 0; li < nladder; ++li) {
+                for (int ri = 0; ri < nruns; ++ri) {
+                    for (int k = 0; k < nkeep; ++k) {
+                        for (int ci = 0; ci < nchunk; ++ci) {
+                            if (ci > 0 && kChunks[ci] == rule_chunk) continue;  // timed as the rule's own
+                            if (walks_runs) {
+                                cand->info.run_tiles = kRuns[ri];
+                                if (variant == PF_ADAPTIVE) cand->info.keep_cached = k;
+                                else cand->info.needs_fixup = cand->info.ntiles > kRuns[ri];
+                            }
+                            if (chunked) cand->info.chunk_nnz = ci == 0 ? rule_chunk : kChunks[ci];
+                            if (variant == PF_PREFREE) cand->info.ladder = li + 1;
+                            set_grid(cand->info);
+                            double us = 0;
+                            st = time_plan(cand, d_row_ptr, d_col, d_val, d_x, d_y, reps, stream, &us);
+                            if (st != PF_OK) {
+                                pf_plan_destroy(cand);
+                                if (best_plan) pf_plan_destroy(best_plan);
+                                return st;
+                            }
+                            ++best.candidates;
+                            if (us < cand_us) {
+                                cand_us = us;
+                                cand_run = cand->info.run_tiles;
+                                cand_keep = cand->info.keep_cached;
+                                cand_chunk = cand->info.chunk_nnz;
+                                cand_ladder = cand->info.ladder;
+                            }
                         }
                     }
                 }
@@ -1162,6 +1272,7 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
                 cand->info.run_tiles = cand_run;
                 cand->info.keep_cached = cand_keep;
                 cand->info.chunk_nnz = cand_chunk;
+                cand->info.ladder = cand_ladder;
                 if (cand->info.variant == PF_FLAT && cand->info.tile == kFlowTile)
                     cand->info.needs_fixup = cand->info.ntiles > cand_run;
                 set_grid(cand->info);
@@ -1170,6 +1281,8 @@ int pf_plan_autotune(pf_plan *plan, const int *d_row_ptr, const int *d_col, cons
                 best.run_tiles = cand->info.run_tiles;
                 best.keep_cached = cand->info.keep_cached;
                 best.chunk_nnz = cand->info.chunk_nnz;
+                best.ladder = cand->info.variant == PF_PREFREE ? cand->info.ladder : 0;
+                best.hybrid = 0;
                 best.us = cand_us;
                 if (best_plan) pf_plan_destroy(best_plan);
                 best_plan = cand;

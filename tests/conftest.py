@@ -3,11 +3,17 @@
 The package directory is `prefree-public_amd/` (not an importable name), so it
 is loaded by path and registered as `prefree_amd`.  Native libraries are built
 only when they are missing (build with __graft_entry__.build() after a change).
+
+PF_AUTO's tests check its built-in rules: the tuning table that ships with the
+library (loaded by default) is switched off here with an empty
+$PREFREE_TUNING_TABLE; the tests of the table load it explicitly.
 """
 import importlib.util
 import os
 import subprocess
 import sys
+
+os.environ["PREFREE_TUNING_TABLE"] = ""
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_DIR = os.path.join(REPO, "prefree-public_amd")
