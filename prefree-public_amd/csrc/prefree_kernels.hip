@@ -1817,8 +1817,13 @@ __device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const Dens
     int cA[U], cB[U];
     T vA[U], vB[U];
     P acc = P(0);
+    // Batches start at the segment's first nnz rounded down to a multiple of 64,
+    // so every 64-lane load covers whole 128-byte lines of col and val (a
+    // segment starts anywhere; unaligned, a load touched one line more); the
+    // lanes before the segment's start read the row's earlier nnz and add nothing.
+    const int ma = ms & ~(kWave - 1);
     const auto issue = [&](int k, int j, int (&c)[U], T (&v)[U]) {
-        const int s = __builtin_amdgcn_readlane(ms, k), e = __builtin_amdgcn_readlane(me, k);
+        const int s = __builtin_amdgcn_readlane(ma, k), e = __builtin_amdgcn_readlane(me, k);
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
 #pragma unroll
@@ -1826,11 +1831,14 @@ __device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const Dens
             load1(rc, rv, j + u * kWave + lane, c[u], v[u]);
     };
     const auto consume = [&](int k, int j, const int (&c)[U], const T (&v)[U]) {
-        const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ms, k);
+        const int base = __builtin_amdgcn_readlane(ma, k);
+        const int lead = __builtin_amdgcn_readlane(ms, k) - base;
+        const int len = __builtin_amdgcn_readlane(me, k) - base;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {  // no product for slots past the segment (x may hold inf or NaN)
+        for (int u = 0; u < U; ++u) {  // no product for slots outside the segment (x may hold inf or NaN)
             const T xv = sx[(c[u] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
-            if (j + u * kWave + lane < len)
+            const int q = j + u * kWave + lane;
+            if (q >= lead && q < len)
                 acc += P(v[u]) * P(xv);
         }
         if (j + kWave * U >= len) {  // the row's last batch
@@ -1840,7 +1848,7 @@ __device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const Dens
         }
     };
     const auto advance = [&](int &k, int &j) {  // the batch after (k, j); false at the end
-        const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ms, k);
+        const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ma, k);
         j += kWave * U;
         if (j < len) return true;
         const uint64_t rest = todo & ~((2ull << k) - 1ull);
@@ -1913,19 +1921,23 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
             sg[w] = s;
             if (w == d.nwin - 1) sg[d.nwin] = e;
         }
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
+        // the same lanes and order as dense_rows_recorded (batches from s rounded down to 64), so that the
+        // call that searches and the calls that read the bounds give the same sums bit for bit
+        const int sa = s & ~(kWave - 1);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + sa, (long long)(e - sa) * 4);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + sa, (long long)(e - sa) * (long long)sizeof(T));
         P acc = P(0);
-        for (int j = 0; j < e - s; j += kWave * U) {
+        for (int j = 0; j < e - sa; j += kWave * U) {
             int c[U];
             T v[U];
 #pragma unroll
             for (int k = 0; k < U; ++k)
                 load1(rc, rv, j + k * kWave + lane, c[k], v[k]);
 #pragma unroll
-            for (int k = 0; k < U; ++k) {  // no product for slots past the segment (x may hold inf or NaN)
+            for (int k = 0; k < U; ++k) {  // no product for slots outside the segment (x may hold inf or NaN)
                 const T xv = sx[(c[k] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
-                if (j + k * kWave + lane < e - s)
+                const int q = j + k * kWave + lane;
+                if (q >= s - sa && q < e - sa)
                     acc += P(v[k]) * P(xv);
             }
         }
