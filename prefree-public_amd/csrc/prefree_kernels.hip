@@ -1633,7 +1633,10 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         } else {
             const int i = run_of_tile(rt, t, lane);
             const int R = rt.nruns + 1;
-            const int nb = rt.runs[3 * R + i], ne = rt.runs[4 * R + i];
+            // tiles from the run's first nnz rounded down to 64, so every 64-lane load covers whole lines of
+            // col and val; the nnz before the run's first row belong to the dense row before it and are
+            // neither gathered nor summed (they precede row_ptr[f])
+            const int nb = rt.runs[3 * R + i] & ~(kWave - 1), ne = rt.runs[4 * R + i];
             kb = nb + (int)(t - rt.runs[i]) * K;
             last = ne - kb <= K;
             B0 = last ? ne : kb + K;

@@ -629,7 +629,8 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     for (int i = 0; i < nruns; ++i) {
         runs[(size_t)i] = (int)tiles;
         const long long rr = runs[(size_t)2 * R + i] - runs[(size_t)R + i];
-        const long long nz = runs[(size_t)4 * R + i] - runs[(size_t)3 * R + i];
+        // the kernel starts a run's tiles at its first nnz rounded down to 64 (whole lines per load)
+        const long long nz = runs[(size_t)4 * R + i] - (runs[(size_t)3 * R + i] & ~63LL);
         tiles += rr > 0 ? std::max(1LL, (nz + K - 1) / K) : 0;
     }
     runs[(size_t)nruns] = (int)tiles;  // 0 when every row is dense: only the dense kernels run
