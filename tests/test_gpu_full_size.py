@@ -49,3 +49,36 @@ def test_full_size_known_answer_and_random(cfg, dtype):
     assert err <= TOL[dtype], f"C{cfg} {dtype} {info['variant_name']}: row {worst} error {err:.3e}"
     print(f"C{cfg} {dtype} {info['variant_name']} {info['tile']}: known answer exact, U[-1,1] max error {err:.2e}",
           flush=True)
+
+
+OTHER = [(5, "prefree", 0, 3), (5, "prefree", 1024, 4), (4, "prefree", 0, 3), (2, "adaptive", 0, 0),
+         (5, "flat", 2048, 0)]
+
+
+@pytest.mark.parametrize("cfg,variant,tile,ladder", OTHER,
+                         ids=[f"C{c}-{v}-{t}-{l}" for c, v, t, l in OTHER])
+def test_full_size_other_tilings(cfg, variant, tile, ladder):
+    """The reference algorithm at full size, atomics on every tile-boundary row over C5's dense rows
+    included, the ADAPTIVE tiling on C2, and C5 in split-row FLAT tiles (a plan whose dense rows are not
+    made hybrid): known-answer inputs bit-exact, U[-1,1] within the tolerance."""
+    rp, col, kv = pf.synth_csr(cfg, seed=1, vals=1, dtypes=("f64",))
+    m, nnz = len(rp) - 1, len(col)
+    kx = pf.synth_x(cfg, m, seed=1, vals=1, dtypes=("f64",))["f64"]
+    print(f"C{cfg} {variant} tile {tile} ladder {ladder}: m={m} nnz={nnz}", flush=True)
+    kw = {"ladder": ladder} if ladder else {}
+    y, info = gpu_spmv(rp, col, kv["f64"], kx, variant, tile, **kw)
+    assert info["variant_name"] == variant and not info["hybrid"]
+    if ladder:
+        assert info["ladder"] == ladder
+    ref = oracle.spmv_omp(rp, col, kv["f64"], kx)
+    bad = np.flatnonzero(ref != y)
+    assert bad.size == 0, f"C{cfg} {variant}: {bad.size} rows differ, first {bad[:5]}"
+    del kv
+    rng = np.random.default_rng(cfg + 10)
+    val = rng.uniform(-1, 1, nnz)
+    x = rng.uniform(-1, 1, m)
+    y, info = gpu_spmv(rp, col, val, x, variant, tile, **kw)
+    ref = oracle.spmv_omp(rp, col, val, x)
+    err, zero_bad, worst = oracle.rownorm_maxerr(rp, col, val, x, ref, y)
+    assert zero_bad == 0 and err <= TOL["f64"], f"C{cfg} {variant}: row {worst} error {err:.3e}"
+    print(f"C{cfg} {variant} {info['tile']}: known answer exact, U[-1,1] max error {err:.2e}", flush=True)
