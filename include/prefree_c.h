@@ -92,14 +92,16 @@ typedef struct pf_plan_info {
     long long chunk_nnz;  /* FLAT 1024/2048 without x windows: tiles dealt to the 8 XCDs in chunks of
                              consecutive tiles of about this many nnz (0 = one chunk per XCD) */
     int ladder;           /* PREFREE: the reduction ladder 1..5 (see pf_plan_set_ladder); 0 otherwise */
-    int hybrid;           /* 1: rows of at least a few thousand nnz with sorted columns ("dense rows") are summed
-                             by x windows staged in LDS, shared by 128 rows at a time, and the other rows (at
-                             most 256 nnz each) in row-aligned tiles; chosen at planning (PF_AUTO or PF_FLAT
-                             with the default tile, columns given) for split-row FLAT matrices of that shape
-                             (pf_plan_set_hybrid switches it) */
-    long long dense_rows; /* hybrid plans: rows summed by x windows */
+    int hybrid;           /* 1: the rows over 256 nnz are summed apart from the others, which go in row-aligned
+                             tiles; chosen at planning (PF_AUTO or PF_FLAT with the default tile, columns given)
+                             for split-row FLAT matrices of that shape (pf_plan_set_hybrid switches it).  Dense
+                             mode: rows of at least a few thousand nnz with sorted columns ("dense rows") summed by
+                             x windows staged in LDS, shared by 128 rows at a time.  Long mode (long_tiles > 0):
+                             the long rows cut into tiles of 1024 nnz dealt to the XCDs by their first column. */
+    long long dense_rows; /* hybrid plans: the rows summed apart (dense rows, or long rows in long mode) */
     int x_halves;         /* hybrid plans: 1 = the runs' tiles are processed once per half of x, by XCDs 0-3 and
                              4-7, so each XCD's random gathers fall in half of x (chosen when x is 4-24 MB) */
+    int long_tiles;       /* hybrid plans in long mode: tiles of the long rows; 0 otherwise */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;

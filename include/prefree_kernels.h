@@ -90,7 +90,23 @@ typedef struct pfk_spmv_args {
                                 to y in that order (each XCD's random gathers then fall in half of x) */
     void *half_part;         /* [m] values of dtype */
     size_t half_part_bytes;
+    /* Hybrid plans whose long rows (over PFK_ALIGN_ROW_MAX nnz) are not all dense with sorted columns: those
+     * rows (dense_rows, n_dense of them) are cut into tiles of PFK_LONG_TILE nnz, each tile's partial sum
+     * computed by one workgroup, and each row's partials added in tile order.  dense_seg, dense_part and
+     * n_win are then unused. */
+    int long_mode;           /* 1: long-row tiles instead of dense x windows */
+    int n_long_tiles;
+    const int *long_tiles;   /* [4 * n_long_tiles], in row order: (row index into dense_rows, first nnz loaded
+                                (a multiple of 64), first nnz of the row in the tile, end) */
+    const int *long_deal;    /* [n_long_tiles] tile indices in the order the 8 XCDs take them: by first column,
+                                XCD k the k-th eighth */
+    const int *long_row_tiles; /* [n_dense + 1] first tile of each long row; the last = n_long_tiles */
+    void *long_part;         /* [n_long_tiles] partial sums, PFK_SLOT_BYTES(dtype) each */
+    size_t long_tiles_bytes, long_deal_bytes, long_row_tiles_bytes, long_part_bytes;
 } pfk_spmv_args;
+
+/* nnz per long-row tile of a hybrid plan in long mode. */
+#define PFK_LONG_TILE 1024
 
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
 #define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
@@ -98,8 +114,8 @@ typedef struct pfk_spmv_args {
 /* Columns per x window of a hybrid plan's dense-row kernel (64 KB of LDS). */
 #define PFK_DENSE_WINDOW(dtype) ((dtype) == 0 ? 8192 : 16384)
 
-/* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums and
- * their combine, three launches.  map_ready 0: the call searches rows and segment bounds (and records them
+/* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums (or, in
+ * long mode, the long-row tiles) and their combine, three or four launches.  map_ready 0: the call searches rows and segment bounds (and records them
  * when run_map / dense_seg are given); 1: it reads them. */
 int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream);
 /* Planning scan of a hybrid plan: every row of at least dmin nnz as (row, row_ptr[row], row_ptr[row+1]) into
@@ -107,6 +123,9 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream);
  * counters[1] = listed rows whose columns decrease somewhere.  counters must be zero on entry. */
 int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *list, int cap, int *counters,
                    void *stream);
+/* out[i] = col[idx[i]] for i < count (planning of long-row tiles: each tile's first column); every idx must lie
+ * in [0, nnz). */
+int pfk_gather_cols(const int *col, long long nnz, const int *idx, int count, int *out, void *stream);
 
 /* Ints of an x-window schedule. */
 #define PFK_SCHED_INTS(ntiles, cap) (16 + 8 * (cap) + (ntiles))

@@ -61,7 +61,7 @@ class PlanInfo(ctypes.Structure):
                 ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
                 ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int), ("hybrid", ctypes.c_int),
-                ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int)]
+                ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int), ("long_tiles", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -102,7 +102,11 @@ class SpmvArgs(ctypes.Structure):
                 ("dense_seg", ctypes.c_void_p), ("dense_part", ctypes.c_void_p), ("runs_bytes", ctypes.c_size_t),
                 ("run_map_bytes", ctypes.c_size_t), ("dense_seg_bytes", ctypes.c_size_t),
                 ("dense_part_bytes", ctypes.c_size_t), ("x_halves", ctypes.c_int), ("half_part", ctypes.c_void_p),
-                ("half_part_bytes", ctypes.c_size_t)]
+                ("half_part_bytes", ctypes.c_size_t), ("long_mode", ctypes.c_int), ("n_long_tiles", ctypes.c_int),
+                ("long_tiles", ctypes.c_void_p), ("long_deal", ctypes.c_void_p), ("long_row_tiles", ctypes.c_void_p),
+                ("long_part", ctypes.c_void_p), ("long_tiles_bytes", ctypes.c_size_t),
+                ("long_deal_bytes", ctypes.c_size_t), ("long_row_tiles_bytes", ctypes.c_size_t),
+                ("long_part_bytes", ctypes.c_size_t)]
 
 
 _lib = None

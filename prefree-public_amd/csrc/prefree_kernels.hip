@@ -2014,6 +2014,120 @@ __global__ __launch_bounds__(kBS) void k_rows_halves_add(T *__restrict__ y, cons
         y[r] = T(acc_t<T>(y[r]) + acc_t<T>(y2[r]));
 }
 
+// ---- k_long: long rows of a hybrid plan in long mode -------------------------
+//
+// A matrix whose long rows (over PFK_ALIGN_ROW_MAX nnz) are not all dense rows
+// with sorted columns (a power-law matrix, C3) keeps its short rows in the
+// row-aligned runs and cuts each long row into tiles of kLongTile nnz.  One
+// workgroup sums one tile: each lane its 4 elements of the wave-strided
+// layout in order, then the wave's DPP tree, then the 4 waves in order, one
+// partial per tile; k_long_sum adds a row's partials in tile order, so the
+// result is deterministic.  The host deals the tiles to the 8 XCDs by their
+// first column, XCD k taking the k-th eighth: with sorted columns each XCD
+// then gathers from about an eighth of x, which stays in its L2.  A tile's
+// loads start at a multiple of 64 nnz (whole lines); its slots before the
+// row's first nnz or past its end add nothing.
+constexpr int kLongTile = PFK_LONG_TILE;
+static_assert(kLongTile == 4 * kBS, "one 4-element group of the wave-strided layout per lane");
+
+struct LongArgs {
+    const int4 *__restrict__ tiles;  // (row index, first nnz loaded, first nnz of the row, end)
+    const int *__restrict__ deal;
+    const int *__restrict__ row_tiles;
+    const int *__restrict__ rows;
+    int nrows, ntiles;
+    void *__restrict__ part;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_long(Args<T> a, LongArgs L)
+{
+    using P = acc_t<T>;
+    __shared__ P s_red[kWaves];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int per = (L.ntiles + kXcds - 1) / kXcds;
+    const int q = (int)(blockIdx.x / kXcds);
+    const int slot = (int)(blockIdx.x % kXcds) * per + q;
+    if (q >= per || slot >= L.ntiles)
+        return;  // whole workgroup: padding of the XCD deal
+    const int t = L.deal[slot];
+    if (t < 0 || t >= L.ntiles) {  // a deal entry that is not a tile: skip it, report it (whole workgroup)
+        if (tid == 0) atomicOr(a.err, 1);
+        return;
+    }
+    const int4 d = L.tiles[t];
+    const int nnz = a.nnz;
+    const int s = min(max(d.y, 0), nnz);                // first nnz loaded
+    const int e = min(max(d.w, s), min(nnz, s + kLongTile));
+    const int lo = min(max(d.z, s), e) - s;             // slots before lo belong to the row before
+    const int len = e - s;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)len * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)len * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+    int c[4];
+    T v[4], xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        load1(rc, rv, tile_elem<T>(0, j), c[j], v[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int qj = tile_elem<T>(0, j);
+        xv[j] = buf_load(rx, qj >= lo && qj < len ? (uint32_t)c[j] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    }
+    P acc = P(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // no product for slots outside the row (x may hold inf or NaN)
+        const int qj = tile_elem<T>(0, j);
+        if (qj >= lo && qj < len)
+            acc += P(v[j]) * P(xv[j]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) s_red[wave] = acc;
+    lds_sync();
+    if (tid == 0) {
+        P tot = s_red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w)
+            tot += s_red[w];
+        static_cast<P *>(L.part)[t] = tot;
+    }
+}
+
+// y of each long row from its tiles' partials: one wave per row, lane j adding
+// tiles j, j + 64, ... in order, then the wave's DPP tree (a fixed order).
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
+{
+    using P = acc_t<T>;
+    const int i = blockIdx.x * kWaves + (int)threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (i >= L.nrows)
+        return;  // whole wave
+    const int r = L.rows[i];
+    if (r < 0 || r >= a.m) {  // a table entry that is not a row (whole wave)
+        if (lane == 0) atomicOr(a.err, 1);
+        return;
+    }
+    const int b0 = min(max(L.row_tiles[i], 0), L.ntiles);
+    const int b1 = min(max(L.row_tiles[i + 1], b0), L.ntiles);
+    const P *pp = static_cast<const P *>(L.part);
+    P sum = P(0);
+    for (int t = b0 + lane; t < b1; t += kWave)
+        sum += pp[t];
+    sum = wave_sum(sum);
+    if (lane == 0) a.y[r] = T(sum);
+}
+
+// Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
+__global__ __launch_bounds__(kBS) void k_gather_cols(const int *__restrict__ col, long long nnz,
+                                                     const int *__restrict__ idx, int count, int *__restrict__ out)
+{
+    for (long long i = (long long)blockIdx.x * kBS + threadIdx.x; i < count; i += (long long)gridDim.x * kBS) {
+        const int k = idx[i];
+        out[i] = k >= 0 && k < nnz ? col[k] : -1;
+    }
+}
+
 // ---- k_flow: FLAT tiles of 256 nnz with carried row sums ------------------
 //
 // Every wave64 walks a run of consecutive 256-nnz tiles (one 4-nnz vector per
@@ -3121,7 +3235,7 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     const bool halves = a->x_halves && a->half_part;
     if (r.ntiles > 0) chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8, halves ? kXcds / 2 : kXcds);
     const RunTable rt{a->runs, a->n_runs};
-    const bool memo = a->map_ready && a->run_map && a->dense_seg;
+    const bool memo = a->map_ready && a->run_map && (a->long_mode || a->dense_seg);
     const bool prio = (long long)a->nnz < 4LL * a->m;
     const dim3 rgrid((unsigned)(r.g8 * kXcds));
     if (a->ntiles == 0)  // every row is dense
@@ -3141,6 +3255,17 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
         hipLaunchKernelGGL((k_rows_halves_add<T>), dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream), r.y, r.y2,
                            a->m);
         PFK_LAUNCHED("k_rows_halves_add");
+    }
+    if (a->long_mode) {
+        const LongArgs L{reinterpret_cast<const int4 *>(a->long_tiles), a->long_deal, a->long_row_tiles,
+                         a->dense_rows, a->n_dense, a->n_long_tiles, a->long_part};
+        const unsigned lgrid = (unsigned)(kXcds * ((a->n_long_tiles + kXcds - 1) / kXcds));
+        hipLaunchKernelGGL((k_long<T>), dim3(lgrid), dim3(kBS), 0, S(stream), r, L);
+        PFK_LAUNCHED("k_long");
+        hipLaunchKernelGGL((k_long_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0,
+                           S(stream), r, L);
+        PFK_LAUNCHED("k_long_sum");
+        return PF_OK;
     }
     const int ngroups = (a->n_dense + DenseShape<T>::kG - 1) / DenseShape<T>::kG;
     const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, a->dense_seg, a->dense_part};
@@ -3189,21 +3314,30 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
     pfk_spmv_args v = *a;  // a hybrid plan may have no run tiles (every row dense)
     v.ntiles = a->ntiles > 0 ? a->ntiles : 1;
     if (a->ntiles < 0 || !args_ok(&v, false) || a->n_dense < 1 || a->n_runs < 1 || !a->dense_rows || !a->runs ||
-        !a->dense_part ||
+        (a->long_mode ? (!a->long_tiles || !a->long_deal || !a->long_row_tiles || !a->long_part ||
+                         a->n_long_tiles < 1)
+                      : !a->dense_part) ||
         (a->tile != 1024 && a->tile != 2048)) {
         snprintf(g_err, sizeof g_err, "hybrid call: missing tables or tile %d", a->tile);
         return PF_ERR_INVALID;
     }
     const long long win = PFK_DENSE_WINDOW(dtype);
-    if (a->n_win != (int)((a->n + win - 1) / win) || a->n_win < 1) {
+    if (!a->long_mode && (a->n_win != (int)((a->n + win - 1) / win) || a->n_win < 1)) {
         snprintf(g_err, sizeof g_err, "hybrid call: %d x windows for n = %d", a->n_win, a->n);
         return PF_ERR_INVALID;
     }
-    const long long nd = a->n_dense, nw = a->n_win;
+    const long long nd = a->n_dense, nw = a->n_win, nl = a->n_long_tiles;
     if (!room(a->runs, a->runs_bytes, 5LL * (a->n_runs + 1) * 4, "run table") ||
-        !room(a->dense_part, a->dense_part_bytes, nd * nw * PFK_SLOT_BYTES(dtype), "dense partial sums") ||
+        (!a->long_mode && !room(a->dense_part, a->dense_part_bytes, nd * nw * PFK_SLOT_BYTES(dtype),
+                                "dense partial sums")) ||
+        (a->long_mode && (!room(a->long_tiles, a->long_tiles_bytes, nl * 16, "long-row tiles") ||
+                          !room(a->long_deal, a->long_deal_bytes, nl * 4, "long-row tile deal") ||
+                          !room(a->long_row_tiles, a->long_row_tiles_bytes, (nd + 1) * 4, "long-row tile index") ||
+                          !room(a->long_part, a->long_part_bytes, nl * PFK_SLOT_BYTES(dtype),
+                                "long-row partial sums"))) ||
         (a->run_map && !room(a->run_map, a->run_map_bytes, a->ntiles * 32, "run tile map")) ||
-        (a->dense_seg && !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")) ||
+        (!a->long_mode && a->dense_seg &&
+         !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")) ||
         (a->x_halves && !room(a->half_part, a->half_part_bytes, (long long)a->m * (dtype == PF_F64 ? 8 : 4),
                               "x-halves row sums")))
         return PF_ERR_INVALID;
@@ -3220,6 +3354,16 @@ int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *lis
     hipLaunchKernelGGL(k_dense_sorted, dim3(64, (unsigned)std::min(cap, 4096)), dim3(kBS), 0, S(stream), col, list,
                        cap, counters);
     PFK_LAUNCHED("k_dense_sorted");
+    return PF_OK;
+}
+
+int pfk_gather_cols(const int *col, long long nnz, const int *idx, int count, int *out, void *stream)
+{
+    if (!col || !idx || !out || count < 0 || nnz < 0) return PF_ERR_INVALID;
+    if (count == 0) return PF_OK;
+    hipLaunchKernelGGL(k_gather_cols, dim3(grid_for(count, kBS, 1024)), dim3(kBS), 0, S(stream), col, nnz, idx, count,
+                       out);
+    PFK_LAUNCHED("k_gather_cols");
     return PF_OK;
 }
 

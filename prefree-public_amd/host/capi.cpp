@@ -5,6 +5,7 @@
 #include "prefree_kernels.h"
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -449,6 +450,12 @@ struct pf_plan {
     bool x_halves = false;       // run tiles processed per half of x (see pfk_spmv_args.x_halves)
     void *half_part = nullptr;   // [m] second-half row sums
     size_t half_part_bytes = 0;
+    // long mode: the long rows (dense_rows) cut into tiles of PFK_LONG_TILE nnz instead of x windows
+    bool long_mode = false;
+    int n_long_tiles = 0;
+    int *long_tiles = nullptr, *long_deal = nullptr, *long_row_tiles = nullptr;
+    void *long_part = nullptr;
+    size_t long_tiles_bytes = 0, long_deal_bytes = 0, long_row_tiles_bytes = 0, long_part_bytes = 0;
 };
 
 namespace {
@@ -566,8 +573,10 @@ long long rows_at_least_pow2(const pf_row_stats &s, int j)
     return c;
 }
 
-// A hybrid plan fits matrices whose long rows (over 256 nnz) are all dense
-// (dense_min or more) and whose columns are checked (the scan needs col).
+// A hybrid plan fits split-row FLAT matrices with some rows over 256 nnz and
+// checked columns (the planning scan reads col) when those rows may all be
+// dense (the histogram allows it) or x exceeds one XCD's L2 (long mode);
+// try_hybrid decides.
 bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_plan_info &info, const int *d_col)
 {
     if (!d_col || (dtype != PF_F64 && dtype != PF_F32) || info.variant != PF_FLAT || info.row_aligned ||
@@ -576,50 +585,62 @@ bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_pl
     const long long t = dense_min(n, dtype);
     int j = 0;
     while ((1LL << j) < t) ++j;
-    if (rows_at_least_pow2(s, j) != s.n_long_rows) return false;
-    const long long nwin = (n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype);
-    return s.n_long_rows * (nwin + 1) <= (64LL << 20);  // segment table under 256 MB
+    return rows_at_least_pow2(s, j) == s.n_long_rows || n * value_bytes(dtype) > kXcdL2Bytes;
 }
 
-// Adds the hybrid path to a split-row FLAT plan when its long rows have sorted
-// columns: lists them (a planning scan), cuts the rows between them into runs
-// of row-aligned tiles and allocates the tables.  Leaves the plan as it is
-// (split-row tiles) otherwise.
+// Adds the hybrid path to a split-row FLAT plan.  A planning scan lists the
+// rows over 256 nnz and checks their columns.  When they are all dense rows
+// (dense_min nnz or more) with sorted columns, they are summed by x windows
+// (dense mode); otherwise, when they hold a tile (1024 nnz) or more on average
+// and x exceeds one XCD's L2, they are cut into tiles dealt to the XCDs by
+// their first column (long mode).  The rows between them are cut into runs of
+// row-aligned tiles.  Leaves the plan as it is (split-row tiles) otherwise.
 int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
 {
     const int dtype = p->info.dtype;
     const long long cap = p->stats.n_long_rows;
-    const int dmin = (int)dense_min(p->n, dtype);
     int *tmp = nullptr;
-    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&tmp), (size_t)(2 + 3 * cap) * sizeof(int)), "dense scan buffer");
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&tmp), (size_t)(2 + 3 * cap) * sizeof(int)), "long-row scan buffer");
     std::vector<int> list((size_t)(3 * cap));
     int cnt[2] = {0, 0};
     int st = pfk_fill_zero(tmp, 2 * sizeof(int), stream);
-    if (st == PF_OK) st = pfk_dense_scan(d_row_ptr, d_col, p->m, dmin, tmp + 2, (int)cap, tmp, stream);
+    if (st == PF_OK) st = pfk_dense_scan(d_row_ptr, d_col, p->m, PFK_ALIGN_ROW_MAX + 1, tmp + 2, (int)cap, tmp, stream);
     if (st == PF_OK) st = pfk_memcpy_d2h(cnt, tmp, sizeof cnt, stream);
     if (st == PF_OK) st = pfk_memcpy_d2h(list.data(), tmp + 2, list.size() * sizeof(int), stream);
     if (st == PF_OK) st = pfk_stream_sync(stream);
     pfk_free(tmp);
-    if (st != PF_OK) return from_kernel_layer(st, "dense scan");
-    if (cnt[0] != cap || cnt[1] != 0) return PF_OK;  // unsorted columns in a long row: stay split-row
+    if (st != PF_OK) return from_kernel_layer(st, "long-row scan");
+    if (cnt[0] != cap) return PF_OK;  // row_ptr and the statistics disagree: stay split-row
 
-    // Dense rows ascending, and the runs of rows between them.
+    // Long rows ascending, and the runs of rows between them.
     std::vector<int> order((size_t)cap);
     for (long long k = 0; k < cap; ++k) order[(size_t)k] = (int)k;
     std::sort(order.begin(), order.end(), [&](int x, int y) { return list[3 * (size_t)x] < list[3 * (size_t)y]; });
     const int nd = (int)cap, nruns = nd + 1, R = nruns + 1;
-    std::vector<int> rows((size_t)nd), runs((size_t)5 * R, 0);
-    long long short_rows = 0, short_nnz = 0;
+    std::vector<int> rows((size_t)nd), rb0((size_t)nd), rb1((size_t)nd), runs((size_t)5 * R, 0);
+    long long short_rows = 0, short_nnz = 0, long_nnz = 0, shortest = INT32_MAX;
+    for (int i = 0; i < nd; ++i) {
+        rows[(size_t)i] = list[3 * (size_t)order[(size_t)i]];
+        rb0[(size_t)i] = list[3 * (size_t)order[(size_t)i] + 1];
+        rb1[(size_t)i] = list[3 * (size_t)order[(size_t)i] + 2];
+        long_nnz += rb1[(size_t)i] - rb0[(size_t)i];
+        shortest = std::min(shortest, (long long)(rb1[(size_t)i] - rb0[(size_t)i]));
+    }
+    const int nwin = (int)((p->n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
+    const long long xb = (long long)p->n * value_bytes(dtype);
+    const bool dense = cnt[1] == 0 && shortest >= dense_min(p->n, dtype) &&
+                       cap * (nwin + 1) <= (64LL << 20);  // segment table under 256 MB
+    const bool lng = !dense && long_nnz >= (long long)PFK_LONG_TILE * cap && xb > kXcdL2Bytes;
+    if (!dense && !lng) return PF_OK;
     for (int i = 0; i < nruns; ++i) {
-        const int rb = i == 0 ? 0 : list[3 * (size_t)order[(size_t)i - 1]] + 1;
-        const int re = i == nd ? p->m : list[3 * (size_t)order[(size_t)i]];
-        const int nb = i == 0 ? 0 : list[3 * (size_t)order[(size_t)i - 1] + 2];
-        const int ne = i == nd ? p->nnz : list[3 * (size_t)order[(size_t)i] + 1];
+        const int rb = i == 0 ? 0 : rows[(size_t)i - 1] + 1;
+        const int re = i == nd ? p->m : rows[(size_t)i];
+        const int nb = i == 0 ? 0 : rb1[(size_t)i - 1];
+        const int ne = i == nd ? p->nnz : rb0[(size_t)i];
         runs[(size_t)R + i] = rb;
         runs[(size_t)2 * R + i] = re;
         runs[(size_t)3 * R + i] = nb;
         runs[(size_t)4 * R + i] = ne;
-        if (i < nd) rows[(size_t)i] = list[3 * (size_t)order[(size_t)i]];
         short_rows += re - rb;
         short_nnz += ne - nb;
     }
@@ -633,47 +654,99 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
         const long long nz = runs[(size_t)4 * R + i] - (runs[(size_t)3 * R + i] & ~63LL);
         tiles += rr > 0 ? std::max(1LL, (nz + K - 1) / K) : 0;
     }
-    runs[(size_t)nruns] = (int)tiles;  // 0 when every row is dense: only the dense kernels run
-    const int nwin = (int)((p->n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
+    runs[(size_t)nruns] = (int)tiles;  // 0 when every row is long: only the long-row kernels run
+    // Long mode: each long row in tiles of PFK_LONG_TILE nnz from its first nnz rounded down to 64.
+    std::vector<int> lt, row_tiles((size_t)nd + 1, 0), first;
+    if (lng) {
+        for (int i = 0; i < nd; ++i) {
+            row_tiles[(size_t)i] = (int)(lt.size() / 4);
+            const long long s0 = rb0[(size_t)i] & ~63LL;
+            for (long long st0 = s0; st0 < rb1[(size_t)i]; st0 += PFK_LONG_TILE) {
+                const long long f = std::max<long long>(st0, rb0[(size_t)i]);
+                lt.insert(lt.end(), {i, (int)st0, (int)f, (int)std::min<long long>(rb1[(size_t)i], st0 + PFK_LONG_TILE)});
+                first.push_back((int)f);
+            }
+        }
+        row_tiles[(size_t)nd] = (int)(lt.size() / 4);
+    }
+    const long long nlt = lng ? (long long)lt.size() / 4 : 0;
     auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
     const size_t b_rows = up((size_t)nd * 4), b_runs = up((size_t)5 * R * 4), b_map = up((size_t)tiles * 32),
-                 b_seg = up((size_t)nd * (nwin + 1) * 4), b_part = up((size_t)nd * nwin * slot_bytes(dtype)),
+                 b_seg = dense ? up((size_t)nd * (nwin + 1) * 4) : 0,
+                 b_part = dense ? up((size_t)nd * nwin * slot_bytes(dtype)) : up((size_t)nlt * slot_bytes(dtype)),
+                 b_lt = up((size_t)nlt * 16), b_deal = up((size_t)nlt * 4), b_rt = lng ? up(((size_t)nd + 1) * 4) : 0,
                  b_half = up((size_t)p->m * value_bytes(dtype));
     void *w = nullptr;
-    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_half), "hybrid tables");
+    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_lt + b_deal + b_rt + b_half), "hybrid tables");
     char *c = static_cast<char *>(w);
     p->ws_hyb = w;
     p->dense_rows = reinterpret_cast<int *>(c);
-    p->runs = reinterpret_cast<int *>(c + b_rows);
-    p->run_map = reinterpret_cast<int *>(c + b_rows + b_runs);
-    p->dense_seg = reinterpret_cast<int *>(c + b_rows + b_runs + b_map);
-    p->dense_part = c + b_rows + b_runs + b_map + b_seg;
-    p->half_part = c + b_rows + b_runs + b_map + b_seg + b_part;
+    c += b_rows;
+    p->runs = reinterpret_cast<int *>(c);
+    c += b_runs;
+    p->run_map = reinterpret_cast<int *>(c);
+    c += b_map;
+    p->dense_seg = dense ? reinterpret_cast<int *>(c) : nullptr;
+    c += b_seg;
+    void *part = c;
+    c += b_part;
+    p->long_tiles = lng ? reinterpret_cast<int *>(c) : nullptr;
+    c += b_lt;
+    p->long_deal = lng ? reinterpret_cast<int *>(c) : nullptr;
+    c += b_deal;
+    p->long_row_tiles = lng ? reinterpret_cast<int *>(c) : nullptr;
+    c += b_rt;
+    p->half_part = c;
     p->half_part_bytes = b_half;
     p->runs_bytes = b_runs;
     p->run_map_bytes = b_map;
     p->dense_seg_bytes = b_seg;
-    p->dense_part_bytes = b_part;
+    p->dense_part = dense ? part : nullptr;
+    p->dense_part_bytes = dense ? b_part : 0;
+    p->long_mode = lng;
+    p->n_long_tiles = (int)nlt;
+    p->long_part = lng ? part : nullptr;
+    p->long_part_bytes = lng ? b_part : 0;
+    p->long_tiles_bytes = b_lt;
+    p->long_deal_bytes = b_deal;
+    p->long_row_tiles_bytes = b_rt;
     p->n_dense = nd;
     p->n_runs = nruns;
-    p->n_win = nwin;
+    p->n_win = dense ? nwin : 0;
     p->run_tile = K;
     p->run_tiles = tiles;
     p->run_chunk = short_nnz < 4 * short_rows ? 0 : kChunkNnz;
     // The runs' random x gathers fall in half of x per XCD when x exceeds one
     // XCD's 4 MB L2 but a half of it nearly fits (x up to 24 MB).
-    const long long xb = (long long)p->n * value_bytes(dtype);
     p->x_halves = xb > kXcdL2Bytes && xb <= 6 * kXcdL2Bytes;
     p->info.x_halves = p->x_halves ? 1 : 0;
     st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
-    // rows the runs never write (the dense rows) keep a zero second-half sum
+    // rows the runs never write (the long rows) keep a zero second-half sum
     if (st == PF_OK) st = pfk_fill_zero(p->half_part, b_half, stream);
     if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
+    if (st == PF_OK && lng) {
+        // deal: the tiles ordered by their first column, XCD k taking the k-th eighth
+        st = pfk_memcpy_h2d(p->long_tiles, lt.data(), lt.size() * 4, stream);
+        if (st == PF_OK) st = pfk_memcpy_h2d(p->long_row_tiles, row_tiles.data(), row_tiles.size() * 4, stream);
+        // first nnz of each tile into the deal slots, their columns into the partial slots (both overwritten below)
+        int *d_first = p->long_deal, *d_cols = static_cast<int *>(part);
+        if (st == PF_OK) st = pfk_memcpy_h2d(d_first, first.data(), first.size() * 4, stream);
+        if (st == PF_OK) st = pfk_gather_cols(d_col, p->nnz, d_first, (int)nlt, d_cols, stream);
+        std::vector<int> fc((size_t)nlt), deal((size_t)nlt);
+        if (st == PF_OK) st = pfk_memcpy_d2h(fc.data(), d_cols, fc.size() * 4, stream);
+        if (st == PF_OK) st = pfk_stream_sync(stream);
+        if (st == PF_OK) {
+            for (long long t = 0; t < nlt; ++t) deal[(size_t)t] = (int)t;
+            std::stable_sort(deal.begin(), deal.end(), [&](int x, int y) { return fc[(size_t)x] < fc[(size_t)y]; });
+            st = pfk_memcpy_h2d(p->long_deal, deal.data(), deal.size() * 4, stream);
+        }
+    }
     if (st == PF_OK) st = pfk_stream_sync(stream);
     if (st != PF_OK) return from_kernel_layer(st, "hybrid tables");
     p->hybrid = true;
     p->info.hybrid = 1;
     p->info.dense_rows = nd;
+    p->info.long_tiles = (int)nlt;
     return PF_OK;
 }
 
@@ -916,10 +989,11 @@ int pf_plan_set_hybrid(pf_plan *plan, int hybrid)
 {
     if (!plan || (hybrid != 0 && hybrid != 1)) return fail(PF_ERR_INVALID, "hybrid must be 0 or 1");
     if (hybrid && !plan->ws_hyb)
-        return fail(PF_ERR_UNSUPPORTED, "this plan has no hybrid tables (no dense rows with sorted columns)");
+        return fail(PF_ERR_UNSUPPORTED, "this plan has no hybrid tables (its rows over 256 nnz are not summed apart)");
     plan->hybrid = hybrid != 0;
     plan->info.hybrid = hybrid;
     plan->info.x_halves = hybrid ? (plan->x_halves ? 1 : 0) : plan->info.x_halves;
+    plan->info.long_tiles = hybrid && plan->long_mode ? plan->n_long_tiles : 0;
     return PF_OK;
 }
 
@@ -1019,6 +1093,16 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         a.x_halves = plan->x_halves ? 1 : 0;
         a.half_part = plan->half_part;
         a.half_part_bytes = plan->half_part_bytes;
+        a.long_mode = plan->long_mode ? 1 : 0;
+        a.n_long_tiles = plan->n_long_tiles;
+        a.long_tiles = plan->long_tiles;
+        a.long_deal = plan->long_deal;
+        a.long_row_tiles = plan->long_row_tiles;
+        a.long_part = plan->long_part;
+        a.long_tiles_bytes = plan->long_tiles_bytes;
+        a.long_deal_bytes = plan->long_deal_bytes;
+        a.long_row_tiles_bytes = plan->long_row_tiles_bytes;
+        a.long_part_bytes = plan->long_part_bytes;
         a.map_ready = (plan->remember_rows && plan->hyb_map_ready) ? 1 : 0;
         PF_TRY(pfk_spmv_hybrid(dt, &a, stream), "hybrid kernels");
         if (plan->remember_rows) plan->hyb_map_ready = true;  // later calls read what this one recorded

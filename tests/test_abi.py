@@ -297,3 +297,39 @@ def test_plan_info_layout_has_ladder():
     s = pf.RowStats(m=1000, nnz=5000, max_row_len=7, min_row_len=3)
     assert pf.select(s, "f64", "prefree").ladder == 3
     assert pf.select(s, "f64", "flat").ladder == 0
+
+
+def _hyb_args(**kw):
+    fake = 0x30000
+    nd, nl, R = 3, 20, 5
+    a = dict(row_ptr=fake, col=fake, val=fake, x=fake, y=fake, m=1000, n=1000, nnz=100 * 1024, tile=1024,
+             ntiles=10, err_flag=fake, dense_rows=fake, n_dense=nd, n_runs=R - 1, runs=fake, runs_bytes=5 * R * 4,
+             long_mode=1, n_long_tiles=nl, long_tiles=fake, long_deal=fake, long_row_tiles=fake, long_part=fake,
+             long_tiles_bytes=nl * 16, long_deal_bytes=nl * 4, long_row_tiles_bytes=(nd + 1) * 4,
+             long_part_bytes=nl * 8)
+    a.update(kw)
+    return pf.SpmvArgs(**a)
+
+
+@pytest.mark.parametrize("field,value,what", [("long_tiles_bytes", 20 * 16 - 1, b"long-row tiles"),
+                                              ("long_deal_bytes", 76, b"long-row tile deal"),
+                                              ("long_row_tiles_bytes", 12, b"long-row tile index"),
+                                              ("long_part_bytes", 20 * 4, b"long-row partial sums"),
+                                              ("long_deal", None, b"missing tables"),
+                                              ("n_long_tiles", 0, b"missing tables")])
+def test_hybrid_long_mode_tables_checked(field, value, what):
+    # pfk_spmv_hybrid in long mode refuses a short or missing long-row table before any launch
+    K = pf.klib()
+    K.pfk_spmv_hybrid.argtypes = [ctypes.c_int, ctypes.POINTER(pf.SpmvArgs), ctypes.c_void_p]
+    a = _hyb_args(**{field: value})
+    assert K.pfk_spmv_hybrid(pf.F64, ctypes.byref(a), None) == 1
+    assert what in K.pfk_last_error()
+
+
+def test_gather_cols_rejects_bad_arguments():
+    K = pf.klib()
+    K.pfk_gather_cols.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    assert K.pfk_gather_cols(None, 10, 0x1000, 4, 0x1000, None) == 1
+    assert K.pfk_gather_cols(0x1000, 10, 0x1000, -1, 0x1000, None) == 1
+    assert K.pfk_gather_cols(0x1000, 10, 0x1000, 0, 0x1000, None) == 0  # nothing to gather: no launch

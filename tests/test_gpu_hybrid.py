@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 def _lengths(pattern, rng, dense_len=(9000, 30000), short=(0, 60)):
     out = []
     for p in pattern:
-        if p == "D":
+        if p in ("D", "L"):  # a dense row, or a long row in the long-mode shapes
             out.append(int(rng.integers(*dense_len)))
         elif p == "E":
             out.append(0)
@@ -193,3 +193,117 @@ def test_full_c5_plan_choice():
     y, info = gpu_spmv(rp, col, v["f64"], x, "auto")
     assert info["hybrid"] == 1 and info["x_halves"] == 1 and info["dense_rows"] == 1000
     assert_parity(rp, col, v["f64"], x, y, "f64", what="C5 hybrid")
+
+
+# ---- long mode: long rows that are not all dense, cut into tiles dealt to the XCDs by their first column ----
+
+LONG_SHAPES = {
+    "long_mix": "200 L 300 L L 50 L 10",
+    "long_first_and_last": "L 500 L 700 L",
+    "only_long": "L L L L",
+    "long_with_empty_runs": "E E L E L E E 80 L",
+}
+
+
+def _long_case(name, dtype, seed=31, sorted_cols=True):
+    # x over one XCD's 4 MB L2 (long mode needs it); long rows of 300-6000 nnz (about 3000 on average,
+    # so each holds a 1024-nnz tile or more on average), short rows of 0-60 nnz
+    rng = np.random.default_rng(seed)
+    n = 600000 if dtype == "f64" else 1100000
+    lengths = _lengths(LONG_SHAPES[name].split(), rng, dense_len=(300, 6000))
+    rp, col = csr_from_lengths(lengths, n, rng, sorted_cols=sorted_cols)
+    return rp, col, n
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("name", sorted(LONG_SHAPES))
+def test_hybrid_long_mode_shapes(name, dtype):
+    rp, col, n = _long_case(name, dtype)
+    lens = np.diff(rp)
+    rng = np.random.default_rng(2)
+    kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
+    y, info = gpu_spmv(rp, col, kv, kx, "flat", dtype=dtype)
+    n_long = int(np.sum(lens > 256))
+    want_tiles = int(sum(-(-(rp[r + 1] - (rp[r] & ~63)) // 1024) for r in np.flatnonzero(lens > 256)))
+    assert info["hybrid"] == 1 and info["dense_rows"] == n_long and info["long_tiles"] == want_tiles, info
+    assert info["x_halves"] == 1
+    assert_parity(rp, col, kv, kx, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"{name}/kat")
+    val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+    x = rng.uniform(-1, 1, n).astype(NP[dtype])
+    y, _ = gpu_spmv(rp, col, val, x, "flat", dtype=dtype)
+    assert_parity(rp, col, val, x, y, dtype, what=f"{name}/random")
+    y, info = gpu_spmv(rp, col, val, x, "flat", dtype=dtype, x_halves=False)
+    assert info["x_halves"] == 0
+    assert_parity(rp, col, val, x, y, dtype, what=f"{name}/random/no halves")
+
+
+def test_hybrid_long_mode_unsorted_columns():
+    # long mode needs no sorted columns (only the XCD deal's locality does)
+    rp, col, n = _long_case("long_mix", "f64", seed=33, sorted_cols=False)
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["hybrid"] == 1 and info["long_tiles"] > 0
+    assert_parity(rp, col, val, x, y, "f64", exact=True, what="long/unsorted")
+
+
+def test_hybrid_long_mode_switch_and_search():
+    rp, col, n = _long_case("long_mix", "f64", seed=35)
+    rng = np.random.default_rng(36)
+    val = rng.uniform(-1, 1, len(col))
+    x = rng.uniform(-1, 1, n)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    m = len(rp) - 1
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    outs = {}
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "flat") as p:
+        assert p.info.hybrid == 1 and p.info.long_tiles > 0
+        for label, setup in (("first", None), ("memo", None), ("split", lambda: p.set_hybrid(False)),
+                             ("back", lambda: p.set_hybrid(True)), ("search", lambda: p.set_remember_rows(False)),
+                             ("memo2", lambda: p.set_remember_rows(True))):
+            if setup:
+                setup()
+            y.fill_(float("nan"))
+            p.execute(d_rp, d_col, d_val, d_x, y)
+            p.check()
+            outs[label] = y.cpu().numpy()
+        assert p.info.long_tiles > 0
+    for label in ("memo", "back", "search", "memo2"):
+        assert np.array_equal(outs[label], outs["first"]), label
+    assert_parity(rp, col, val, x, outs["first"], "f64", what="long hybrid")
+    assert_parity(rp, col, val, x, outs["split"], "f64", what="long split-row")
+
+
+def test_hybrid_long_mode_special_values():
+    rp, col, n = _long_case("long_first_and_last", "f64", seed=37)
+    rng = np.random.default_rng(38)
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    for arr in (val, x):
+        idx = rng.choice(len(arr), size=max(1, len(arr) // 700), replace=False)
+        arr[idx] = rng.choice([np.nan, np.inf, -np.inf], size=len(idx))
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["long_tiles"] > 0
+    ref = oracle.spmv_serial(rp, col, val, x)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(y[ok], ref[ok])
+
+
+def test_hybrid_long_mode_refused_below_a_tile_per_row():
+    # long rows of 257-600 nnz (under a 1024-nnz tile on average): the plan stays split-row
+    rng = np.random.default_rng(39)
+    lengths = _lengths("200 L 300 L L 50 L".split(), rng, dense_len=(257, 600))
+    rp, col = csr_from_lengths(lengths, 600000, rng)
+    val, x = oracle.initvec(len(col)), oracle.initvec(600000)
+    y, info = gpu_spmv(rp, col, val, x, "flat")
+    assert info["hybrid"] == 0
+    assert_parity(rp, col, val, x, y, "f64", exact=True, what="short long rows")
+
+
+def test_full_c3_plan_choice():
+    # C3 as bench.py measures it: long mode (4442 long rows, most far below a dense row) with x halves
+    rp, col, v = pf.synth_csr(3, seed=1, dtypes=("f64",))
+    x = pf.synth_x(3, len(rp) - 1, seed=1)["f64"]
+    y, info = gpu_spmv(rp, col, v["f64"], x, "auto")
+    assert info["hybrid"] == 1 and info["x_halves"] == 1 and info["long_tiles"] > 0
+    assert info["dense_rows"] == int(np.sum(np.diff(rp) > 256))
+    assert_parity(rp, col, v["f64"], x, y, "f64", what="C3 long mode")
