@@ -74,7 +74,7 @@ def kernel_name(info):
     """The dominant kernel of a plan's step (prefree-public_amd/csrc/prefree_kernels.hip)."""
     v = info["variant_name"]
     if info.get("hybrid"):
-        return "k_dense + k_rows (runs)"
+        return "k_long + k_rows (runs)" if info.get("long_tiles") else "k_dense + k_rows (runs)"
     if v == "adaptive":
         return "k_wave"
     if v == "prefree":
@@ -269,7 +269,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
     gbs = bytes_eff / (ev_ms * 1e6)
     key = f"C{cfg}-{dt}-{info['variant_name']}-{info['tile']}" + (
         f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
-        "-rows" if info["row_aligned"] else "") + ("-hybrid" if info["hybrid"] else "")
+        "-rows" if info["row_aligned"] else "") + (("-long" if info["long_tiles"] else "-hybrid") if info["hybrid"] else "")
     traffic = traffic_from_profiles(key)
     rec = {
         "workload": WORKLOADS[cfg] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
@@ -282,6 +282,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         "split_row_combine": bool(info["needs_fixup"]) and not info["hybrid"], "plan_ms": round(t_plan, 3),
         "ladder": info["ladder"] if info["variant_name"] == "prefree" else None,
         "hybrid": bool(info["hybrid"]), "dense_rows": info["dense_rows"] if info["hybrid"] else None,
+        "long_tiles": info["long_tiles"] if info["hybrid"] and info["long_tiles"] else None,
         "x_halves": bool(info["x_halves"]) if info["hybrid"] else None,
         "tuning_table": os.path.relpath(os.path.realpath(pf.tuning_table()), REPO) if pf.tuning_table() else None,
         "steps": steps, "warmup": warmup,
@@ -297,8 +298,12 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
                      "launch_ms": round(ev_ms, 6), "algorithmic_bytes": bytes_eff,
                      "traffic_gbps": round(traffic / (ev_ms * 1e6), 1) if traffic else None,
                      "traffic_key": key,
-                     "note": ("step = k_rows over the runs of short rows + k_dense over the dense rows' x windows "
-                              "+ k_dense_sum; launch_ms covers all three" if info["hybrid"] else
+                     "note": ("step = k_rows over the runs of short rows + k_long over the long rows' tiles "
+                              "+ k_long_sum (+ k_rows_halves_add with x halves); launch_ms covers them all"
+                              if info["hybrid"] and info["long_tiles"] else
+                              "step = k_rows over the runs of short rows + k_dense over the dense rows' x windows "
+                              "+ k_dense_sum (+ k_rows_halves_add with x halves); launch_ms covers them all"
+                              if info["hybrid"] else
                               "step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},
     }
@@ -569,7 +574,7 @@ def main():
                  f"{h['cfg']}: {h['values']}"),
         "config": {k: h[k] for k in ("workload", "cfg", "rows", "cols", "nnz", "seed", "variant", "tile", "tiles",
                                      "run_tiles", "row_aligned", "x_windows", "xcd_chunk_nnz", "split_row_combine",
-                                     "hybrid", "dense_rows", "x_halves", "plan_ms", "tuning_table")},
+                                     "hybrid", "dense_rows", "long_tiles", "x_halves", "plan_ms", "tuning_table")},
         "gbps_effective": h["gbps_effective"],
         "pct_peak_hbm": h["pct_peak_hbm"],
         "bytes_model": h["bytes_model"],
