@@ -656,7 +656,8 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     }
     runs[(size_t)nruns] = (int)tiles;  // 0 when every row is long: only the long-row kernels run
     // Long mode: each long row in tiles of PFK_LONG_TILE nnz from its first nnz rounded down to 64.
-    std::vector<int> lt, row_tiles((size_t)nd + 1, 0), first;
+    // host arrays copied to the device stay alive until the stream is synchronised below
+    std::vector<int> lt, row_tiles((size_t)nd + 1, 0), first, fc, deal;
     if (lng) {
         for (int i = 0; i < nd; ++i) {
             row_tiles[(size_t)i] = (int)(lt.size() / 4);
@@ -732,7 +733,8 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
         int *d_first = p->long_deal, *d_cols = static_cast<int *>(part);
         if (st == PF_OK) st = pfk_memcpy_h2d(d_first, first.data(), first.size() * 4, stream);
         if (st == PF_OK) st = pfk_gather_cols(d_col, p->nnz, d_first, (int)nlt, d_cols, stream);
-        std::vector<int> fc((size_t)nlt), deal((size_t)nlt);
+        fc.resize((size_t)nlt);
+        deal.resize((size_t)nlt);
         if (st == PF_OK) st = pfk_memcpy_d2h(fc.data(), d_cols, fc.size() * 4, stream);
         if (st == PF_OK) st = pfk_stream_sync(stream);
         if (st == PF_OK) {
