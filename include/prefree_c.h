@@ -69,6 +69,7 @@ typedef struct pf_row_stats {
     long long n_bad_cols;     /* col[j] outside [0,n); -1 when columns were not checked */
     long long hist_log2[33];  /* [0]: empty rows; [k]: rows with 2^(k-1) <= len < 2^k */
     long long n_long_rows;    /* rows longer than 256 nnz (the longest a row-aligned tile takes) */
+    long long max_short_row_len; /* longest row of at most 256 nnz */
 } pf_row_stats;
 
 /* Launch configuration chosen for a matrix. */

@@ -103,6 +103,11 @@ typedef struct pfk_spmv_args {
     const int *long_row_tiles; /* [n_dense + 1] first tile of each long row; the last = n_long_tiles */
     void *long_part;         /* [n_long_tiles] partial sums, PFK_SLOT_BYTES(dtype) each */
     size_t long_tiles_bytes, long_deal_bytes, long_row_tiles_bytes, long_part_bytes;
+    int ovf_cap;             /* row-aligned FLAT tiles (and hybrid runs): an upper bound on the length of any row
+                                they hold; 0 = unknown.  When it is at most 64 and the rows are not in the
+                                short-row mode (under 4 nnz per row on average), the last row's overflow past a
+                                tile's nominal range is loaded with the range, and a tile whose overflow exceeds
+                                the bound sets the error flag. */
 } pfk_spmv_args;
 
 /* nnz per long-row tile of a hybrid plan in long mode. */

@@ -46,7 +46,8 @@ class RowStats(ctypes.Structure):
                 ("min_row_len", ctypes.c_longlong), ("n_empty_rows", ctypes.c_longlong),
                 ("n_decreasing", ctypes.c_longlong), ("row_ptr_first", ctypes.c_longlong),
                 ("row_ptr_last", ctypes.c_longlong), ("n_bad_cols", ctypes.c_longlong),
-                ("hist_log2", ctypes.c_longlong * 33), ("n_long_rows", ctypes.c_longlong)]
+                ("hist_log2", ctypes.c_longlong * 33), ("n_long_rows", ctypes.c_longlong),
+                ("max_short_row_len", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_ if k != "hist_log2"}
@@ -106,7 +107,7 @@ class SpmvArgs(ctypes.Structure):
                 ("long_tiles", ctypes.c_void_p), ("long_deal", ctypes.c_void_p), ("long_row_tiles", ctypes.c_void_p),
                 ("long_part", ctypes.c_void_p), ("long_tiles_bytes", ctypes.c_size_t),
                 ("long_deal_bytes", ctypes.c_size_t), ("long_row_tiles_bytes", ctypes.c_size_t),
-                ("long_part_bytes", ctypes.c_size_t)]
+                ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int)]
 
 
 _lib = None

@@ -106,6 +106,7 @@ struct Args {
     int *__restrict__ sched;      // split-row FLAT x-window schedule (see k_flat), or null
     long long sched_cap;          // tiles per XCD list
     T *__restrict__ y2;           // x-halves runs: the second half's row sums (k_rows_halves_add adds them to y)
+    int ovf_cap;                  // row-aligned tiles: longest row (at most kAlignRowMax); 0 = unknown
 };
 
 // Long-row threshold of ADAPTIVE for tile size K (keys per wave tile).  A
@@ -1346,10 +1347,12 @@ struct RowsDesc {
 //     also covers some of them (the compiler cannot count loads a wave may
 //     skip).  C4: 310.5 instead of 320.4 us (fp64), 224.3 instead of 227.9
 //     (fp32); on C2 it costs 0.5-0.7 us in fp32 / fp16, hence the split.
+//   preloaded: the overflow col / val (oc, ov) were loaded with the nominal
+//     range, before the rows were known (see k_rows); only its gathers remain.
 template <typename T, int K, bool EARLY_RP, bool HALVES = false>
 __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, const int (&c)[RowsShape<T, K>::kVPT][4],
                                            T (&xv)[RowsShape<T, K>::kVPT][4], T &ov, T &xo,
-                                           int (&rr)[RowsShape<T, K>::kRpPer], int &oc)
+                                           int (&rr)[RowsShape<T, K>::kRpPer], int &oc, bool preloaded)
 {
     using S = RowsShape<T, K>;
     const int tid = threadIdx.x;
@@ -1367,10 +1370,12 @@ __device__ __forceinline__ void rows_loads(const Args<T> &a, const RowsDesc &d, 
     // read only by lanes below nov.
     constexpr bool kSkipOvf = S::kVPT == 1 && !EARLY_RP;
     const bool ovw = !kSkipOvf || wave * kWave < d.nov;  // wave-uniform
-    oc = -1;
-    if (ovw) {
-        oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
-        ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+    if (!preloaded) {
+        oc = -1;
+        if (ovw) {
+            oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
+            ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+        }
     }
     const __amdgpu_buffer_rsrc_t rrp = make_rsrc(a.rp + d.f0, (long long)d.cnt * 4);
     const auto rp_loads = [&] {
@@ -1658,6 +1663,19 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     }
     int c[VPT][4];
     T v[VPT][4];
+    // The overflow of the tile's last row past kb + K is shorter than the
+    // longest row (ovf_cap, from the plan's statistics): when that is known
+    // and at most a wave, wave 0 loads its col / val here with the nominal
+    // range, before the rows are known, so its gathers need not wait for a
+    // load issued after the row search (C5's runs: 835 instead of 842 us per
+    // step, C2 50.7 instead of 51.1).  Longer caps cost more than they save
+    // (C3's runs, rows up to 256: 210 instead of 206 us, the cap re-read by
+    // every tile), and so does the short-row mode, whose loads are ordered
+    // for the row_ptr stream (C4: 307 instead of 299 us).
+    const bool pre = !PRIO && a.ovf_cap > 0 && a.ovf_cap <= kWave;
+    const int ocap = (pre && !last) ? max(0, min(a.ovf_cap, nnz - (kb + K))) : 0;
+    int oc = -1;
+    T ov = T(0);
     if (!DESC) {
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + kb, (long long)(B0 - kb) * 4);
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + kb, val_range_bytes<T>(B0 - kb));
@@ -1670,6 +1688,13 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
             } else {
                 load4(rc, rv, tid + k * kBS, c[k], v[k]);
             }
+        }
+        if (wave == 0 && ocap > 0) {  // wave-uniform
+            const int ob = ocap > 0 ? kb + K : 0;
+            const __amdgpu_buffer_rsrc_t rco = make_rsrc(a.col + ob, (long long)ocap * 4);
+            const __amdgpu_buffer_rsrc_t rvo = make_rsrc(a.val + ob, val_range_bytes<T>(ocap));
+            oc = (int)__builtin_amdgcn_raw_buffer_load_b32(rco, tid * 4, 0, kAuxNt);
+            ov = buf_load(rvo, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
         }
     }
     if (MODE != kFlatMemo) {
@@ -1707,7 +1732,9 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     // bounded by these checks even if row_ptr changed after planning.
     const int ovf = last ? 0 : rpl - (int)ke;  // nnz of the last row past the nominal range
     const bool ok = f >= 0 && l >= f && l <= m && kb >= 0 && B0 >= kb && B0 <= nnz && rpf >= kb && rpf <= rpl &&
-                    rpl <= nnz && (last ? (l == lend && rpl == nend && rpl == B0) : (ovf >= 0 && ovf < kAlignRowMax));
+                    rpl <= nnz &&
+                    (last ? (l == lend && rpl == nend && rpl == B0)
+                          : (ovf >= 0 && ovf < kAlignRowMax && (!pre || ovf <= ocap)));
     if (!ok && tid == 0) atomicOr(a.err, 1);
     const int f0 = ok ? f : 0;
     const int nr = ok ? l - f : 0;
@@ -1725,9 +1752,9 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     const bool second = HALVES && blockIdx.x % kXcds >= kXcds / 2;  // the second half of x, rows into y2
     const int hx = (a.n + 1) / 2;
     const RowsDesc d{kb, B0, f0, nr, nov, A, B, min(nr + 1, S::kRpCap), second ? hx : 0, second ? a.n : hx};
-    T xv[VPT][4], ov, xo;
-    int rr[S::kRpPer], oc;
-    rows_loads<T, K, PRIO, HALVES>(a, d, c, xv, ov, xo, rr, oc);
+    T xv[VPT][4], xo;
+    int rr[S::kRpPer];
+    rows_loads<T, K, PRIO, HALVES>(a, d, c, xv, ov, xo, rr, oc, pre);
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     rows_stage<T, K, HALVES>(d, c, v, xv, oc, ov, xo, rr, s_prod, s_rp);
     lds_sync();
@@ -2827,7 +2854,7 @@ __global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ id
 // Layout of the statistics block (unsigned long long):
 enum StatSlot {
     kStMax = 0, kStMin = 1, kStEmpty = 2, kStDec = 3, kStFirst = 4, kStLast = 5, kStBadCol = 6,
-    kStHist = 7, kStOverAlign = 40, kStCount = 44
+    kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStCount = 44
 };
 
 __global__ void k_stats_init(unsigned long long *out)
@@ -2841,12 +2868,12 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
                                                    unsigned long long *__restrict__ out)
 {
     __shared__ unsigned int s_hist[33];
-    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over;
+    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short;
     const int tid = threadIdx.x;
     if (tid < 33) s_hist[tid] = 0;
-    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; }
+    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; }
     __syncthreads();
-    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0;
+    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0, lshort = 0;
     for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
         int len = rp[r + 1] - rp[r];
         if (len < 0) { ++ldec; len = 0; }
@@ -2855,6 +2882,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         lmin = min(lmin, u);
         lempty += (u == 0);
         lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
+        if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
         atomicAdd(&s_hist[u == 0 ? 0 : 32 - __clz(u)], 1u);
     }
     atomicMax(&s_max, lmax);
@@ -2862,6 +2890,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     atomicAdd(&s_empty, lempty);
     atomicAdd(&s_dec, ldec);
     atomicAdd(&s_over, lover);
+    atomicMax(&s_short, lshort);
     __syncthreads();
     if (tid < 33 && s_hist[tid]) atomicAdd(out + kStHist + tid, (unsigned long long)s_hist[tid]);
     if (tid == 0) {
@@ -2870,6 +2899,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         atomicAdd(out + kStEmpty, (unsigned long long)s_empty);
         atomicAdd(out + kStDec, (unsigned long long)s_dec);
         atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
+        atomicMax(out + kStMaxShort, (unsigned long long)s_short);
         if (blockIdx.x == 0) {
             out[kStFirst] = (unsigned long long)(long long)rp[0];
             out[kStLast] = (unsigned long long)(long long)rp[m];
@@ -2992,6 +3022,7 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.sched = a->sched;
     r.sched_cap = a->sched_cap;
     r.y2 = static_cast<T *>(a->half_part);
+    r.ovf_cap = a->ovf_cap;
     return r;
 }
 

@@ -836,6 +836,7 @@ int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int
     out->n_bad_cols = (d_col && nnz > 0) ? (long long)h[6] : (nnz > 0 ? -1 : 0);
     for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
     out->n_long_rows = (long long)h[40];
+    out->max_short_row_len = (long long)h[41];
     return PF_OK;
 }
 
@@ -1042,7 +1043,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     if (!d_row_ptr || !d_y || (plan->nnz > 0 && (!d_col || !d_val || !d_x)))
         return fail(PF_ERR_INVALID, "NULL matrix or vector pointer");
     if (!aligned16(d_col) || !aligned16(d_val)) return fail(PF_ERR_ALIGN, "col/val not 16-byte aligned");
-    pfk_spmv_args a;
+    pfk_spmv_args a{};
     a.row_ptr = d_row_ptr;
     a.col = d_col;
     a.val = d_val;
@@ -1072,6 +1073,9 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.owner_bytes = plan->owner_bytes;
     a.row_map_bytes = plan->row_map_bytes;
     a.sched_bytes = plan->sched_bytes;
+    // no row of a row-aligned tile is longer than this (longer rows take other plans), so the tile kernel can
+    // load a tile's overflow with its nominal range
+    a.ovf_cap = plan->info.row_aligned ? (int)std::min<long long>(PFK_ALIGN_ROW_MAX, plan->stats.max_row_len) : 0;
     const int dt = plan->info.dtype;
     if (plan->hybrid) {
         a.ntiles = plan->run_tiles;
@@ -1106,6 +1110,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         a.long_row_tiles_bytes = plan->long_row_tiles_bytes;
         a.long_part_bytes = plan->long_part_bytes;
         a.map_ready = (plan->remember_rows && plan->hyb_map_ready) ? 1 : 0;
+        a.ovf_cap = (int)std::min<long long>(PFK_ALIGN_ROW_MAX, plan->stats.max_short_row_len);  // the runs' rows
         PF_TRY(pfk_spmv_hybrid(dt, &a, stream), "hybrid kernels");
         if (plan->remember_rows) plan->hyb_map_ready = true;  // later calls read what this one recorded
         return PF_OK;

@@ -369,23 +369,27 @@ def test_malformed_csr_rejected_at_planning():
     assert e.value.status == 6
 
 
+@pytest.mark.parametrize("long_row", [400, 200])
 @pytest.mark.parametrize("tile", [1024, 2048])
-def test_kernel_error_flag_on_changed_row_ptr(tile):
-    # A row-aligned FLAT plan accepts rows of at most 256 nnz.  A different but
-    # valid row_ptr (same m and nnz, monotone, row 0 at 0, row m at nnz, every
-    # column in range) with one row of 400 nnz makes a tile's last row overflow
-    # it: the search sets the plan's error flag (every access stays clamped to
-    # the tile), pf_plan_check reports PF_ERR_KERNEL once and clears the flag,
-    # and the next call on the planned row_ptr is clean and exact.
+def test_kernel_error_flag_on_changed_row_ptr(tile, long_row):
+    # A row-aligned FLAT plan accepts rows of at most 256 nnz, and loads a
+    # tile's overflow past its nominal range for rows no longer than the
+    # planned matrix's longest (5 here).  A different but valid row_ptr (same
+    # m and nnz, monotone, row 0 at 0, row m at nnz, every column in range)
+    # with one row of 400 nnz (past 256) or 200 nnz (past the planned 5) makes
+    # a tile's last row overflow it by 300 or 100: the search sets the plan's
+    # error flag (every access stays clamped to the tile), pf_plan_check
+    # reports PF_ERR_KERNEL once and clears the flag, and the next call on the
+    # planned row_ptr is clean and exact.
     import torch
 
     m, n = 4000, 4000
     rng = np.random.default_rng(tile)
     rp, col = csr_from_lengths([5] * m, n, rng)
     lengths = np.full(m, 5)
-    r = tile - 20                   # starts at 5r = 5 tile - 100: runs 300 nnz into the next tile
-    lengths[r] = 400
-    lengths[r + 1:r + 1 + 395] = 4  # nnz unchanged
+    r = tile - 20                   # starts at 5r = 5 tile - 100: runs long_row - 100 nnz into the next tile
+    lengths[r] = long_row
+    lengths[r + 1:r + 1 + long_row - 5] = 4  # nnz unchanged
     assert lengths.sum() == 5 * m
     rp_bad = np.zeros(m + 1, dtype=np.int32)
     np.cumsum(lengths, out=rp_bad[1:])
