@@ -70,6 +70,9 @@ typedef struct pf_row_stats {
     long long hist_log2[33];  /* [0]: empty rows; [k]: rows with 2^(k-1) <= len < 2^k */
     long long n_long_rows;    /* rows longer than 256 nnz (the longest a row-aligned tile takes) */
     long long max_short_row_len; /* longest row of at most 256 nnz */
+    long long guess_dev;      /* largest |r - row_ptr[r] * m / nnz| over the rows, rounded up: how far a row
+                                 lies from where the mean density puts it (sizes the row searches' first
+                                 probe round) */
 } pf_row_stats;
 
 /* Launch configuration chosen for a matrix. */
@@ -78,7 +81,8 @@ typedef struct pf_plan_info {
     int dtype;            /* pf_dtype */
     int tile;             /* keys per tile (ADAPTIVE: rows+nnz, FLAT/PREFREE: nnz) */
     int long_row_min;     /* ADAPTIVE: rows longer than this are split across tiles */
-    int guess_spread;     /* row search: spacing of the interpolated first probe round, 0 = none */
+    int guess_spread;     /* row search: spacing of the interpolated first probe round (the smallest power of
+                             two, at most 64, whose 64 probes cover guess_dev; rows of at most 64 nnz), 0 = none */
     int needs_fixup;      /* 1 when split rows need the combine kernel */
     int run_tiles;        /* ADAPTIVE: consecutive tiles walked by one wave64 */
     int keep_cached;      /* ADAPTIVE: 1 = col/val read with ordinary loads (the matrix fits the

@@ -47,7 +47,7 @@ class RowStats(ctypes.Structure):
                 ("n_decreasing", ctypes.c_longlong), ("row_ptr_first", ctypes.c_longlong),
                 ("row_ptr_last", ctypes.c_longlong), ("n_bad_cols", ctypes.c_longlong),
                 ("hist_log2", ctypes.c_longlong * 33), ("n_long_rows", ctypes.c_longlong),
-                ("max_short_row_len", ctypes.c_longlong)]
+                ("max_short_row_len", ctypes.c_longlong), ("guess_dev", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_ if k != "hist_log2"}

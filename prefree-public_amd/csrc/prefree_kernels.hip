@@ -1570,6 +1570,106 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
     }
 }
 
+// Row search of a row-aligned tile (the row holding nnz v), in two parts so
+// that the first probe round can be issued ahead of the tile's col / val
+// loads: a wave's vector loads complete in issue order, so a probe issued
+// after them would wait for them.  Once the bracket holds at most kClose
+// rows, the closing round reads the row bounds after its start with one
+// scalar load, which completes on a counter of its own.  Same result as
+// wave_search_lt_next.
+constexpr int kClose = 16;  // row bounds read by the closing round of a row search
+
+struct RowProbe {
+    int guess;
+    int k;       // row_ptr[guess + (lane - 32) * spread] for a valid probe
+    bool valid;  // the probe lies inside (0, m)
+};
+
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ RowProbe row_probe_issue(const int *__restrict__ rp, int m, uint32_t v, int nnz,
+                                                    int spread, int lane)
+{
+    RowProbe p;
+    // the row at the matrix's mean density (a hint: any value gives the same result)
+    const double g = nnz > 0 ? (double)v * ((double)m / (double)nnz) : 0.0;
+    p.guess = uni((int)fmin(g, (double)(m > 0 ? m - 1 : 0)));
+    const long long q = (long long)p.guess + (long long)(lane - 32) * spread;
+    p.valid = spread > 0 && q > 0 && q < m;
+    p.k = p.valid ? rp[(int)q] : 0;
+    return p;
+}
+
+// Largest r in [0, m) with row_ptr[r] < v (v > 0), and row_ptr[r + 1] in
+// next_key, from the first round's probe.  Whole wave active; wave-uniform
+// (the bracket is kept in scalar registers).
+__device__ __forceinline__ int row_probe_finish(const int *__restrict__ rp, int m, uint32_t v, const RowProbe &p,
+                                                int spread, int lane, int &next_key)
+{
+    typedef const int __attribute__((address_space(4))) cint;
+    // row_ptr + i through the constant address space: the compiler reads it with scalar loads at a uniform
+    // address (row_ptr is read-only in every kernel)
+    const auto srp = [&](int i) {
+        const unsigned long long qa = reinterpret_cast<unsigned long long>(rp + i);
+        // readfirstlane returns int: keep each half unsigned, so the low half is zero-extended
+        const unsigned alo = __builtin_amdgcn_readfirstlane((unsigned)qa);
+        const unsigned ahi = __builtin_amdgcn_readfirstlane((unsigned)(qa >> 32));
+        return (const cint *)(((unsigned long long)ahi << 32) | (unsigned long long)alo);
+    };
+    int lo = 0, hi = m;  // row_ptr[lo] < v; hi == m or row_ptr[hi] >= v
+    // the guess is uniform, but the compiler only knows that of a value read from one lane
+    const int g = uni(p.guess);
+    if (spread > 0) {
+        const uint64_t okm = __ballot(p.valid && (uint32_t)p.k < v);
+        const uint64_t badm = __ballot(p.valid && (uint32_t)p.k >= v);
+        // both are positions of valid probes, inside (0, m)
+        const int nlo = okm ? g + (63 - __clzll(okm) - 32) * spread : lo;
+        const int nhi = badm ? g + (__ffsll((long long)badm) - 1 - 32) * spread : hi;
+        if (nlo < nhi) { lo = nlo; hi = nhi; }
+    }
+    bool have = false;
+    int key = 0;
+    if (spread > 0 && hi - lo == 1 && hi < m) {  // hi is a probe of the first round: its row_ptr is that lane's
+        have = true;
+        key = __builtin_amdgcn_readlane(p.k, (hi - g) / spread + 32);
+    }
+    while (hi - lo > 1) {
+        if (hi - lo <= kClose && lo <= m - kClose) {
+            // closing round: row_ptr[lo + 1 + i] for i < kClose (one 64-byte scalar load), all inside
+            // row_ptr's m + 1 entries; the answer is lo plus the count of those inside the bracket below v
+            const cint *q = srp(lo + 1);
+            int kk[kClose];
+#pragma unroll
+            for (int i = 0; i < kClose; ++i) kk[i] = q[i];
+            const int w = hi - lo - 1;
+            int c = 0;
+#pragma unroll
+            for (int i = 0; i < kClose - 1; ++i) c += (i < w && (uint32_t)kk[i] < v) ? 1 : 0;
+            int nk = kk[0];
+#pragma unroll
+            for (int i = 1; i < kClose; ++i) nk = i == c ? kk[i] : nk;
+            next_key = nk;
+            return lo + c;
+        }
+        const int step = (int)(((long long)hi - lo + 63) >> 6);
+        const long long pp = (long long)lo + (long long)lane * step;
+        const bool probe = lane > 0 && pp < hi;
+        const int k = probe ? rp[(int)pp] : 0;
+        const bool ok = probe && (uint32_t)k < v;
+        const int c = __popcll(__ballot(ok));
+        if (step == 1 && c + 1 < kWave && lo + c + 1 < hi) {
+            have = true;
+            key = __builtin_amdgcn_readlane(k, c + 1);
+        }
+        const int nlo = lo + c * step;  // a probe's position, below hi
+        const long long nhi = (long long)nlo + step;
+        hi = uni(nhi < hi ? (int)nhi : hi);
+        lo = uni(nlo);
+    }
+    next_key = have ? key : *srp(lo + 1);
+    return lo;
+}
+
 // Runs of a hybrid plan: the rows between two dense rows (or a matrix end), each
 // cut into row-aligned tiles of its own; `runs` holds, with R = nruns + 1,
 // tile_begin[R] then row_begin, row_end, nnz_begin, nnz_end [R each].
@@ -1661,6 +1761,12 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         const int2 e0 = mp[t], e1 = mp[t + 1];
         f = e0.x; rpf = e0.y; l = e1.x; rpl = e1.y;
     }
+    // Search modes: waves 2 and 3 issue the first probe round of their row
+    // searches (f, l) ahead of the tile's col / val loads.
+    RowProbe probe{0, 0, false};
+    if (MODE != kFlatMemo && ((wave == 2 && kb != 0) || (wave == 3 && !last)))
+        probe = row_probe_issue(a.rp, m, wave == 2 ? (uint32_t)kb : ke, nnz, a.guess_spread, lane);
+    __builtin_amdgcn_sched_barrier(0);
     int c[VPT][4];
     T v[VPT][4];
     // The overflow of the tile's last row past kb + K is shorter than the
@@ -1701,9 +1807,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         if (wave == 2) {  // f: first row with row_ptr >= kb
             int r = 0;
             const int ff = kb == 0 ? (r = a.rp[0], 0)
-                                   : wave_search_lt_next(a.rp, m, (uint32_t)kb,
-                                                         key_guess<false>((uint32_t)kb, m, nnz), a.guess_spread,
-                                                         lane, r) + 1;
+                                   : row_probe_finish(a.rp, m, (uint32_t)kb, probe, a.guess_spread, lane, r) + 1;
             if (lane == 0) {
                 s_info[0] = ff; s_info[1] = r;
                 if (!RUNS && MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
@@ -1711,8 +1815,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         } else if (wave == 3) {  // l: first row with row_ptr >= ke (the run's or matrix's end for a last tile)
             int r = 0;
             const int ll = last ? (r = a.rp[lend], lend)
-                                : wave_search_lt_next(a.rp, m, ke, key_guess<false>(ke, m, nnz), a.guess_spread, lane,
-                                                      r) + 1;
+                                : row_probe_finish(a.rp, m, ke, probe, a.guess_spread, lane, r) + 1;
             if (lane == 0) {
                 s_info[2] = ll; s_info[3] = r;
                 if (!RUNS && MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
@@ -2854,7 +2957,7 @@ __global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ id
 // Layout of the statistics block (unsigned long long):
 enum StatSlot {
     kStMax = 0, kStMin = 1, kStEmpty = 2, kStDec = 3, kStFirst = 4, kStLast = 5, kStBadCol = 6,
-    kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStCount = 44
+    kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStGuessDev = 42, kStCount = 44
 };
 
 __global__ void k_stats_init(unsigned long long *out)
@@ -2868,13 +2971,19 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
                                                    unsigned long long *__restrict__ out)
 {
     __shared__ unsigned int s_hist[33];
-    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short;
+    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev;
     const int tid = threadIdx.x;
     if (tid < 33) s_hist[tid] = 0;
-    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; }
+    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; s_dev = 0; }
     __syncthreads();
     unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0, lshort = 0;
+    // distance in rows between row r and where the matrix's mean density puts row_ptr[r] (the row
+    // searches' first guess), largest over the rows; 0 when row_ptr[m] is not positive
+    const int total = rp[m];
+    const double per = total > 0 ? (double)m / (double)total : 0.0;
+    double ldev = 0.0;
     for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
+        if (total > 0) ldev = fmax(ldev, fabs((double)r - (double)rp[r] * per));
         int len = rp[r + 1] - rp[r];
         if (len < 0) { ++ldec; len = 0; }
         const unsigned int u = (unsigned int)len;
@@ -2891,6 +3000,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     atomicAdd(&s_dec, ldec);
     atomicAdd(&s_over, lover);
     atomicMax(&s_short, lshort);
+    atomicMax(&s_dev, (unsigned int)fmin(ceil(ldev), 4294967295.0));
     __syncthreads();
     if (tid < 33 && s_hist[tid]) atomicAdd(out + kStHist + tid, (unsigned long long)s_hist[tid]);
     if (tid == 0) {
@@ -2900,6 +3010,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         atomicAdd(out + kStDec, (unsigned long long)s_dec);
         atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
         atomicMax(out + kStMaxShort, (unsigned long long)s_short);
+        atomicMax(out + kStGuessDev, (unsigned long long)s_dev);
         if (blockIdx.x == 0) {
             out[kStFirst] = (unsigned long long)(long long)rp[0];
             out[kStLast] = (unsigned long long)(long long)rp[m];

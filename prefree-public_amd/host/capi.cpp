@@ -371,9 +371,14 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     r.tile = tile;
     const long long m = s.m, nnz = s.nnz;
     // A regular matrix keeps row index and key position nearly proportional:
-    // one interpolated probe round of 64 rows spaced 64 apart brackets the row.
+    // one interpolated probe round of 64 rows brackets the row when their
+    // spacing covers the largest distance of a row from its guess (the row
+    // search's answer lies within guess_dev + 2 rows of the guess).  The
+    // smallest such spacing leaves the fewest rows to the closing round.
     const bool regular = s.max_row_len <= 64;
-    r.guess_spread = regular ? 64 : 0;
+    int spread = 1;
+    while (spread < 64 && 31LL * spread < s.guess_dev + 3) spread *= 2;
+    r.guess_spread = regular ? spread : 0;
     const long long vb = slot_bytes(dtype);
     if (variant == PF_ADAPTIVE) {
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
@@ -837,6 +842,7 @@ int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int
     for (int k = 0; k < 33; ++k) out->hist_log2[k] = (long long)h[7 + k];
     out->n_long_rows = (long long)h[40];
     out->max_short_row_len = (long long)h[41];
+    out->guess_dev = (long long)h[42];
     return PF_OK;
 }
 

@@ -75,6 +75,19 @@ def make_stats(m, nnz, max_len, empty=0):
     return s
 
 
+@pytest.mark.parametrize("dev,spread", [(0, 1), (28, 1), (29, 2), (59, 2), (60, 4), (411, 16), (1981, 64),
+                                        (1982, 64), (10 ** 9, 64)])
+def test_guess_spread_covers_the_deviation(dev, spread):
+    """The first probe round spans guess - 32 s .. guess + 31 s, and a row search's answer lies within
+    guess_dev + 2 rows of the guess: s is the smallest power of two with 31 s >= guess_dev + 3, at most
+    64; rows longer than 64 nnz take no interpolated round."""
+    s = make_stats(1 << 20, 5 << 20, 5)
+    s.guess_dev = dev
+    assert pf.select(s, "f64", "flat").guess_spread == spread
+    s.max_row_len = 65
+    assert pf.select(s, "f64", "flat").guess_spread == 0
+
+
 def run_for(ntiles, resident, cap=16):
     return max(1, min(cap, -(-ntiles // resident)))
 
@@ -82,6 +95,7 @@ def run_for(ntiles, resident, cap=16):
 def test_select_auto_banded_is_flat():
     """C2 shape: short regular rows -> FLAT, 1024 nnz per tile (fp64) / 2048 (fp32)."""
     s = make_stats(4194304, 20963328, 5)
+    s.guess_dev = 410  # C2's rows lie up to 410 rows from where the mean density puts them
     i = pf.select(s, "f64", "auto")
     assert i.variant == pf.FLAT and i.tile == 1024
     assert i.ntiles == -(-20963328 // 1024)
@@ -91,7 +105,7 @@ def test_select_auto_banded_is_flat():
     assert i.chunk_nnz == 1 << 15
     rounds = -(-(-(-i.ntiles // 8)) // 32)
     assert i.grid % 8 == 0 and i.grid >= i.ntiles and i.grid - i.ntiles < 8 * rounds
-    assert i.guess_spread == 64
+    assert i.guess_spread == 16      # 64 probes 16 rows apart cover 410 + 2 rows either side
     i32 = pf.select(s, "f32", "auto")
     assert i32.variant == pf.FLAT and i32.tile == 2048
     wide = pf.select(make_stats(4194304, 4194304 * 40, 60), "f64", "auto")   # rows up to 60 nnz: still FLAT

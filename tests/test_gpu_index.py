@@ -57,7 +57,8 @@ def test_tile_descriptors_match_model(merged, tile, spread, run):
         assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
 
 
-@pytest.mark.parametrize("spread,chunk", [(0, 0), (64, 1 << 15), (1000, 3000)])
+@pytest.mark.parametrize("spread,chunk", [(0, 0), (1, 1 << 15), (2, 3000), (16, 1 << 15), (64, 1 << 15),
+                                          (1000, 3000)])
 @pytest.mark.parametrize("tile", [1024, 2048])
 def test_row_aligned_descriptors_match_model(tile, spread, chunk):
     """Row-aligned FLAT tiles (rows starting in the tile, whole): exact descriptors wherever no

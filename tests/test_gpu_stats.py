@@ -1,0 +1,61 @@
+"""Row statistics on the GPU (pf_row_stats_compute: k_row_stats, k_col_check) against numpy, exactly."""
+import numpy as np
+import pytest
+
+import prefree_amd as pf
+from csr_cases import edge_cases
+from gpu_util import dev
+
+pytestmark = pytest.mark.gpu
+
+ALIGN_MAX = 256  # PFK_ALIGN_ROW_MAX
+
+
+def cases():
+    out = [(name, rp, col, n) for name, rp, col, n in edge_cases()]
+    for cfg, scale in ((1, 0), (2, 300), (3, 60000), (4, 400000), (5, 40000)):
+        rp, col, _ = pf.synth_csr(cfg, seed=4, scale_n=scale, dtypes=())
+        out.append((f"C{cfg}", rp, col, len(rp) - 1))
+    return out
+
+
+def expected(rp, col, n):
+    m, nnz = len(rp) - 1, int(rp[-1])
+    lens = np.diff(rp.astype(np.int64))
+    hist = np.zeros(33, dtype=np.int64)
+    for L in lens:
+        hist[0 if L == 0 else int(L).bit_length()] += 1
+    short = lens[lens <= ALIGN_MAX]
+    dev = 0
+    if m > 0 and nnz > 0:
+        # the kernel's own arithmetic in binary64, no contraction: r - row_ptr[r] * (m / nnz)
+        d = np.abs(np.arange(m, dtype=np.float64) - rp[:m].astype(np.float64) * (m / nnz))
+        dev = int(np.ceil(d.max()))
+    return dict(m=m, nnz=nnz, max_row_len=int(lens.max(initial=0)), min_row_len=int(lens.min()) if m else 0,
+                n_empty_rows=int((lens == 0).sum()), n_decreasing=0, row_ptr_first=int(rp[0]),
+                row_ptr_last=nnz, n_bad_cols=int(((col < 0) | (col >= n)).sum()), n_long_rows=int((lens > ALIGN_MAX).sum()),
+                max_short_row_len=int(short.max(initial=0)), guess_dev=dev, hist=hist)
+
+
+@pytest.mark.parametrize("name,rp,col,n", cases(), ids=[c[0] for c in cases()])
+def test_row_stats_match_numpy(name, rp, col, n):
+    m, nnz = len(rp) - 1, int(rp[-1])
+    s = pf.row_stats(dev(rp), dev(col) if nnz else None, m, n, nnz)
+    want = expected(rp, col, n)
+    for k, v in want.items():
+        if k == "hist":
+            assert list(s.hist_log2) == list(v), name
+        elif k == "min_row_len" and m == 0:
+            continue
+        else:
+            assert getattr(s, k) == v, (name, k, getattr(s, k), v)
+
+
+def test_c2_plan_takes_the_deviation_spread():
+    """C2 at full size: rows up to 410 from the mean-density guess -> 64 probes 16 rows apart."""
+    rp, col, _ = pf.synth_csr(2, seed=1, dtypes=())
+    m, nnz = len(rp) - 1, int(rp[-1])
+    s = pf.row_stats(dev(rp), dev(col), m, m, nnz)
+    assert s.guess_dev == expected(rp, col, m)["guess_dev"] == 410
+    with pf.Plan(dev(rp), dev(col), m, m, nnz, "f64") as p:
+        assert p.info.guess_spread == 16
