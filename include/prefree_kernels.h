@@ -108,6 +108,12 @@ typedef struct pfk_spmv_args {
                                 short-row mode (under 4 nnz per row on average), the last row's overflow past a
                                 tile's nominal range is loaded with the range, and a tile whose overflow exceeds
                                 the bound sets the error flag. */
+    /* Hybrid: a second stream (non-blocking, default priority) and two events made with pfk_event_create_fence.
+       When all three are set, the runs run on aux_stream alongside the dense-row (or long-row) kernels on the
+       caller's stream, which waits for them before the combines.  NULL: one stream, in sequence. */
+    void *aux_stream;
+    void *ev_fork;
+    void *ev_join;
 } pfk_spmv_args;
 
 /* nnz per long-row tile of a hybrid plan in long mode. */
@@ -197,6 +203,7 @@ int pfk_stream_create(void **s);
 int pfk_stream_destroy(void *s);
 int pfk_stream_sync(void *s);
 int pfk_event_create(void **e);
+int pfk_event_create_fence(void **e);  /* an event without timing, for ordering streams */
 int pfk_event_destroy(void *e);
 int pfk_event_record(void *e, void *s);
 int pfk_event_sync(void *e);

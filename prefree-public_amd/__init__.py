@@ -107,7 +107,8 @@ class SpmvArgs(ctypes.Structure):
                 ("long_tiles", ctypes.c_void_p), ("long_deal", ctypes.c_void_p), ("long_row_tiles", ctypes.c_void_p),
                 ("long_part", ctypes.c_void_p), ("long_tiles_bytes", ctypes.c_size_t),
                 ("long_deal_bytes", ctypes.c_size_t), ("long_row_tiles_bytes", ctypes.c_size_t),
-                ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int)]
+                ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int),
+                ("aux_stream", ctypes.c_void_p), ("ev_fork", ctypes.c_void_p), ("ev_join", ctypes.c_void_p)]
 
 
 _lib = None

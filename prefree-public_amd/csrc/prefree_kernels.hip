@@ -3084,6 +3084,12 @@ int hip_fail(hipError_t e, const char *what)
         if (e_ != hipSuccess) return hip_fail(e_, what);         \
     } while (0)
 
+#define PFK_TRY(expr)                                            \
+    do {                                                         \
+        const int rc_ = (expr);                                  \
+        if (rc_ != PF_OK) return rc_;                            \
+    } while (0)
+
 inline hipStream_t S(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline unsigned grid_for(long long work, long long per_block, long long cap)
@@ -3380,30 +3386,54 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     const bool memo = a->map_ready && a->run_map && (a->long_mode || a->dense_seg);
     const bool prio = (long long)a->nnz < 4LL * a->m;
     const dim3 rgrid((unsigned)(r.g8 * kXcds));
+    // Two streams: the runs (bound by the address units and L2 hits) on the
+    // second, the dense rows' stream of col / val (bound by HBM) on the
+    // caller's; they share no output until the combines, which run on the
+    // caller's stream after it waits for the runs.
+    const bool fork = a->aux_stream && a->ev_fork && a->ev_join && a->ntiles > 0;
+    void *rs = stream;
+    if (fork) {
+        PFK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(a->ev_fork), S(stream)));
+        PFK_HIP(hipStreamWaitEvent(S(a->aux_stream), reinterpret_cast<hipEvent_t>(a->ev_fork), 0));
+        rs = a->aux_stream;
+    }
+    const auto join = [&]() -> int {
+        if (!fork) return PF_OK;
+        PFK_HIP(hipEventRecord(reinterpret_cast<hipEvent_t>(a->ev_join), S(a->aux_stream)));
+        PFK_HIP(hipStreamWaitEvent(S(stream), reinterpret_cast<hipEvent_t>(a->ev_join), 0));
+        return PF_OK;
+    };
     if (a->ntiles == 0)  // every row is dense
         ;
     else if (halves && memo)
-        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     else if (halves)
-        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     else if (memo && prio)
-        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, true, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, true, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     else if (memo)
-        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+        hipLaunchKernelGGL((k_rows<T, K, kFlatMemo, false, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     else
-        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true>), rgrid, dim3(kBS), 0, S(stream), r, a->run_map, nullptr, rt);
+        hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     if (a->ntiles > 0) PFK_LAUNCHED("k_rows (runs)");
-    if (a->ntiles > 0 && halves) {
-        hipLaunchKernelGGL((k_rows_halves_add<T>), dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream), r.y, r.y2,
-                           a->m);
-        PFK_LAUNCHED("k_rows_halves_add");
-    }
+    // y = first half + second half over every row (a dense or long row's y is
+    // written after it, by its own combine)
+    const auto halves_add = [&]() -> int {
+        if (a->ntiles > 0 && halves) {
+            hipLaunchKernelGGL((k_rows_halves_add<T>), dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream), r.y,
+                               r.y2, a->m);
+            PFK_LAUNCHED("k_rows_halves_add");
+        }
+        return PF_OK;
+    };
+    if (!fork) PFK_TRY(halves_add());
     if (a->long_mode) {
         const LongArgs L{reinterpret_cast<const int4 *>(a->long_tiles), a->long_deal, a->long_row_tiles,
                          a->dense_rows, a->n_dense, a->n_long_tiles, a->long_part};
         const unsigned lgrid = (unsigned)(kXcds * ((a->n_long_tiles + kXcds - 1) / kXcds));
         hipLaunchKernelGGL((k_long<T>), dim3(lgrid), dim3(kBS), 0, S(stream), r, L);
         PFK_LAUNCHED("k_long");
+        if (fork) { PFK_TRY(join()); PFK_TRY(halves_add()); }
         hipLaunchKernelGGL((k_long_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0,
                            S(stream), r, L);
         PFK_LAUNCHED("k_long_sum");
@@ -3417,6 +3447,7 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     else
         hipLaunchKernelGGL((k_dense<T, kFlatSearch>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense");
+    if (fork) { PFK_TRY(join()); PFK_TRY(halves_add()); }
     hipLaunchKernelGGL((k_dense_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense_sum");
     return PF_OK;
@@ -3784,6 +3815,14 @@ int pfk_event_create(void **e)
 {
     hipEvent_t h;
     PFK_HIP(hipEventCreate(&h));
+    *e = h;
+    return PF_OK;
+}
+
+int pfk_event_create_fence(void **e)
+{
+    hipEvent_t h;
+    PFK_HIP(hipEventCreateWithFlags(&h, hipEventDisableTiming));
     *e = h;
     return PF_OK;
 }

@@ -307,3 +307,47 @@ def test_full_c3_plan_choice():
     assert info["hybrid"] == 1 and info["x_halves"] == 1 and info["long_tiles"] > 0
     assert info["dense_rows"] == int(np.sum(np.diff(rp) > 256))
     assert_parity(rp, col, v["f64"], x, y, "f64", what="C3 long mode")
+
+
+@pytest.mark.parametrize("kind", ["dense", "dense-halves", "long"])
+def test_hybrid_graph_replays_match_eager(kind):
+    # A hybrid plan whose x fits one XCD's L2 (the dense shapes here) runs its runs on a second stream beside
+    # the dense rows' kernel, forked from and joined back to the caller's stream with events; the long shape
+    # (x 4.8 MB) uses one stream.  Captured into a HIP graph on the plan's stream, every replay gives the eager
+    # y bit for bit, with eager calls and synchronisation between the replays.
+    if kind == "long":
+        rp, col, n = _long_case("long_mix", "f64")
+    else:
+        rp, col, n = _case("many_short_runs", seed=41)
+    rng = np.random.default_rng(42)
+    m = len(rp) - 1
+    val = rng.uniform(-1, 1, len(col))
+    x = rng.uniform(-1, 1, n)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        plan = pf.Plan(d_rp, d_col, m, n, len(col), "f64", "flat", stream=s)
+        assert plan.info.hybrid == 1
+        if kind == "dense-halves":
+            plan.set_x_halves(1)
+        assert plan.info.x_halves == (0 if kind == "dense" else 1)
+        plan.execute(d_rp, d_col, d_val, d_x, y, stream=s)     # first call: searches and records
+        s.synchronize()
+        eager = y.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(3):
+                plan.execute(d_rp, d_col, d_val, d_x, y, stream=s)
+        for rep in range(3):
+            y.fill_(float("nan"))
+            g.replay()
+            s.synchronize()
+            assert torch.equal(y, eager), f"replay {rep} differs from the eager result"
+            y.fill_(0.0)
+            plan.execute(d_rp, d_col, d_val, d_x, y, stream=s)
+            s.synchronize()
+            assert torch.equal(y, eager)
+        plan.check(stream=s)
+        plan.close()
+    assert_parity(rp, col, val, x, eager.cpu().numpy(), "f64", what=f"{kind}/graph")
