@@ -6,9 +6,17 @@
 // of row_ptr (device_common.hpp: wave_search_lt) or, from a plan's second call
 // on, by reading the rows its first call found.
 //
-//  * k_rows<T, K, MODE, PRIO>  (PF_FLAT, K = 1024 / 2048 nnz; the default when
-//    no row holds more than 256 nnz)  Tile t owns the rows starting in its nnz
-//    range, whole: one launch per step, no split rows.
+//  * k_rows<T, K, MODE, PRIO, RUNS, HALVES>  (PF_FLAT, K = 1024 / 2048 nnz;
+//    the default when no row holds more than 256 nnz)  Tile t owns the rows
+//    starting in its nnz range, whole: one launch per step, no split rows.
+//    Its search mode splits the row search (row_probe_issue / _finish) so the
+//    first probe round goes out ahead of the tile's loads.  RUNS: the runs of
+//    short rows of a hybrid plan; HALVES: once per half of x.
+//  * k_dense<T, MODE> + k_dense_sum  (hybrid plans, dense mode)  Dense rows by
+//    x windows staged in LDS, a partial per (row, window), added in order.
+//  * k_long<T> + k_long_sum  (hybrid plans, long mode)  Long rows cut into
+//    1024-nnz tiles dealt to the XCDs by first column, partials added in order.
+//  * k_rows_halves_add  y = first half's row sums + second half's.
 //  * k_flat<T, K, MODE>  (PF_FLAT 1024 / 2048, rows longer than 256 nnz)  The
 //    same nnz tiles with rows cut at tile edges; k_fixup combines the pieces.
 //    With the x-window schedule (sched_tile) tiles go to the XCDs by the part
