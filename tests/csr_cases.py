@@ -67,6 +67,10 @@ def edge_cases(seed=7):
     # overflow reaches every wave of the workgroup, not only the first 64 lanes.
     add("rows_of_255", [255] * 160, 3000)
     add("rows_65_to_256", list(rng.integers(65, 257, size=300)), 4000)
+    # Rows of at most 64 nnz (the longest row bounds the overflow a row-aligned tile loads with its nominal
+    # range): overflows of up to 63 nnz, one wave of preloaded slots.
+    add("rows_of_64", [64] * 200, 3000)
+    add("rows_1_to_64", list(rng.integers(1, 65, size=700)), 5000)
     # The same overflows under 4 nnz per row on average (the row-aligned kernel's short-row mode).
     add("sparse_long_rows", list(np.where(rng.random(20000) < 0.02, rng.integers(65, 257, size=20000), 0)), 20000)
     return out
