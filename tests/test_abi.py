@@ -347,3 +347,34 @@ def test_gather_cols_rejects_bad_arguments():
     assert K.pfk_gather_cols(None, 10, 0x1000, 4, 0x1000, None) == 1
     assert K.pfk_gather_cols(0x1000, 10, 0x1000, -1, 0x1000, None) == 1
     assert K.pfk_gather_cols(0x1000, 10, 0x1000, 0, 0x1000, None) == 0  # nothing to gather: no launch
+
+
+STRUCTS = [("pf_row_stats", "RowStats", "prefree_c.h"), ("pf_plan_info", "PlanInfo", "prefree_c.h"),
+           ("pf_tune_result", "TuneResult", "prefree_c.h"), ("pfk_spmv_args", "SpmvArgs", "prefree_kernels.h")]
+
+
+def test_ctypes_mirrors_match_the_c_structs(tmp_path):
+    """Every ctypes mirror in prefree-public_amd/__init__.py has the size, field order and field offsets of its
+    struct in include/*.h, as the C compiler lays it out (a small C program prints sizeof / offsetof)."""
+    inc = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include")
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "prefree_c.h"', '#include "prefree_kernels.h"',
+             "int main(void) {"]
+    for cname, pyname, _ in STRUCTS:
+        lines.append(f'printf("{pyname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _t in getattr(pf, pyname)._fields_:
+            lines.append(f'printf("{pyname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["return 0; }"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", inc, "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {}
+    for line in filter(None, out):
+        py, field, value = line.split()
+        got[(py, field)] = int(value)
+    for _cname, pyname, _ in STRUCTS:
+        cls = getattr(pf, pyname)
+        assert got[(pyname, "sizeof")] == ctypes.sizeof(cls), pyname
+        for fname, _t in cls._fields_:
+            assert got[(pyname, fname)] == getattr(cls, fname).offset, (pyname, fname)
