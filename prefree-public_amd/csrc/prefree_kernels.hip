@@ -1932,6 +1932,63 @@ __device__ __forceinline__ int wave_lower_bound(const int *__restrict__ col, int
     return hi;
 }
 
+// Both bounds of a window's segment in a dense row, lower_bound(v1) and
+// lower_bound(v2) over col[a, b) (sorted), searched side by side: the first
+// round probes 64 positions `spread` apart around each value's place in the
+// row if its columns were spread evenly over [0, n) (c * len / n past a),
+// which for a row of uniform random columns brackets it to `spread` entries;
+// then 64-ary rounds inside the brackets, one load per lane for each search
+// still open.  Whole wave active; the same results as wave_lower_bound.
+__device__ __forceinline__ void wave_lower_bound2(const int *__restrict__ col, int a, int b, int n, int v1, int v2,
+                                                  int lane, int &r1, int &r2)
+{
+    const long long len = (long long)b - a;
+    const int spread = uni((int)max(1.0, ceil(sqrt((double)len) / 16.0)));
+    int lo[2] = {a - 1, a - 1}, hi[2] = {b, b};  // col[lo] < v, col[hi] >= v, both virtual at the ends
+    const int v[2] = {v1, v2};
+    int k[2], g[2];
+    bool valid[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const double place = n > 0 ? (double)v[t] * ((double)len / (double)n) : 0.0;
+        g[t] = uni(a + (int)fmin(fmax(place, 0.0), (double)len));
+        const long long p = (long long)g[t] + (long long)(lane - 32) * spread;
+        valid[t] = p >= a && p < b;
+        k[t] = valid[t] ? col[(int)p] : 0;
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint64_t okm = __ballot(valid[t] && k[t] < v[t]);
+        const uint64_t badm = __ballot(valid[t] && k[t] >= v[t]);
+        // positions of valid probes, inside [a, b)
+        const int nlo = okm ? g[t] + (63 - __clzll(okm) - 32) * spread : lo[t];
+        const int nhi = badm ? g[t] + (__ffsll((long long)badm) - 1 - 32) * spread : hi[t];
+        if (nlo < nhi) { lo[t] = nlo; hi[t] = nhi; }
+    }
+    while (hi[0] - lo[0] > 1 || hi[1] - lo[1] > 1) {
+        int step[2], kk[2];
+        bool pr[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            step[t] = (hi[t] - lo[t] + 63) >> 6;
+            const int pp = lo[t] + lane * step[t];
+            pr[t] = hi[t] - lo[t] > 1 && lane > 0 && pp < hi[t];
+            kk[t] = pr[t] ? col[pp] : 0;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (hi[t] - lo[t] > 1) {  // wave-uniform
+                const int c = __popcll(__ballot(pr[t] && kk[t] < v[t]));
+                const int nlo = lo[t] + c * step[t];
+                hi[t] = uni(min(nlo + step[t], hi[t]));
+                lo[t] = uni(nlo);
+            }
+        }
+    }
+    r1 = hi[0];
+    r2 = hi[1];
+}
+
 // The recorded-bounds call (kFlatMemo): each wave reads the window bounds of
 // all its rows (one load per lane) before the window is staged, and streams
 // its rows' segments as one sequence of batches of U loads per lane, double
@@ -2056,8 +2113,8 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
         const int a0 = min(max(a.rp[r], 0), nnz);
         const int a1 = min(max(a.rp[r + 1], a0), nnz);
         int *sg = d.seg + (long long)i * (d.nwin + 1);
-        const int s = wave_lower_bound(a.col, a0, a1, c0, lane);
-        const int e = w == d.nwin - 1 ? a1 : wave_lower_bound(a.col, s, a1, c0 + W, lane);
+        int s, e;  // (every column of the last window is below c0 + W: its e is a1)
+        wave_lower_bound2(a.col, a0, a1, a.n, c0, c0 + W, lane, s, e);
         if (MODE == kFlatSearch && d.seg && lane == 0) {
             sg[w] = s;
             if (w == d.nwin - 1) sg[d.nwin] = e;
