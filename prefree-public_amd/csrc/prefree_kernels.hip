@@ -1918,99 +1918,21 @@ struct DenseArgs {
     void *__restrict__ part;       // [nd][nwin] partial sums (accumulation type)
 };
 
-// First j in [a, b) with col[j] >= v (b if none); col sorted in [a, b).  One wave.
-__device__ __forceinline__ int wave_lower_bound(const int *__restrict__ col, int a, int b, int v, int lane)
-{
-    int lo = a - 1, hi = b;  // col[lo] < v, col[hi] >= v, both virtual at the ends
-    while (hi - lo > 1) {
-        const int step = (hi - lo + 63) >> 6;
-        const int p = lo + lane * step;
-        const bool ok = lane > 0 && p < hi && col[p] < v;
-        lo += __popcll(__ballot(ok)) * step;
-        hi = min(lo + step, hi);
-    }
-    return hi;
-}
-
-// Both bounds of a window's segment in a dense row, lower_bound(v1) and
-// lower_bound(v2) over col[a, b) (sorted), searched side by side: the first
-// round probes 64 positions `spread` apart around each value's place in the
-// row if its columns were spread evenly over [0, n) (c * len / n past a),
-// which for a row of uniform random columns brackets it to `spread` entries;
-// then 64-ary rounds inside the brackets, one load per lane for each search
-// still open.  Whole wave active; the same results as wave_lower_bound.
-__device__ __forceinline__ void wave_lower_bound2(const int *__restrict__ col, int a, int b, int n, int v1, int v2,
-                                                  int lane, int &r1, int &r2)
-{
-    const long long len = (long long)b - a;
-    const int spread = uni((int)max(1.0, ceil(sqrt((double)len) / 16.0)));
-    int lo[2] = {a - 1, a - 1}, hi[2] = {b, b};  // col[lo] < v, col[hi] >= v, both virtual at the ends
-    const int v[2] = {v1, v2};
-    int k[2], g[2];
-    bool valid[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const double place = n > 0 ? (double)v[t] * ((double)len / (double)n) : 0.0;
-        g[t] = uni(a + (int)fmin(fmax(place, 0.0), (double)len));
-        const long long p = (long long)g[t] + (long long)(lane - 32) * spread;
-        valid[t] = p >= a && p < b;
-        k[t] = valid[t] ? col[(int)p] : 0;
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const uint64_t okm = __ballot(valid[t] && k[t] < v[t]);
-        const uint64_t badm = __ballot(valid[t] && k[t] >= v[t]);
-        // positions of valid probes, inside [a, b)
-        const int nlo = okm ? g[t] + (63 - __clzll(okm) - 32) * spread : lo[t];
-        const int nhi = badm ? g[t] + (__ffsll((long long)badm) - 1 - 32) * spread : hi[t];
-        if (nlo < nhi) { lo[t] = nlo; hi[t] = nhi; }
-    }
-    while (hi[0] - lo[0] > 1 || hi[1] - lo[1] > 1) {
-        int step[2], kk[2];
-        bool pr[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            step[t] = (hi[t] - lo[t] + 63) >> 6;
-            const int pp = lo[t] + lane * step[t];
-            pr[t] = hi[t] - lo[t] > 1 && lane > 0 && pp < hi[t];
-            kk[t] = pr[t] ? col[pp] : 0;
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (hi[t] - lo[t] > 1) {  // wave-uniform
-                const int c = __popcll(__ballot(pr[t] && kk[t] < v[t]));
-                const int nlo = lo[t] + c * step[t];
-                hi[t] = uni(min(nlo + step[t], hi[t]));
-                lo[t] = uni(nlo);
-            }
-        }
-    }
-    r1 = hi[0];
-    r2 = hi[1];
-}
-
-// The recorded-bounds call (kFlatMemo): each wave reads the window bounds of
-// all its rows (one load per lane) before the window is staged, and streams
-// its rows' segments as one sequence of batches of U loads per lane, double
-// buffered: the next batch (of the same row or the next one) is in flight
-// while the current one is summed, so neither a row change nor a row's last
-// partial batch leaves the wave without loads in flight.
+// The segments of a wave's rows in window w, lane k holding [ms, me) of row
+// i0 + kWaves k (k < nk; read by the recorded-bounds call, one load per lane,
+// or found by the call that searches), streamed as one sequence of batches of
+// U loads per lane, double buffered: the next batch (of the same row or the
+// next one) is in flight while the current one is summed, so neither a row
+// change nor a row's last partial batch leaves the wave without loads in
+// flight.  Both calls sum through here, so they give the same sums bit for bit.
 template <typename T>
-__device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const DenseArgs &d, const T *sx, int w,
-                                                    int c0, int i0, int nk)
+__device__ __forceinline__ void dense_rows_stream(const Args<T> &a, const DenseArgs &d, const T *sx, int w, int c0,
+                                                  int i0, int nk, int ms, int me)
 {
     using P = acc_t<T>;
     constexpr int W = DenseShape<T>::kW, U = DenseShape<T>::kU;
     const int lane = threadIdx.x & (kWave - 1);
-    const int nnz = a.nnz;
-    // lane k: the segment [ms, me) of row i0 + kWaves k in window w
-    int ms = 0, me = 0;
-    if (lane < nk) {
-        const int *sg = d.seg + (long long)(i0 + kWaves * lane) * (d.nwin + 1) + w;
-        ms = min(max(sg[0], 0), nnz);
-        me = min(max(sg[1], ms), nnz);
-        if (me == ms) static_cast<P *>(d.part)[(long long)(i0 + kWaves * lane) * d.nwin + w] = P(0);
-    }
+    if (lane < nk && me == ms) static_cast<P *>(d.part)[(long long)(i0 + kWaves * lane) * d.nwin + w] = P(0);
     const uint64_t todo = __ballot(lane < nk && me > ms);
     int cA[U], cB[U];
     T vA[U], vB[U];
@@ -2075,19 +1997,116 @@ __device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const Dens
     }
 }
 
+// The recorded-bounds call: lane k reads the bounds of row i0 + kWaves k.
+template <typename T>
+__device__ __forceinline__ void dense_rows_recorded(const Args<T> &a, const DenseArgs &d, const T *sx, int w,
+                                                    int c0, int i0, int nk)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nnz = a.nnz;
+    int ms = 0, me = 0;
+    if (lane < nk) {
+        const int *sg = d.seg + (long long)(i0 + kWaves * lane) * (d.nwin + 1) + w;
+        ms = min(max(sg[0], 0), nnz);
+        me = min(max(sg[1], ms), nnz);
+    }
+    dense_rows_stream<T>(a, d, sx, w, c0, i0, nk, ms, me);
+}
+
+// One lane's lower_bound(v) over col[a, b) (sorted): a first round of 8
+// probes `sp` apart around `guess`, then 8-ary rounds inside the bracket.
+// Every probe lies in [a, b), and the loop ends for any data (each round
+// leaves at most an eighth of the bracket).
+__device__ __forceinline__ int lane_lower_bound(const int *__restrict__ col, int a, int b, int v, int guess, int sp)
+{
+    int lo = a - 1, hi = b;  // col[lo] < v, col[hi] >= v, both virtual at the ends
+    {
+        int k[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const long long p = (long long)guess + (long long)(i - 4) * sp;
+            k[i] = (p >= a && p < b) ? col[(int)p] : 0;
+        }
+        int nlo = lo, nhi = hi;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const long long p = (long long)guess + (long long)(i - 4) * sp;
+            if (p >= a && p < b) {
+                if (k[i] < v) nlo = max(nlo, (int)p);
+                else nhi = min(nhi, (int)p);
+            }
+        }
+        if (nlo < nhi) { lo = nlo; hi = nhi; }  // (columns out of order: keep the whole row)
+    }
+    while (hi - lo > 1) {
+        const int step = (hi - lo + 7) >> 3;
+        int k[7];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) {
+            const int p = lo + i * step;
+            k[i - 1] = p < hi ? col[p] : 0;
+        }
+        int c = 0;
+#pragma unroll
+        for (int i = 1; i < 8; ++i)
+            c += (lo + i * step < hi && k[i - 1] < v) ? 1 : 0;
+        const int nlo = lo + c * step;
+        hi = min(nlo + step, hi);
+        lo = nlo;
+    }
+    return hi;
+}
+
+// The call that searches (kFlatSearch): lane k finds the segment of row
+// i0 + kWaves k in window w itself, the 32 rows side by side (a row's place
+// for column c guessed as c * len / n past its start, the rows' columns being
+// spread over [0, n)), records it when the plan keeps bounds, and the wave
+// sums the segments exactly as the recorded-bounds call does.
+template <typename T>
+__device__ __forceinline__ void dense_rows_searched(const Args<T> &a, const DenseArgs &d, const T *sx, int w,
+                                                    int c0, int i0, int nk)
+{
+    constexpr int W = DenseShape<T>::kW;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nnz = a.nnz;
+    int ms = 0, me = 0;
+    if (lane < nk) {
+        const int i = i0 + kWaves * lane;
+        const int r = d.rows[i];
+        if (r < 0 || r >= a.m) {  // a table entry that is not a row: an empty segment, reported
+            atomicOr(a.err, 1);
+        } else {
+            const int a0 = min(max(a.rp[r], 0), nnz);
+            const int a1 = min(max(a.rp[r + 1], a0), nnz);
+            const int len = a1 - a0;
+            const int sp = (int)max(1.0, ceil(sqrt((double)len) / 4.0));
+            const auto guess = [&](int v) {
+                const double place = a.n > 0 ? (double)v * ((double)len / (double)a.n) : 0.0;
+                return a0 + (int)fmin(fmax(place, 0.0), (double)max(len - 1, 0));
+            };
+            ms = lane_lower_bound(a.col, a0, a1, c0, guess(c0), sp);
+            me = lane_lower_bound(a.col, a0, a1, c0 + W, guess(c0 + W), sp);
+            if (d.seg) {
+                int *sg = d.seg + (long long)i * (d.nwin + 1);
+                sg[w] = ms;
+                if (w == d.nwin - 1) sg[d.nwin] = me;
+            }
+        }
+    }
+    dense_rows_stream<T>(a, d, sx, w, c0, i0, nk, ms, me);
+}
+
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
 {
-    using P = acc_t<T>;
-    constexpr int W = DenseShape<T>::kW, G = DenseShape<T>::kG, U = DenseShape<T>::kU;
+    constexpr int W = DenseShape<T>::kW, G = DenseShape<T>::kG;
     __shared__ __attribute__((aligned(16))) T sx[W];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int tid = threadIdx.x, wave = tid / kWave;
     const int xcd = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
     const int wper = (d.nwin + kXcds - 1) / kXcds;
     const int w = xcd * wper + q % wper, g = q / wper;
     if (w >= d.nwin || g >= d.ngroups)
         return;
-    const int m = a.m, nnz = a.nnz;
     const int c0 = w * W;
     const int i_end = min(d.nd, (g + 1) * G);
     {  // the window x[c0, c0 + W) into LDS, 16 bytes per lane and load; zeros past n
@@ -2098,50 +2117,13 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
             *reinterpret_cast<u32x4 *>(sx + i * kPer) = __builtin_amdgcn_raw_buffer_load_b128(rx, i * 16, 0, 0);
     }
     lds_sync();
-    if constexpr (MODE == kFlatMemo) {
-        static_assert(G / kWaves <= kWave, "one lane per row of a wave");
-        const int i0 = g * G + wave;
-        dense_rows_recorded<T>(a, d, sx, w, c0, i0, i0 < i_end ? (i_end - i0 + kWaves - 1) / kWaves : 0);
-        return;
-    }
-    for (int i = g * G + wave; i < i_end; i += kWaves) {
-        const int r = d.rows[i];
-        if (r < 0 || r >= m) {  // a table entry that is not a row: skip it, report it
-            if (lane == 0) atomicOr(a.err, 1);
-            continue;
-        }
-        const int a0 = min(max(a.rp[r], 0), nnz);
-        const int a1 = min(max(a.rp[r + 1], a0), nnz);
-        int *sg = d.seg + (long long)i * (d.nwin + 1);
-        int s, e;  // (every column of the last window is below c0 + W: its e is a1)
-        wave_lower_bound2(a.col, a0, a1, a.n, c0, c0 + W, lane, s, e);
-        if (MODE == kFlatSearch && d.seg && lane == 0) {
-            sg[w] = s;
-            if (w == d.nwin - 1) sg[d.nwin] = e;
-        }
-        // the same lanes and order as dense_rows_recorded (batches from s rounded down to 64), so that the
-        // call that searches and the calls that read the bounds give the same sums bit for bit
-        const int sa = s & ~(kWave - 1);
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + sa, (long long)(e - sa) * 4);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + sa, (long long)(e - sa) * (long long)sizeof(T));
-        P acc = P(0);
-        for (int j = 0; j < e - sa; j += kWave * U) {
-            int c[U];
-            T v[U];
-#pragma unroll
-            for (int k = 0; k < U; ++k)
-                load1(rc, rv, j + k * kWave + lane, c[k], v[k]);
-#pragma unroll
-            for (int k = 0; k < U; ++k) {  // no product for slots outside the segment (x may hold inf or NaN)
-                const T xv = sx[(c[k] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
-                const int q = j + k * kWave + lane;
-                if (q >= s - sa && q < e - sa)
-                    acc += P(v[k]) * P(xv);
-            }
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) static_cast<P *>(d.part)[(long long)i * d.nwin + w] = acc;
-    }
+    static_assert(G / kWaves <= kWave, "one lane per row of a wave");
+    const int i0 = g * G + wave;
+    const int nk = i0 < i_end ? (i_end - i0 + kWaves - 1) / kWaves : 0;
+    if constexpr (MODE == kFlatMemo)
+        dense_rows_recorded<T>(a, d, sx, w, c0, i0, nk);
+    else
+        dense_rows_searched<T>(a, d, sx, w, c0, i0, nk);
 }
 
 // y of each dense row from its window partial sums: one wave per row, lane j
