@@ -1588,31 +1588,53 @@ __device__ __forceinline__ void rows_reduce(const Args<T> &a, const RowsDesc &d,
 constexpr int kClose = 16;  // row bounds read by the closing round of a row search
 
 struct RowProbe {
-    int guess;
-    int k;       // row_ptr[guess + (lane - 32) * spread] for a valid probe
-    bool valid;  // the probe lies inside (0, m)
+    int guess, spread;  // the probes: guess + (lane - 32) * spread
+    int lo0, hi0;       // the bracket they refine: row_ptr[lo0] < v; hi0 == m or row_ptr[hi0] >= v
+    int k;              // row_ptr of this lane's probe, when valid
+    bool valid;         // the probe lies inside (lo0, hi0)
 };
 
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+__device__ __forceinline__ RowProbe row_probe_at(const int *__restrict__ rp, int guess, int spread, int lo0, int hi0,
+                                                 int lane)
+{
+    RowProbe p;
+    p.guess = uni(guess);
+    p.spread = uni(spread);
+    p.lo0 = uni(lo0);
+    p.hi0 = uni(hi0);
+    const long long q = (long long)p.guess + (long long)(lane - 32) * p.spread;
+    p.valid = p.spread > 0 && q > p.lo0 && q < p.hi0;
+    p.k = p.valid ? rp[(int)q] : 0;
+    return p;
+}
+
+// Whole matrix: around the row the matrix's mean density gives (a hint: any
+// value gives the same result), `spread` from the plan (0: no probe round).
 __device__ __forceinline__ RowProbe row_probe_issue(const int *__restrict__ rp, int m, uint32_t v, int nnz,
                                                     int spread, int lane)
 {
-    RowProbe p;
-    // the row at the matrix's mean density (a hint: any value gives the same result)
     const double g = nnz > 0 ? (double)v * ((double)m / (double)nnz) : 0.0;
-    p.guess = uni((int)fmin(g, (double)(m > 0 ? m - 1 : 0)));
-    const long long q = (long long)p.guess + (long long)(lane - 32) * spread;
-    p.valid = spread > 0 && q > 0 && q < m;
-    p.k = p.valid ? rp[(int)q] : 0;
-    return p;
+    return row_probe_at(rp, (int)fmin(g, (double)(m > 0 ? m - 1 : 0)), spread, 0, m, lane);
+}
+
+// Inside a run of a hybrid plan, rows [r0, r1): the 63 probes spread evenly
+// over the run.  row_ptr[r0 - 1] (the dense or long row before the run) is
+// below any key of the run's tiles, and row_ptr[r1] (the run's end) at or
+// above it, so the search never leaves the run.
+__device__ __forceinline__ RowProbe row_probe_run(const int *__restrict__ rp, int r0, int r1, int lane)
+{
+    const int lo0 = max(r0 - 1, 0);
+    const int sp = max(1, (r1 - lo0 - 1 + 62) / 63);
+    return row_probe_at(rp, lo0 + 32 * sp, sp, lo0, r1, lane);
 }
 
 // Largest r in [0, m) with row_ptr[r] < v (v > 0), and row_ptr[r + 1] in
 // next_key, from the first round's probe.  Whole wave active; wave-uniform
 // (the bracket is kept in scalar registers).
 __device__ __forceinline__ int row_probe_finish(const int *__restrict__ rp, int m, uint32_t v, const RowProbe &p,
-                                                int spread, int lane, int &next_key)
+                                                int lane, int &next_key)
 {
     typedef const int __attribute__((address_space(4))) cint;
     // row_ptr + i through the constant address space: the compiler reads it with scalar loads at a uniform
@@ -1624,20 +1646,21 @@ __device__ __forceinline__ int row_probe_finish(const int *__restrict__ rp, int 
         const unsigned ahi = __builtin_amdgcn_readfirstlane((unsigned)(qa >> 32));
         return (const cint *)(((unsigned long long)ahi << 32) | (unsigned long long)alo);
     };
-    int lo = 0, hi = m;  // row_ptr[lo] < v; hi == m or row_ptr[hi] >= v
-    // the guess is uniform, but the compiler only knows that of a value read from one lane
-    const int g = uni(p.guess);
+    // the probe's fields are uniform, but the compiler only knows that of values read from one lane
+    const int g = uni(p.guess), spread = uni(p.spread);
+    int lo = uni(p.lo0), hi = uni(p.hi0);  // row_ptr[lo] < v; hi == m or row_ptr[hi] >= v
+    bool hi_probed = false;
     if (spread > 0) {
         const uint64_t okm = __ballot(p.valid && (uint32_t)p.k < v);
         const uint64_t badm = __ballot(p.valid && (uint32_t)p.k >= v);
-        // both are positions of valid probes, inside (0, m)
+        // both are positions of valid probes, inside (lo, hi)
         const int nlo = okm ? g + (63 - __clzll(okm) - 32) * spread : lo;
         const int nhi = badm ? g + (__ffsll((long long)badm) - 1 - 32) * spread : hi;
-        if (nlo < nhi) { lo = nlo; hi = nhi; }
+        if (nlo < nhi) { lo = nlo; hi = nhi; hi_probed = badm != 0; }
     }
     bool have = false;
     int key = 0;
-    if (spread > 0 && hi - lo == 1 && hi < m) {  // hi is a probe of the first round: its row_ptr is that lane's
+    if (hi_probed && hi - lo == 1) {  // hi is a probe of the first round: its row_ptr is that lane's
         have = true;
         key = __builtin_amdgcn_readlane(p.k, (hi - g) / spread + 32);
     }
@@ -1735,6 +1758,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     int kb = (int)(t * K);
     int B0 = last ? nnz : kb + K;
     int lend = m, nend = nnz;
+    int run_r0 = 0;  // RUNS search: the run's first row
     int f = 0, rpf = 0, l = 0, rpl = 0;
     if constexpr (RUNS) {
         if (MODE == kFlatMemo) {  // recorded by the call that searched: (f, rpf, l, rpl), (kb, B0, last)
@@ -1754,6 +1778,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
             last = ne - kb <= K;
             B0 = last ? ne : kb + K;
             lend = rt.runs[2 * R + i];
+            run_r0 = rt.runs[R + i];
             nend = ne;
         }
     }
@@ -1761,6 +1786,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         kb = min(max(kb, 0), nnz);
         B0 = min(max(B0, kb), min(nnz, kb + K));
         lend = min(max(lend, 0), m);
+        run_r0 = min(max(run_r0, 0), lend);
     }
     const uint32_t ke = last ? (uint32_t)nend + 1u : (uint32_t)(kb + K);
 
@@ -1771,9 +1797,10 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     }
     // Search modes: waves 2 and 3 issue the first probe round of their row
     // searches (f, l) ahead of the tile's col / val loads.
-    RowProbe probe{0, 0, false};
+    RowProbe probe{0, 0, 0, m, 0, false};
     if (MODE != kFlatMemo && ((wave == 2 && kb != 0) || (wave == 3 && !last)))
-        probe = row_probe_issue(a.rp, m, wave == 2 ? (uint32_t)kb : ke, nnz, a.guess_spread, lane);
+        probe = RUNS ? row_probe_run(a.rp, run_r0, lend, lane)
+                     : row_probe_issue(a.rp, m, wave == 2 ? (uint32_t)kb : ke, nnz, a.guess_spread, lane);
     __builtin_amdgcn_sched_barrier(0);
     int c[VPT][4];
     T v[VPT][4];
@@ -1814,16 +1841,14 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     if (MODE != kFlatMemo) {
         if (wave == 2) {  // f: first row with row_ptr >= kb
             int r = 0;
-            const int ff = kb == 0 ? (r = a.rp[0], 0)
-                                   : row_probe_finish(a.rp, m, (uint32_t)kb, probe, a.guess_spread, lane, r) + 1;
+            const int ff = kb == 0 ? (r = a.rp[0], 0) : row_probe_finish(a.rp, m, (uint32_t)kb, probe, lane, r) + 1;
             if (lane == 0) {
                 s_info[0] = ff; s_info[1] = r;
                 if (!RUNS && MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
             }
         } else if (wave == 3) {  // l: first row with row_ptr >= ke (the run's or matrix's end for a last tile)
             int r = 0;
-            const int ll = last ? (r = a.rp[lend], lend)
-                                : row_probe_finish(a.rp, m, ke, probe, a.guess_spread, lane, r) + 1;
+            const int ll = last ? (r = a.rp[lend], lend) : row_probe_finish(a.rp, m, ke, probe, lane, r) + 1;
             if (lane == 0) {
                 s_info[2] = ll; s_info[3] = r;
                 if (!RUNS && MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
