@@ -1709,11 +1709,33 @@ struct RunTable {
     int nruns;
 };
 
-// The run holding run tile t: the largest i < nruns with tile_begin[i] <= t (a
-// wave-cooperative search; every probe stays inside the table).
-__device__ __forceinline__ int run_of_tile(const RunTable &rt, long long t, int lane)
+// The run holding run tile t: the largest i < nruns with tile_begin[i] <= t.
+// First 16 entries around where t falls if the runs held equal numbers of
+// tiles, read with one scalar load (the table is small and shared by every
+// workgroup, so it stays in the scalar cache); when those do not bracket t, a
+// wave-cooperative search.  Every read stays inside the table.
+__device__ __forceinline__ int run_of_tile(const RunTable &rt, long long t, long long ntiles, int lane)
 {
-    long long lo = 0, hi = rt.nruns;  // tile_begin[lo] <= t < tile_begin[hi] (tile_begin[nruns] = total)
+    typedef const int __attribute__((address_space(4))) cint;
+    const int nr = rt.nruns;
+    if (nr >= 16 && ntiles > 0) {
+        const long long gl = t * nr / ntiles - 8;
+        const int g = uni((int)min(max(gl, 0LL), (long long)(nr - 16)));  // entries [g, g + 16) of [0, nr)
+        const unsigned long long qa = reinterpret_cast<unsigned long long>(rt.runs + g);
+        const unsigned alo = __builtin_amdgcn_readfirstlane((unsigned)qa);  // each half unsigned (zero-extended)
+        const unsigned ahi = __builtin_amdgcn_readfirstlane((unsigned)(qa >> 32));
+        const cint *q = (const cint *)(((unsigned long long)ahi << 32) | (unsigned long long)alo);
+        int kk[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kk[i] = q[i];
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c += (long long)kk[i] <= t ? 1 : 0;
+        // the entries at or below t are a prefix; t is bracketed when the first is one and the last is not
+        // (or the window ends the table, whose end tile_begin[nr] is above every tile)
+        if (c > 0 && (c < 16 || g + 16 == nr)) return g + c - 1;
+    }
+    long long lo = 0, hi = nr;  // tile_begin[lo] <= t < tile_begin[hi] (tile_begin[nruns] = total)
     while (hi - lo > 1) {
         const long long step = (hi - lo + 63) >> 6;
         const long long p = lo + (long long)lane * step;
@@ -1768,7 +1790,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
             kb = e1.x; B0 = e1.y; last = e1.z != 0;
             lend = l; nend = rpl;
         } else {
-            const int i = run_of_tile(rt, t, lane);
+            const int i = run_of_tile(rt, t, a.ntiles, lane);
             const int R = rt.nruns + 1;
             // tiles from the run's first nnz rounded down to 64, so every 64-lane load covers whole lines of
             // col and val; the nnz before the run's first row belong to the dense row before it and are
