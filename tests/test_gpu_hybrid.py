@@ -41,6 +41,7 @@ SHAPES = {
     "only_dense": "D D D",
     "single_dense_middle": "1000 D 1000",
     "many_short_runs": " ".join(["D 3"] * 60),
+    "uneven_runs": "5000 D " + " ".join(["D 2"] * 40),
 }
 
 
@@ -351,3 +352,38 @@ def test_hybrid_graph_replays_match_eager(kind):
         plan.check(stream=s)
         plan.close()
     assert_parity(rp, col, val, x, eager.cpu().numpy(), "f64", what=f"{kind}/graph")
+
+
+@pytest.mark.parametrize("halves", [False, True], ids=["one-pass", "x-halves"])
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("name", sorted(SHAPES) + ["long:" + s for s in sorted(LONG_SHAPES)])
+def test_hybrid_search_every_call(name, dtype, halves):
+    # Calls that search (the run tiles' rows inside their runs, each tile's run in the run table, the dense
+    # rows' window bounds) give the y of the calls that read what the first call recorded, bit for bit, on
+    # every edge shape: many equal runs (the run lookup's proportional window), one long run before many
+    # short ones (its fallback search), empty runs, dense or long rows first and last.
+    if name.startswith("long:"):
+        rp, col, n = _long_case(name[5:], dtype, seed=41)
+    else:
+        rp, col, n = _case(name, seed=41)
+    rng = np.random.default_rng(42)
+    val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+    x = rng.uniform(-1, 1, n).astype(NP[dtype])
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    m = len(rp) - 1
+    y = torch.empty(m, dtype=TORCH[dtype], device="cuda")
+    outs = {}
+    with pf.Plan(d_rp, d_col, m, n, len(col), dtype, "flat") as p:
+        assert p.info.hybrid == 1
+        p.set_x_halves(halves)
+        assert p.info.x_halves == int(halves)
+        for label, remember in (("first", True), ("memo", True), ("search", False), ("search2", False),
+                                ("memo2", True)):
+            p.set_remember_rows(remember)
+            y.fill_(float("nan"))
+            p.execute(d_rp, d_col, d_val, d_x, y)
+            p.check()
+            outs[label] = y.cpu().numpy()
+    for label in ("memo", "search", "search2", "memo2"):
+        assert np.array_equal(outs[label], outs["first"]), label
+    assert_parity(rp, col, val, x, outs["first"], dtype, what=f"{name}/search every call")
