@@ -71,13 +71,13 @@ typedef struct pfk_spmv_args {
     size_t owner_bytes;
     size_t row_map_bytes;
     size_t sched_bytes;
-    /* Hybrid plans (pfk_spmv_hybrid) only.  Dense rows (sorted columns) are summed by x windows of
-     * PFK_DENSE_WINDOW(dtype) columns; the rows between them form runs, each cut into row-aligned
+    /* Hybrid plans (pfk_spmv_hybrid) only.  Dense rows (sorted columns) are summed by x windows of at most
+     * PFK_DENSE_WINDOW(dtype) columns (pfk_dense_nwin, pfk_dense_width); the rows between them form runs, each cut into row-aligned
      * tiles of `tile` nnz (every run row holds at most PFK_ALIGN_ROW_MAX nnz).  ntiles counts the tiles
      * of all runs. */
     const int *dense_rows;   /* [n_dense] row indices, ascending */
     int n_dense;
-    int n_win;               /* ceil(n / PFK_DENSE_WINDOW(dtype)) */
+    int n_win;               /* pfk_dense_nwin(n, dtype) */
     int n_runs;
     const int *runs;         /* [5 * (n_runs + 1)]: tile_begin[n_runs + 1] (the last = ntiles), then row_begin,
                                 row_end, nnz_begin, nnz_end [n_runs + 1 each, the last unused] */
@@ -122,8 +122,24 @@ typedef struct pfk_spmv_args {
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
 #define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
 
-/* Columns per x window of a hybrid plan's dense-row kernel (64 KB of LDS). */
+/* Columns per x window of a hybrid plan's dense-row kernel, at most (64 KB of LDS). */
 #define PFK_DENSE_WINDOW(dtype) ((dtype) == 0 ? 8192 : 16384)
+
+/* x windows of a dense-mode hybrid plan: the fewest of at most PFK_DENSE_WINDOW(dtype) columns, rounded up to a
+ * multiple of 8 so that each XCD takes as many windows as the others. */
+static inline int pfk_dense_nwin(long long n, int dtype)
+{
+    const long long k = (n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype);
+    return (int)((k + 7) / 8 * 8);
+}
+
+/* Columns of each of those windows (the last may reach past n): n / n_win rounded up to a multiple of 64, so
+ * every window starts on a 128-byte line of x.  At most PFK_DENSE_WINDOW(dtype) when n_win = pfk_dense_nwin. */
+static inline int pfk_dense_width(long long n, int n_win)
+{
+    const long long c = n_win > 0 ? (n + n_win - 1) / n_win : 0;
+    return (int)((c + 63) / 64 * 64);
+}
 
 /* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums (or, in
  * long mode, the long-row tiles) and their combine, three or four launches.  map_ready 0: the call searches rows and segment bounds (and records them

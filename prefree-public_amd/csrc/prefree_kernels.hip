@@ -1961,6 +1961,8 @@ struct DenseArgs {
     int nd;
     int nwin;
     int ngroups;
+    int win;                       // columns per window (at most kW), window w = [w win, (w + 1) win)
+    int gsz;                       // dense rows per group (at most kG): the groups are as even as they can be
     int *__restrict__ seg;         // [nd][nwin + 1] first nnz of each window (recorded / read)
     void *__restrict__ part;       // [nd][nwin] partial sums (accumulation type)
 };
@@ -2113,7 +2115,7 @@ template <typename T>
 __device__ __forceinline__ void dense_rows_searched(const Args<T> &a, const DenseArgs &d, const T *sx, int w,
                                                     int c0, int i0, int nk)
 {
-    constexpr int W = DenseShape<T>::kW;
+    const int W = d.win;
     const int lane = threadIdx.x & (kWave - 1);
     const int nnz = a.nnz;
     int ms = 0, me = 0;
@@ -2131,8 +2133,9 @@ __device__ __forceinline__ void dense_rows_searched(const Args<T> &a, const Dens
                 const double place = a.n > 0 ? (double)v * ((double)len / (double)a.n) : 0.0;
                 return a0 + (int)fmin(fmax(place, 0.0), (double)max(len - 1, 0));
             };
+            const int ce = (int)min((long long)c0 + W, (long long)a.n);  // the window's end, at most n
             ms = lane_lower_bound(a.col, a0, a1, c0, guess(c0), sp);
-            me = lane_lower_bound(a.col, a0, a1, c0 + W, guess(c0 + W), sp);
+            me = lane_lower_bound(a.col, a0, a1, ce, guess(ce), sp);
             if (d.seg) {
                 int *sg = d.seg + (long long)i * (d.nwin + 1);
                 sg[w] = ms;
@@ -2154,18 +2157,20 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
     const int w = xcd * wper + q % wper, g = q / wper;
     if (w >= d.nwin || g >= d.ngroups)
         return;
-    const int c0 = w * W;
-    const int i_end = min(d.nd, (g + 1) * G);
-    {  // the window x[c0, c0 + W) into LDS, 16 bytes per lane and load; zeros past n
-        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + c0, (long long)min(W, a.n - c0) * (long long)sizeof(T));
+    const int c0 = (int)min((long long)w * d.win, (long long)a.n);  // a window past n holds no column
+    const int i_end = min(d.nd, (g + 1) * d.gsz);
+    {  // the window x[c0, c0 + win) into LDS, 16 bytes per lane and load; zeros past n
+        const long long have = max(0LL, min((long long)d.win, (long long)a.n - c0));
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (have > 0 ? c0 : 0), have * (long long)sizeof(T));
         constexpr int kPer = 16 / (int)sizeof(T);
+        const int nv = min(d.win, W) / kPer;
 #pragma unroll 4
-        for (int i = tid; i < W / kPer; i += kBS)
+        for (int i = tid; i < nv; i += kBS)
             *reinterpret_cast<u32x4 *>(sx + i * kPer) = __builtin_amdgcn_raw_buffer_load_b128(rx, i * 16, 0, 0);
     }
     lds_sync();
     static_assert(G / kWaves <= kWave, "one lane per row of a wave");
-    const int i0 = g * G + wave;
+    const int i0 = g * d.gsz + wave;
     const int nk = i0 < i_end ? (i_end - i0 + kWaves - 1) / kWaves : 0;
     if constexpr (MODE == kFlatMemo)
         dense_rows_recorded<T>(a, d, sx, w, c0, i0, nk);
@@ -3534,7 +3539,9 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
         return PF_OK;
     }
     const int ngroups = (a->n_dense + DenseShape<T>::kG - 1) / DenseShape<T>::kG;
-    const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, a->dense_seg, a->dense_part};
+    const int gsz = ngroups > 0 ? (a->n_dense + ngroups - 1) / ngroups : 0;
+    const DenseArgs d{a->dense_rows, a->n_dense, a->n_win, ngroups, pfk_dense_width(a->n, a->n_win), gsz,
+                      a->dense_seg, a->dense_part};
     const unsigned dgrid = (unsigned)(kXcds * ((a->n_win + kXcds - 1) / kXcds) * ngroups);
     if (memo)
         hipLaunchKernelGGL((k_dense<T, kFlatMemo>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
@@ -3588,8 +3595,8 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
         snprintf(g_err, sizeof g_err, "hybrid call: missing tables or tile %d", a->tile);
         return PF_ERR_INVALID;
     }
-    const long long win = PFK_DENSE_WINDOW(dtype);
-    if (!a->long_mode && (a->n_win != (int)((a->n + win - 1) / win) || a->n_win < 1)) {
+    if (!a->long_mode && (a->n_win != pfk_dense_nwin(a->n, dtype) || a->n_win < 1 ||
+                          pfk_dense_width(a->n, a->n_win) > PFK_DENSE_WINDOW(dtype))) {
         snprintf(g_err, sizeof g_err, "hybrid call: %d x windows for n = %d", a->n_win, a->n);
         return PF_ERR_INVALID;
     }

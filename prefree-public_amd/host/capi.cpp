@@ -633,7 +633,7 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
         long_nnz += rb1[(size_t)i] - rb0[(size_t)i];
         shortest = std::min(shortest, (long long)(rb1[(size_t)i] - rb0[(size_t)i]));
     }
-    const int nwin = (int)((p->n + PFK_DENSE_WINDOW(dtype) - 1) / PFK_DENSE_WINDOW(dtype));
+    const int nwin = pfk_dense_nwin(p->n, dtype);
     const long long xb = (long long)p->n * value_bytes(dtype);
     const bool dense = cnt[1] == 0 && shortest >= dense_min(p->n, dtype) &&
                        cap * (nwin + 1) <= (64LL << 20);  // segment table under 256 MB

@@ -23,8 +23,10 @@ HEADERS = {
 
 
 def declared_functions(header):
+    """Functions the header declares for the library to export (its static inline helpers are header-only)."""
     text = open(os.path.join(REPO, "include", header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"static inline[^{;]*\{.*?\n\}", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(pfk?_[a-z0-9_]+)\s*\(", text)))
 
 
@@ -378,3 +380,32 @@ def test_ctypes_mirrors_match_the_c_structs(tmp_path):
         assert got[(pyname, "sizeof")] == ctypes.sizeof(cls), pyname
         for fname, _t in cls._fields_:
             assert got[(pyname, fname)] == getattr(cls, fname).offset, (pyname, fname)
+
+
+def test_dense_windows_cover_x_evenly(tmp_path):
+    """pfk_dense_nwin / pfk_dense_width (include/prefree_kernels.h): a multiple of 8 windows (one share per XCD),
+    each a multiple of 64 columns and at most PFK_DENSE_WINDOW(dtype), together covering [0, n), with no more
+    windows than the fewest of that width rounded up to a multiple of 8."""
+    inc = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include")
+    src = tmp_path / "win.c"
+    src.write_text("\n".join([
+        "#include <stdio.h>", '#include "prefree_kernels.h"', "int main(void) {",
+        "  const long long ns[] = {1, 63, 64, 65, 8191, 8192, 8193, 60000, 65536, 65537, 600000, 1000000, 1100000,",
+        "                          2000000, 4194304, 20000000, 2147483647LL};",
+        "  for (int t = 0; t < 2; ++t) for (unsigned i = 0; i < sizeof ns / sizeof ns[0]; ++i) {",
+        "    const int nw = pfk_dense_nwin(ns[i], t), w = pfk_dense_width(ns[i], nw);",
+        '    printf("%d %lld %d %d\\n", t, ns[i], nw, w);',
+        "  }", "  return 0; }"]) + "\n")
+    exe = tmp_path / "win"
+    subprocess.run(["gcc", "-std=c11", "-I", inc, "-o", str(exe), str(src)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    rows = [tuple(int(v) for v in line.split()) for line in out if line]
+    assert len(rows) == 34
+    for dtype, n, nw, w in rows:
+        cap = 8192 if dtype == 0 else 16384
+        fewest = -(-n // cap)
+        assert nw % 8 == 0 and fewest <= nw < fewest + 8, (dtype, n, nw)
+        assert w % 64 == 0 and 0 < w <= cap, (dtype, n, w)
+        assert nw * w >= n, (dtype, n, nw, w)
+    c5 = {(d, n): (nw, w) for d, n, nw, w in rows}
+    assert c5[(0, 1000000)] == (128, 7872) and c5[(1, 1000000)] == (64, 15680)
