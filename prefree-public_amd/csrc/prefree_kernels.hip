@@ -1619,15 +1619,34 @@ __device__ __forceinline__ RowProbe row_probe_issue(const int *__restrict__ rp, 
     return row_probe_at(rp, (int)fmin(g, (double)(m > 0 ? m - 1 : 0)), spread, 0, m, lane);
 }
 
-// Inside a run of a hybrid plan, rows [r0, r1): the 63 probes spread evenly
-// over the run.  row_ptr[r0 - 1] (the dense or long row before the run) is
-// below any key of the run's tiles, and row_ptr[r1] (the run's end) at or
-// above it, so the search never leaves the run.
-__device__ __forceinline__ RowProbe row_probe_run(const int *__restrict__ rp, int r0, int r1, int lane)
+// Inside a run of a hybrid plan, rows [r0, r1) holding nnz [n0, n1): the 256
+// row_ptr entries around the row that linear interpolation over the run puts
+// the key v at, four consecutive entries per lane (one 16-byte load each).  A
+// key they bracket is found in this one round (row_window_finish); a run's
+// rows deviate from the interpolation by a few rows (a random walk pinned at
+// both ends: C5's runs of about 1000 rows of 8-64 nnz, 7 rows at most by one
+// standard deviation).  row_ptr[r0 - 1] (the dense or long row before the
+// run) is below any key of the run's tiles, and row_ptr[r1] (the run's end)
+// at or above it, so the search never leaves the run.
+struct RowWindow {
+    int base;      // entries [base, base + 256), base a multiple of 4
+    int lo0, hi0;  // the bracket they refine: row_ptr[lo0] < v <= row_ptr[hi0]
+    u32x4 k;       // row_ptr[base + 4 lane + j], 0 past row_ptr's m + 1 entries
+};
+
+__device__ __forceinline__ RowWindow row_window_run(const int *__restrict__ rp, int m, int r0, int r1, int n0,
+                                                    int n1, uint32_t v, int lane)
 {
-    const int lo0 = max(r0 - 1, 0);
-    const int sp = max(1, (r1 - lo0 - 1 + 62) / 63);
-    return row_probe_at(rp, lo0 + 32 * sp, sp, lo0, r1, lane);
+    RowWindow w;
+    const double f = n1 > n0 ? ((double)v - (double)n0) / ((double)n1 - (double)n0) : 0.0;
+    const int g = r0 + (int)fmin(fmax(f * (double)(r1 - r0), 0.0), (double)max(r1 - r0, 0));
+    w.base = uni(max(0, g - 4 * kWave / 2) & ~3);
+    w.lo0 = uni(max(r0 - 1, 0));
+    w.hi0 = uni(r1);
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(rp + w.base, (long long)max(0, min(4 * kWave, m + 1 - w.base)) * 4);
+    w.k = __builtin_amdgcn_raw_buffer_load_b128(rr, lane * 16, 0, 0);
+    return w;
 }
 
 // Largest r in [0, m) with row_ptr[r] < v (v > 0), and row_ptr[r + 1] in
@@ -1699,6 +1718,38 @@ __device__ __forceinline__ int row_probe_finish(const int *__restrict__ rp, int 
     }
     next_key = have ? key : *srp(lo + 1);
     return lo;
+}
+
+// Largest r in [lo0, hi0) with row_ptr[r] < v, and row_ptr[r + 1] in
+// next_key, from a run tile's window.  The window's entries strictly inside
+// (lo0, hi0) below v are a prefix of them (row_ptr is non-decreasing): when
+// the entry after that prefix is also in the window, the two bracket v and
+// the search ends here; otherwise row_probe_finish goes on from the bracket
+// the window left.  Whole wave active; wave-uniform.
+__device__ __forceinline__ int row_window_finish(const int *__restrict__ rp, int m, uint32_t v, const RowWindow &w,
+                                                 int lane, int &next_key)
+{
+    const int base = uni(w.base), lo0 = uni(w.lo0), hi0 = uni(w.hi0);
+    const int s = min(max(lo0 + 1 - base, 0), 4 * kWave);  // entries [s, e) of the window lie inside (lo0, hi0)
+    const int e = min(max(hi0 - base, s), 4 * kWave);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * lane + j;
+        c += __popcll(__ballot(i >= s && i < e && w.k[j] < v));
+    }
+    const int nlo = c > 0 ? base + s + c - 1 : lo0;  // row_ptr[nlo] < v
+    if (s + c < e && (c > 0 || s + base == lo0 + 1)) {  // row_ptr[nlo + 1] >= v is the window's entry s + c
+        const int i = s + c;
+        const unsigned k0 = __builtin_amdgcn_readlane(w.k[0], i >> 2), k1 = __builtin_amdgcn_readlane(w.k[1], i >> 2);
+        const unsigned k2 = __builtin_amdgcn_readlane(w.k[2], i >> 2), k3 = __builtin_amdgcn_readlane(w.k[3], i >> 2);
+        const int sel = i & 3;
+        next_key = (int)(sel == 0 ? k0 : sel == 1 ? k1 : sel == 2 ? k2 : k3);
+        return nlo;
+    }
+    const int nhi = s + c < e ? base + s + c : hi0;
+    const RowProbe p{0, 0, nlo, nhi, 0, false};  // no first round: 64-ary rounds from (nlo, nhi)
+    return row_probe_finish(rp, m, v, p, lane, next_key);
 }
 
 // Runs of a hybrid plan: the rows between two dense rows (or a matrix end), each
@@ -1780,7 +1831,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     int kb = (int)(t * K);
     int B0 = last ? nnz : kb + K;
     int lend = m, nend = nnz;
-    int run_r0 = 0;  // RUNS search: the run's first row
+    int run_r0 = 0, run_n0 = 0, run_n1 = 0;  // RUNS search: the run's first row, its nnz range
     int f = 0, rpf = 0, l = 0, rpl = 0;
     if constexpr (RUNS) {
         if (MODE == kFlatMemo) {  // recorded by the call that searched: (f, rpf, l, rpl), (kb, B0, last)
@@ -1801,6 +1852,8 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
             B0 = last ? ne : kb + K;
             lend = rt.runs[2 * R + i];
             run_r0 = rt.runs[R + i];
+            run_n0 = rt.runs[3 * R + i];
+            run_n1 = ne;
             nend = ne;
         }
     }
@@ -1820,9 +1873,14 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     // Search modes: waves 2 and 3 issue the first probe round of their row
     // searches (f, l) ahead of the tile's col / val loads.
     RowProbe probe{0, 0, 0, m, 0, false};
-    if (MODE != kFlatMemo && ((wave == 2 && kb != 0) || (wave == 3 && !last)))
-        probe = RUNS ? row_probe_run(a.rp, run_r0, lend, lane)
-                     : row_probe_issue(a.rp, m, wave == 2 ? (uint32_t)kb : ke, nnz, a.guess_spread, lane);
+    RowWindow window{0, 0, m, u32x4{0u, 0u, 0u, 0u}};
+    if (MODE != kFlatMemo && ((wave == 2 && kb != 0) || (wave == 3 && !last))) {
+        const uint32_t key = wave == 2 ? (uint32_t)kb : ke;
+        if constexpr (RUNS)
+            window = row_window_run(a.rp, m, run_r0, lend, run_n0, run_n1, key, lane);
+        else
+            probe = row_probe_issue(a.rp, m, key, nnz, a.guess_spread, lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
     int c[VPT][4];
     T v[VPT][4];
@@ -1863,14 +1921,18 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     if (MODE != kFlatMemo) {
         if (wave == 2) {  // f: first row with row_ptr >= kb
             int r = 0;
-            const int ff = kb == 0 ? (r = a.rp[0], 0) : row_probe_finish(a.rp, m, (uint32_t)kb, probe, lane, r) + 1;
+            const int ff = kb == 0 ? (r = a.rp[0], 0)
+                                   : (RUNS ? row_window_finish(a.rp, m, (uint32_t)kb, window, lane, r)
+                                           : row_probe_finish(a.rp, m, (uint32_t)kb, probe, lane, r)) + 1;
             if (lane == 0) {
                 s_info[0] = ff; s_info[1] = r;
                 if (!RUNS && MODE == kFlatSearch && map) reinterpret_cast<int2 *>(map)[t] = make_int2(ff, r);
             }
         } else if (wave == 3) {  // l: first row with row_ptr >= ke (the run's or matrix's end for a last tile)
             int r = 0;
-            const int ll = last ? (r = a.rp[lend], lend) : row_probe_finish(a.rp, m, ke, probe, lane, r) + 1;
+            const int ll = last ? (r = a.rp[lend], lend)
+                                : (RUNS ? row_window_finish(a.rp, m, ke, window, lane, r)
+                                        : row_probe_finish(a.rp, m, ke, probe, lane, r)) + 1;
             if (lane == 0) {
                 s_info[2] = ll; s_info[3] = r;
                 if (!RUNS && MODE == kFlatSearch && map && last) reinterpret_cast<int2 *>(map)[t + 1] = make_int2(ll, r);
