@@ -1992,14 +1992,16 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
 // A dense row (at least the plan's dense_min nnz, columns sorted) sweeps all of
 // x.  Summed tile by tile, each of its tiles drags its whole x span from L2
 // into a CU's L1 for a few nnz per line.  Here a workgroup stages one window
-// of W consecutive x entries in LDS and sums, for each of G dense rows, the
-// segment of the row whose columns fall in the window: x is read once per
-// G rows instead of once per row.  Workgroup (window w, group g) is dealt so
-// that an XCD takes a contiguous eighth of the windows (its x entries stay in
-// its L2).  Each (row, window) partial sum goes to part[row][w]; k_dense_sum
-// adds them up.  Segment bounds: MODE kFlatSearch finds them by
-// a wave search of the row's columns and records them in seg; kFlatMemo reads
-// them.  C5 (1000 rows of 50k-500k nnz, 280M nnz): 558 us against 742 us for
+// of win consecutive x entries (at most W, 64 KB) in LDS and sums, for each of
+// at most G dense rows, the segment of the row whose columns fall in the
+// window: x is read once per group of rows instead of once per row.  The
+// windows are a multiple of 8 (pfk_dense_nwin) and the groups as even as they
+// can be, and workgroup (window w, group g) is dealt so that each XCD takes a
+// contiguous eighth of the windows (its x entries stay in its L2): every XCD
+// does the same work.  Each (row, window) partial sum goes to part[row][w];
+// k_dense_sum adds them up.  Segment bounds: MODE kFlatSearch finds them by a
+// per-lane search of each row's columns and records them in seg; kFlatMemo
+// reads them.  C5 (1000 rows of 50k-500k nnz, 280M nnz): 558 us against 742 us for
 // the same rows in split-row tiles with the x-window schedule.  16 loads in
 // flight per lane and 128 rows per workgroup were the best of U = 4-16 and
 // G = 64-256 (C5 fp64 whole step 896-1015 us, fp32 598-942).
