@@ -73,6 +73,10 @@ typedef struct pf_row_stats {
     long long guess_dev;      /* largest |r - row_ptr[r] * m / nnz| over the rows, rounded up: how far a row
                                  lies from where the mean density puts it (sizes the row searches' first
                                  probe round) */
+    long long line_q1_row_ptr;   /* row_ptr[m / 4] and row_ptr[3m / 4]: the line through (row_ptr[m / 4], m / 4) */
+    long long line_q3_row_ptr;   /* and (row_ptr[3m / 4], 3m / 4) puts row_ptr values at rows */
+    long long line_far_rows;     /* rows more than 28 rows from where that line puts their row_ptr (m when the
+                                    line is undefined: m < 4 or row_ptr[m / 4] == row_ptr[3m / 4]) */
 } pf_row_stats;
 
 /* Launch configuration chosen for a matrix. */
@@ -107,6 +111,10 @@ typedef struct pf_plan_info {
     int x_halves;         /* hybrid plans: 1 = the runs' tiles are processed once per half of x, by XCDs 0-3 and
                              4-7, so each XCD's random gathers fall in half of x (chosen when x is 4-24 MB) */
     int long_tiles;       /* hybrid plans in long mode: tiles of the long rows; 0 otherwise */
+    double guess_a, guess_b; /* row-aligned FLAT tiles: when guess_a > 0, their row searches' first probe round
+                                is centred on row guess_a * key + guess_b with a spacing of 1 (the line of
+                                pf_row_stats, chosen when at most m / 256 rows lie over 28 rows from it); 0:
+                                key * m / nnz with guess_spread */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;

@@ -114,6 +114,10 @@ typedef struct pfk_spmv_args {
     void *aux_stream;
     void *ev_fork;
     void *ev_join;
+    /* Row-aligned FLAT tiles that search rows: when guess_a > 0 the first probe round for key v is centred on
+       row guess_a * v + guess_b, 64 rows apart by 1; else on v * m / nnz, guess_spread apart.  Any values give
+       the same rows (a round that does not bracket the key is followed by wider ones). */
+    double guess_a, guess_b;
 } pfk_spmv_args;
 
 /* nnz per long-row tile of a hybrid plan in long mode. */
@@ -179,7 +183,7 @@ int pfk_flow_resident_waves(int dtype, long long *waves);
 /* Workgroups a FLAT 1024/2048 launch without a schedule uses for ntiles tiles and chunk_nnz. */
 long long pfk_flat_grid(long long ntiles, int tile, long long chunk_nnz);
 
-/* Row statistics.  d_out: 44 unsigned long long (layout in prefree_kernels.hip). */
+/* Row statistics.  d_out: 46 unsigned long long (layout in prefree_kernels.hip). */
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,
                   unsigned long long *d_out, void *stream);
 

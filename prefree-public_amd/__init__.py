@@ -47,7 +47,9 @@ class RowStats(ctypes.Structure):
                 ("n_decreasing", ctypes.c_longlong), ("row_ptr_first", ctypes.c_longlong),
                 ("row_ptr_last", ctypes.c_longlong), ("n_bad_cols", ctypes.c_longlong),
                 ("hist_log2", ctypes.c_longlong * 33), ("n_long_rows", ctypes.c_longlong),
-                ("max_short_row_len", ctypes.c_longlong), ("guess_dev", ctypes.c_longlong)]
+                ("max_short_row_len", ctypes.c_longlong), ("guess_dev", ctypes.c_longlong),
+                ("line_q1_row_ptr", ctypes.c_longlong), ("line_q3_row_ptr", ctypes.c_longlong),
+                ("line_far_rows", ctypes.c_longlong)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_ if k != "hist_log2"}
@@ -62,7 +64,8 @@ class PlanInfo(ctypes.Structure):
                 ("grid", ctypes.c_longlong),
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
                 ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int), ("hybrid", ctypes.c_int),
-                ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int), ("long_tiles", ctypes.c_int)]
+                ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int), ("long_tiles", ctypes.c_int),
+                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -108,7 +111,8 @@ class SpmvArgs(ctypes.Structure):
                 ("long_part", ctypes.c_void_p), ("long_tiles_bytes", ctypes.c_size_t),
                 ("long_deal_bytes", ctypes.c_size_t), ("long_row_tiles_bytes", ctypes.c_size_t),
                 ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int),
-                ("aux_stream", ctypes.c_void_p), ("ev_fork", ctypes.c_void_p), ("ev_join", ctypes.c_void_p)]
+                ("aux_stream", ctypes.c_void_p), ("ev_fork", ctypes.c_void_p), ("ev_join", ctypes.c_void_p),
+                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double)]
 
 
 _lib = None
@@ -355,14 +359,14 @@ def spmv(row_ptr, col, val, x, y, m, n, nnz, dtype="f64", variant="auto", stream
 
 
 def tile_descriptors(row_ptr, m, nnz, tile, merged, out, err_flag, guess_spread=0, run_tiles=0, stream=None,
-                     row_aligned=False, chunk_nnz=0):
+                     row_aligned=False, chunk_nnz=0, guess_a=0.0, guess_b=0.0):
     """pfk_debug_tile_desc: per-tile descriptors of ADAPTIVE (merged) / FLAT (split or row-aligned
     tiles, dealt to the XCDs in chunks of chunk_nnz) into `out` (int32[8*ntiles])."""
     total = nnz + m if merged else nnz
     ntiles = max(1, -(-total // tile))
     a = SpmvArgs(row_ptr=_p(row_ptr), m=m, n=m, nnz=nnz, tile=tile, guess_spread=guess_spread,
                  run_tiles=run_tiles, ntiles=ntiles, err_flag=_p(err_flag), row_aligned=int(bool(row_aligned)),
-                 chunk_nnz=int(chunk_nnz))
+                 chunk_nnz=int(chunk_nnz), guess_a=float(guess_a), guess_b=float(guess_b))
     _check(klib().pfk_debug_tile_desc(F64, int(bool(merged)), ctypes.byref(a), _p(out), _s(stream)),
            "pfk_debug_tile_desc")
     return ntiles

@@ -102,6 +102,7 @@ struct Args {
     int n;
     int nnz;
     int guess_spread;
+    double guess_a, guess_b;  // row-aligned tiles' row searches: the line row = guess_a * key + guess_b (a > 0)
     long long ntiles;
     long long g8;        // tiles per XCD, padded to whole chunks (grid = 8 * g8)
     long long xch;       // tiles per chunk (see xcd_tile)
@@ -1610,13 +1611,16 @@ __device__ __forceinline__ RowProbe row_probe_at(const int *__restrict__ rp, int
     return p;
 }
 
-// Whole matrix: around the row the matrix's mean density gives (a hint: any
-// value gives the same result), `spread` from the plan (0: no probe round).
+// Whole matrix: around the row the matrix's mean density gives, `spread`
+// from the plan (0: no probe round), or, when the plan fitted a line to
+// row_ptr (ga > 0), around the row the line gives, 1 apart.  A hint: any
+// value gives the same result.
 __device__ __forceinline__ RowProbe row_probe_issue(const int *__restrict__ rp, int m, uint32_t v, int nnz,
-                                                    int spread, int lane)
+                                                    int spread, double ga, double gb, int lane)
 {
-    const double g = nnz > 0 ? (double)v * ((double)m / (double)nnz) : 0.0;
-    return row_probe_at(rp, (int)fmin(g, (double)(m > 0 ? m - 1 : 0)), spread, 0, m, lane);
+    const double g = ga > 0.0 ? ga * (double)v + gb : (nnz > 0 ? (double)v * ((double)m / (double)nnz) : 0.0);
+    const double gc = fmin(fmax(g, 0.0), (double)(m > 0 ? m - 1 : 0));  // (NaN: 0)
+    return row_probe_at(rp, (int)gc, ga > 0.0 ? 1 : spread, 0, m, lane);
 }
 
 // Inside a run of a hybrid plan, rows [r0, r1) holding nnz [n0, n1): the 256
@@ -1879,7 +1883,7 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
         if constexpr (RUNS)
             window = row_window_run(a.rp, m, run_r0, lend, run_n0, run_n1, key, lane);
         else
-            probe = row_probe_issue(a.rp, m, key, nnz, a.guess_spread, lane);
+            probe = row_probe_issue(a.rp, m, key, nnz, a.guess_spread, a.guess_a, a.guess_b, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
     int c[VPT][4];
@@ -3120,7 +3124,8 @@ __global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ id
 // Layout of the statistics block (unsigned long long):
 enum StatSlot {
     kStMax = 0, kStMin = 1, kStEmpty = 2, kStDec = 3, kStFirst = 4, kStLast = 5, kStBadCol = 6,
-    kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStGuessDev = 42, kStCount = 44
+    kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStGuessDev = 42, kStLineQ1 = 43, kStLineQ3 = 44,
+    kStLineFar = 45, kStCount = 46
 };
 
 __global__ void k_stats_init(unsigned long long *out)
@@ -3134,10 +3139,12 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
                                                    unsigned long long *__restrict__ out)
 {
     __shared__ unsigned int s_hist[33];
-    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev;
+    __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev, s_far;
     const int tid = threadIdx.x;
     if (tid < 33) s_hist[tid] = 0;
-    if (tid == 0) { s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; s_dev = 0; }
+    if (tid == 0) {
+        s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; s_dev = 0; s_far = 0;
+    }
     __syncthreads();
     unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0, lshort = 0;
     // distance in rows between row r and where the matrix's mean density puts row_ptr[r] (the row
@@ -3145,8 +3152,17 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     const int total = rp[m];
     const double per = total > 0 ? (double)m / (double)total : 0.0;
     double ldev = 0.0;
+    // rows more than 28 rows from the line through (row_ptr[m / 4], m / 4) and (row_ptr[3m / 4], 3m / 4), the
+    // row-aligned tiles' alternative first guess (every row counts when the line is undefined)
+    const int q1 = m / 4, q3 = (int)(3LL * m / 4);
+    const int p1 = m >= 4 ? rp[q1] : 0, p3 = m >= 4 ? rp[q3] : 0;
+    const bool line = m >= 4 && p3 > p1;
+    const double la = line ? (double)(q3 - q1) / ((double)p3 - (double)p1) : 0.0;
+    const double lb = line ? (double)q1 - la * (double)p1 : 0.0;
+    unsigned int lfar = 0;
     for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
         if (total > 0) ldev = fmax(ldev, fabs((double)r - (double)rp[r] * per));
+        lfar += !line || fabs((double)r - (la * (double)rp[r] + lb)) > 28.0;
         int len = rp[r + 1] - rp[r];
         if (len < 0) { ++ldec; len = 0; }
         const unsigned int u = (unsigned int)len;
@@ -3164,6 +3180,7 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     atomicAdd(&s_over, lover);
     atomicMax(&s_short, lshort);
     atomicMax(&s_dev, (unsigned int)fmin(ceil(ldev), 4294967295.0));
+    atomicAdd(&s_far, lfar);
     __syncthreads();
     if (tid < 33 && s_hist[tid]) atomicAdd(out + kStHist + tid, (unsigned long long)s_hist[tid]);
     if (tid == 0) {
@@ -3174,9 +3191,12 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
         atomicMax(out + kStMaxShort, (unsigned long long)s_short);
         atomicMax(out + kStGuessDev, (unsigned long long)s_dev);
+        atomicAdd(out + kStLineFar, (unsigned long long)s_far);
         if (blockIdx.x == 0) {
             out[kStFirst] = (unsigned long long)(long long)rp[0];
             out[kStLast] = (unsigned long long)(long long)rp[m];
+            out[kStLineQ1] = (unsigned long long)(long long)p1;
+            out[kStLineQ3] = (unsigned long long)(long long)p3;
         }
     }
 }
@@ -3290,6 +3310,8 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.n = a->n;
     r.nnz = a->nnz;
     r.guess_spread = a->guess_spread;
+    r.guess_a = a->guess_a > 0.0 ? a->guess_a : 0.0;  // (false for NaN)
+    r.guess_b = r.guess_a > 0.0 ? a->guess_b : 0.0;
     r.ntiles = a->ntiles;
     r.g8 = (a->ntiles + kXcds - 1) / kXcds;
     r.xch = r.g8;

@@ -379,6 +379,15 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
     int spread = 1;
     while (spread < 64 && 31LL * spread < s.guess_dev + 3) spread *= 2;
     r.guess_spread = regular ? spread : 0;
+    // A matrix whose row_ptr is nearly a straight line away from its ends (C2: the first grid row's rows are a
+    // nnz shorter than the rest, which shifts every later row 410 rows off the mean-density guess) puts almost
+    // every row within 28 rows of the line through its quartile rows: row-aligned tiles then centre their
+    // first probe round there, 1 row apart, and most searches end in that round.
+    const long long q1 = m / 4, q3 = 3 * m / 4;
+    if (regular && m >= 4 && s.line_q3_row_ptr > s.line_q1_row_ptr && s.line_far_rows * 256 <= m) {
+        r.guess_a = (double)(q3 - q1) / ((double)s.line_q3_row_ptr - (double)s.line_q1_row_ptr);
+        r.guess_b = (double)q1 - r.guess_a * (double)s.line_q1_row_ptr;
+    }
     const long long vb = slot_bytes(dtype);
     if (variant == PF_ADAPTIVE) {
         r.long_row_min = pfk_adaptive_long_row_min(dtype, tile);
@@ -830,12 +839,12 @@ int check_matrix_args(const int *d_row_ptr, const int *d_col, int m, int n, int 
     return PF_OK;
 }
 
-// Row statistics of a device CSR through a caller-supplied block of 44
+// Row statistics of a device CSR through a caller-supplied block of 46
 // unsigned long long (synchronises `stream`).
 int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int m, int n, long long nnz,
               pf_row_stats *out, void *stream)
 {
-    unsigned long long h[44];
+    unsigned long long h[46];
     int st = pfk_row_stats(d_row_ptr, d_col, m, n, nnz, d, stream);
     if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
     if (st == PF_OK) st = pfk_stream_sync(stream);
@@ -854,6 +863,9 @@ int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int
     out->n_long_rows = (long long)h[40];
     out->max_short_row_len = (long long)h[41];
     out->guess_dev = (long long)h[42];
+    out->line_q1_row_ptr = (long long)h[43];
+    out->line_q3_row_ptr = (long long)h[44];
+    out->line_far_rows = (long long)h[45];
     return PF_OK;
 }
 
@@ -900,7 +912,7 @@ int pf_row_stats_compute(const int *d_row_ptr, const int *d_col, int m, int n, l
     if (!out || !d_row_ptr || m < 0 || n < 0 || nnz < 0)
         return fail(PF_ERR_INVALID, "pf_row_stats_compute: bad argument");
     unsigned long long *d = nullptr;
-    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), 44 * sizeof(unsigned long long)), "stats buffer");
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), 46 * sizeof(unsigned long long)), "stats buffer");
     const int st = stats_via(d, d_row_ptr, d_col, m, n, nnz, out, stream);
     pfk_free(d);
     return st;
@@ -1071,6 +1083,8 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     a.nnz = plan->nnz;
     a.tile = plan->info.tile;
     a.guess_spread = plan->info.guess_spread;
+    a.guess_a = plan->info.guess_a;
+    a.guess_b = plan->info.guess_b;
     a.run_tiles = plan->info.run_tiles;
     a.keep_cached = plan->info.keep_cached;
     a.ntiles = plan->info.ntiles;

@@ -57,10 +57,25 @@ def test_tile_descriptors_match_model(merged, tile, spread, run):
         assert bad.size == 0, f"{name}: tile {bad[0]} got {got[bad[0]]} model {model[bad[0]]}"
 
 
+LINES = [None, "fit", "steep", "shallow", "offset", "huge"]
+
+
+def _line(rp, kind):
+    """A first-guess line row = a * key + b for the row-aligned tiles' searches: the plan's fit through the
+    quartile rows, or deliberately wrong ones (any line must give the same rows)."""
+    m, nnz = len(rp) - 1, int(rp[-1])
+    if kind is None or nnz == 0:
+        return 0.0, 0.0
+    a = m / nnz
+    return {"fit": (a, 0.0), "steep": (3.0 * a, 0.0), "shallow": (a / 7.0, 5.0), "offset": (a, -0.3 * m),
+            "huge": (1e12, 1e15)}[kind]
+
+
+@pytest.mark.parametrize("line", LINES, ids=[str(k) for k in LINES])
 @pytest.mark.parametrize("spread,chunk", [(0, 0), (1, 1 << 15), (2, 3000), (16, 1 << 15), (64, 1 << 15),
                                           (1000, 3000)])
 @pytest.mark.parametrize("tile", [1024, 2048])
-def test_row_aligned_descriptors_match_model(tile, spread, chunk):
+def test_row_aligned_descriptors_match_model(tile, spread, chunk, line):
     """Row-aligned FLAT tiles (rows starting in the tile, whole): exact descriptors wherever no
     tile's last row reaches 256 or more nnz past the tile's nominal end (always so when rows hold at
     most 256 nnz, the planning rule); otherwise the kernel refuses (error flag), since its product
@@ -73,8 +88,9 @@ def test_row_aligned_descriptors_match_model(tile, spread, chunk):
         ntiles = len(model)
         out = torch.full((8 * ntiles,), -7, dtype=torch.int32, device=DEV)
         err = torch.zeros(64, dtype=torch.int32, device=DEV)
+        ga, gb = _line(rp, line)
         got_tiles = pf.tile_descriptors(dev(rp), m, nnz, tile, False, out, err, guess_spread=spread,
-                                        row_aligned=True, chunk_nnz=chunk)
+                                        row_aligned=True, chunk_nnz=chunk, guess_a=ga, guess_b=gb)
         torch.cuda.synchronize()
         assert got_tiles == ntiles
         kb = np.arange(ntiles - 1, dtype=np.int64) * tile
