@@ -1628,8 +1628,8 @@ __device__ __forceinline__ RowProbe row_probe_issue(const int *__restrict__ rp, 
 // the key v at, four consecutive entries per lane (one 16-byte load each).  A
 // key they bracket is found in this one round (row_window_finish); a run's
 // rows deviate from the interpolation by a few rows (a random walk pinned at
-// both ends: C5's runs of about 1000 rows of 8-64 nnz, 7 rows at most by one
-// standard deviation).  row_ptr[r0 - 1] (the dense or long row before the
+// both ends: in C5's runs of about 1000 rows of 8-64 nnz its standard
+// deviation is at most about 7 rows).  row_ptr[r0 - 1] (the dense or long row before the
 // run) is below any key of the run's tiles, and row_ptr[r1] (the run's end)
 // at or above it, so the search never leaves the run.
 struct RowWindow {
