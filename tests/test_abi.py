@@ -90,6 +90,28 @@ def test_guess_spread_covers_the_deviation(dev, spread):
     assert pf.select(s, "f64", "flat").guess_spread == 0
 
 
+def test_line_guess_when_nearly_every_row_is_near_the_quartile_line():
+    """Row-aligned searches centre their first round on the line through (row_ptr[m/4], m/4) and
+    (row_ptr[3m/4], 3m/4) when at most m/256 rows lie over 28 rows from it (guess_a, guess_b); otherwise, or
+    when the line is undefined or the rows are longer than 64 nnz, on the mean-density guess (guess_a 0)."""
+    m, nnz = 1 << 20, 5 << 20
+    s = make_stats(m, nnz, 5)
+    s.guess_dev = 410
+    s.line_q1_row_ptr, s.line_q3_row_ptr = 5 * (m // 4) - 2048, 5 * (3 * m // 4) - 2048
+    s.line_far_rows = m // 256
+    i = pf.select(s, "f64", "flat")
+    a = (3 * m // 4 - m // 4) / (s.line_q3_row_ptr - s.line_q1_row_ptr)
+    assert i.guess_a == a and i.guess_b == m // 4 - a * s.line_q1_row_ptr and i.guess_spread == 16
+    s.line_far_rows = m // 256 + 1  # one row too many
+    assert pf.select(s, "f64", "flat").guess_a == 0.0
+    s.line_far_rows = 0
+    s.line_q3_row_ptr = s.line_q1_row_ptr  # no line through two equal row_ptr values
+    assert pf.select(s, "f64", "flat").guess_a == 0.0
+    s.line_q3_row_ptr = 5 * (3 * m // 4) - 2048
+    s.max_row_len = 65
+    assert pf.select(s, "f64", "flat").guess_a == 0.0
+
+
 def run_for(ntiles, resident, cap=16):
     return max(1, min(cap, -(-ntiles // resident)))
 
