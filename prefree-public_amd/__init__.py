@@ -112,7 +112,8 @@ class SpmvArgs(ctypes.Structure):
                 ("long_deal_bytes", ctypes.c_size_t), ("long_row_tiles_bytes", ctypes.c_size_t),
                 ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int),
                 ("aux_stream", ctypes.c_void_p), ("ev_fork", ctypes.c_void_p), ("ev_join", ctypes.c_void_p),
-                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double)]
+                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double),
+                ("row_apart", ctypes.c_void_p), ("row_apart_bytes", ctypes.c_size_t)]
 
 
 _lib = None

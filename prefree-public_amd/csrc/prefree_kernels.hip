@@ -2251,11 +2251,9 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
 // order: deterministic).  One thread per row walking 123 windows took 34 us
 // on C5; a wave per row takes a few.
 template <typename T>
-__global__ __launch_bounds__(kBS) void k_dense_sum(Args<T> a, DenseArgs d)
+__device__ __forceinline__ void dense_sum_row(const Args<T> &a, const DenseArgs &d, int i, int lane)
 {
     using P = acc_t<T>;
-    const int i = blockIdx.x * kWaves + (int)threadIdx.x / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
     if (i >= d.nd)
         return;  // whole wave
     const int r = d.rows[i];
@@ -2267,6 +2265,12 @@ __global__ __launch_bounds__(kBS) void k_dense_sum(Args<T> a, DenseArgs d)
         sum += pp[w];
     sum = wave_sum(sum);
     if (lane == 0) a.y[r] = T(sum);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_dense_sum(Args<T> a, DenseArgs d)
+{
+    dense_sum_row<T>(a, d, blockIdx.x * kWaves + (int)threadIdx.x / kWave, threadIdx.x & (kWave - 1));
 }
 
 // Planning scan of a hybrid plan: every row of at least `dmin` nnz goes to the
@@ -2393,11 +2397,9 @@ __global__ __launch_bounds__(kBS) void k_long(Args<T> a, LongArgs L)
 // y of each long row from its tiles' partials: one wave per row, lane j adding
 // tiles j, j + 64, ... in order, then the wave's DPP tree (a fixed order).
 template <typename T>
-__global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
+__device__ __forceinline__ void long_sum_row(const Args<T> &a, const LongArgs &L, int i, int lane)
 {
     using P = acc_t<T>;
-    const int i = blockIdx.x * kWaves + (int)threadIdx.x / kWave;
-    const int lane = threadIdx.x & (kWave - 1);
     if (i >= L.nrows)
         return;  // whole wave
     const int r = L.rows[i];
@@ -2413,6 +2415,33 @@ __global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
         sum += pp[t];
     sum = wave_sum(sum);
     if (lane == 0) a.y[r] = T(sum);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
+{
+    long_sum_row<T>(a, L, blockIdx.x * kWaves + (int)threadIdx.x / kWave, threadIdx.x & (kWave - 1));
+}
+
+// Hybrid plans with x halves: the first hblocks workgroups form y = y + y2
+// over the rows not summed apart (apart[r] == 0), as k_rows_halves_add does,
+// and the others combine the rows summed apart, one wave per row, as
+// k_dense_sum (LONG false) or k_long_sum (LONG true) do; neither part writes
+// the other's rows, so one launch does both.
+template <typename T, bool LONG>
+__global__ __launch_bounds__(kBS) void k_combine(Args<T> a, DenseArgs d, LongArgs L,
+                                                 const unsigned char *__restrict__ apart, int hblocks)
+{
+    if ((int)blockIdx.x < hblocks) {
+        for (long long r = (long long)blockIdx.x * kBS + threadIdx.x; r < a.m; r += (long long)hblocks * kBS)
+            if (!apart[r]) a.y[r] = T(acc_t<T>(a.y[r]) + acc_t<T>(a.y2[r]));
+        return;
+    }
+    const int i = ((int)blockIdx.x - hblocks) * kWaves + (int)threadIdx.x / kWave;
+    if constexpr (LONG)
+        long_sum_row<T>(a, L, i, threadIdx.x & (kWave - 1));
+    else
+        dense_sum_row<T>(a, d, i, threadIdx.x & (kWave - 1));
 }
 
 // Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
@@ -3611,16 +3640,26 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
         }
         return PF_OK;
     };
-    if (!fork) PFK_TRY(halves_add());
+    // With the rows summed apart marked, the halves' add joins their combine (one launch at the end)
+    const bool fuse = a->ntiles > 0 && halves && a->row_apart;
+    const int hblocks = fuse ? (int)grid_for(a->m, kBS, 8192) : 0;
+    const unsigned sblocks = (unsigned)((a->n_dense + kWaves - 1) / kWaves);
+    if (!fork && !fuse) PFK_TRY(halves_add());
     if (a->long_mode) {
         const LongArgs L{reinterpret_cast<const int4 *>(a->long_tiles), a->long_deal, a->long_row_tiles,
                          a->dense_rows, a->n_dense, a->n_long_tiles, a->long_part};
         const unsigned lgrid = (unsigned)(kXcds * ((a->n_long_tiles + kXcds - 1) / kXcds));
         hipLaunchKernelGGL((k_long<T>), dim3(lgrid), dim3(kBS), 0, S(stream), r, L);
         PFK_LAUNCHED("k_long");
-        if (fork) { PFK_TRY(join()); PFK_TRY(halves_add()); }
-        hipLaunchKernelGGL((k_long_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0,
-                           S(stream), r, L);
+        if (fork) PFK_TRY(join());
+        if (fuse) {
+            hipLaunchKernelGGL((k_combine<T, true>), dim3((unsigned)hblocks + sblocks), dim3(kBS), 0, S(stream), r,
+                               DenseArgs{}, L, a->row_apart, hblocks);
+            PFK_LAUNCHED("k_combine");
+            return PF_OK;
+        }
+        if (fork) PFK_TRY(halves_add());
+        hipLaunchKernelGGL((k_long_sum<T>), dim3(sblocks), dim3(kBS), 0, S(stream), r, L);
         PFK_LAUNCHED("k_long_sum");
         return PF_OK;
     }
@@ -3634,8 +3673,15 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     else
         hipLaunchKernelGGL((k_dense<T, kFlatSearch>), dim3(dgrid), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense");
-    if (fork) { PFK_TRY(join()); PFK_TRY(halves_add()); }
-    hipLaunchKernelGGL((k_dense_sum<T>), dim3((unsigned)((a->n_dense + kWaves - 1) / kWaves)), dim3(kBS), 0, S(stream), r, d);
+    if (fork) PFK_TRY(join());
+    if (fuse) {
+        hipLaunchKernelGGL((k_combine<T, false>), dim3((unsigned)hblocks + sblocks), dim3(kBS), 0, S(stream), r, d,
+                           LongArgs{}, a->row_apart, hblocks);
+        PFK_LAUNCHED("k_combine");
+        return PF_OK;
+    }
+    if (fork) PFK_TRY(halves_add());
+    hipLaunchKernelGGL((k_dense_sum<T>), dim3(sblocks), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense_sum");
     return PF_OK;
 }
@@ -3699,7 +3745,8 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
         (!a->long_mode && a->dense_seg &&
          !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")) ||
         (a->x_halves && !room(a->half_part, a->half_part_bytes, (long long)a->m * (dtype == PF_F64 ? 8 : 4),
-                              "x-halves row sums")))
+                              "x-halves row sums")) ||
+        (a->row_apart && !room(a->row_apart, a->row_apart_bytes, (long long)a->m, "rows summed apart")))
         return PF_ERR_INVALID;
     if (dtype == PF_F64) return a->tile == 1024 ? launch_hybrid<double, 1024>(a, stream) : launch_hybrid<double, 2048>(a, stream);
     return a->tile == 1024 ? launch_hybrid<float, 1024>(a, stream) : launch_hybrid<float, 2048>(a, stream);

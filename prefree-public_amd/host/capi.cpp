@@ -464,6 +464,8 @@ struct pf_plan {
     bool x_halves = false;       // run tiles processed per half of x (see pfk_spmv_args.x_halves)
     void *half_part = nullptr;   // [m] second-half row sums
     size_t half_part_bytes = 0;
+    unsigned char *row_apart = nullptr;  // [m] 1 for the rows summed apart (see pfk_spmv_args.row_apart)
+    size_t row_apart_bytes = 0;
     // long mode: the long rows (dense_rows) cut into tiles of PFK_LONG_TILE nnz instead of x windows
     bool long_mode = false;
     int n_long_tiles = 0;
@@ -692,9 +694,10 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
                  b_seg = dense ? up((size_t)nd * (nwin + 1) * 4) : 0,
                  b_part = dense ? up((size_t)nd * nwin * slot_bytes(dtype)) : up((size_t)nlt * slot_bytes(dtype)),
                  b_lt = up((size_t)nlt * 16), b_deal = up((size_t)nlt * 4), b_rt = lng ? up(((size_t)nd + 1) * 4) : 0,
-                 b_half = up((size_t)p->m * value_bytes(dtype));
+                 b_half = up((size_t)p->m * value_bytes(dtype)), b_apart = up((size_t)p->m);
     void *w = nullptr;
-    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_lt + b_deal + b_rt + b_half), "hybrid tables");
+    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_lt + b_deal + b_rt + b_half + b_apart),
+           "hybrid tables");
     char *c = static_cast<char *>(w);
     p->ws_hyb = w;
     p->dense_rows = reinterpret_cast<int *>(c);
@@ -715,6 +718,9 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     c += b_rt;
     p->half_part = c;
     p->half_part_bytes = b_half;
+    c += b_half;
+    p->row_apart = reinterpret_cast<unsigned char *>(c);
+    p->row_apart_bytes = b_apart;
     p->runs_bytes = b_runs;
     p->run_map_bytes = b_map;
     p->dense_seg_bytes = b_seg;
@@ -740,6 +746,9 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
     // rows the runs never write (the long rows) keep a zero second-half sum
     if (st == PF_OK) st = pfk_fill_zero(p->half_part, b_half, stream);
+    std::vector<unsigned char> apart((size_t)p->m, 0);
+    for (long long i = 0; i < nd; ++i) apart[(size_t)rows[(size_t)i]] = 1;
+    if (st == PF_OK && p->m > 0) st = pfk_memcpy_h2d(p->row_apart, apart.data(), apart.size(), stream);
     if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
     if (st == PF_OK && lng) {
         // deal: the tiles ordered by their first column, XCD k taking the k-th eighth
@@ -1130,6 +1139,8 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         a.x_halves = plan->x_halves ? 1 : 0;
         a.half_part = plan->half_part;
         a.half_part_bytes = plan->half_part_bytes;
+        a.row_apart = plan->row_apart;
+        a.row_apart_bytes = plan->row_apart_bytes;
         a.long_mode = plan->long_mode ? 1 : 0;
         a.n_long_tiles = plan->n_long_tiles;
         a.long_tiles = plan->long_tiles;

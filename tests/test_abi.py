@@ -354,12 +354,15 @@ def _hyb_args(**kw):
                                               ("long_row_tiles_bytes", 12, b"long-row tile index"),
                                               ("long_part_bytes", 20 * 4, b"long-row partial sums"),
                                               ("long_deal", None, b"missing tables"),
-                                              ("n_long_tiles", 0, b"missing tables")])
+                                              ("n_long_tiles", 0, b"missing tables"),
+                                              ("row_apart_bytes", 999, b"rows summed apart")])
 def test_hybrid_long_mode_tables_checked(field, value, what):
     # pfk_spmv_hybrid in long mode refuses a short or missing long-row table before any launch
     K = pf.klib()
     K.pfk_spmv_hybrid.argtypes = [ctypes.c_int, ctypes.POINTER(pf.SpmvArgs), ctypes.c_void_p]
     a = _hyb_args(**{field: value})
+    if field == "row_apart_bytes":  # one byte per row (m = 1000), checked when the table is given
+        a.row_apart = 0x30000
     assert K.pfk_spmv_hybrid(pf.F64, ctypes.byref(a), None) == 1
     assert what in K.pfk_last_error()
 
