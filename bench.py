@@ -299,10 +299,12 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
                      "traffic_gbps": round(traffic / (ev_ms * 1e6), 1) if traffic else None,
                      "traffic_key": key,
                      "note": ("step = k_rows over the runs of short rows + k_long over the long rows' tiles "
-                              "+ k_long_sum (+ k_rows_halves_add with x halves); launch_ms covers them all"
+                              "+ k_long_sum (k_combine, which also adds the x halves, with x halves); "
+                              "launch_ms covers them all"
                               if info["hybrid"] and info["long_tiles"] else
                               "step = k_rows over the runs of short rows + k_dense over the dense rows' x windows "
-                              "+ k_dense_sum (+ k_rows_halves_add with x halves); launch_ms covers them all"
+                              "+ k_dense_sum (k_combine, which also adds the x halves, with x halves); "
+                              "launch_ms covers them all"
                               if info["hybrid"] else
                               "step = tile kernel + split-row combine kernel; launch_ms covers both"
                               if info["needs_fixup"] else "step = one tile-kernel launch")},

@@ -16,7 +16,9 @@
 //    x windows staged in LDS, a partial per (row, window), added in order.
 //  * k_long<T> + k_long_sum  (hybrid plans, long mode)  Long rows cut into
 //    1024-nnz tiles dealt to the XCDs by first column, partials added in order.
-//  * k_rows_halves_add  y = first half's row sums + second half's.
+//  * k_combine<T, LONG>  (hybrid plans with x halves)  y = first half's row
+//    sums + second half's over the runs' rows, and the dense or long rows'
+//    combine, in one launch; k_rows_halves_add the add alone.
 //  * k_flat<T, K, MODE>  (PF_FLAT 1024 / 2048, rows longer than 256 nnz)  The
 //    same nnz tiles with rows cut at tile edges; k_fixup combines the pieces.
 //    With the x-window schedule (sched_tile) tiles go to the XCDs by the part
