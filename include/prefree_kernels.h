@@ -118,9 +118,9 @@ typedef struct pfk_spmv_args {
        row guess_a * v + guess_b, 64 rows apart by 1; else on v * m / nnz, guess_spread apart.  Any values give
        the same rows (a round that does not bracket the key is followed by wider ones). */
     double guess_a, guess_b;
-    /* Hybrid plans with x halves: [m] bytes, 1 for the rows summed apart (dense_rows), 0 for the others.  When
-       given, the halves' add (y += half_part over the runs' rows) and the combine of the rows summed apart are
-       one launch (neither writes the other's rows); NULL: two launches. */
+    /* Hybrid plans with x halves (required then): [m] bytes, 1 for the rows summed apart (dense_rows), 0 for the
+       others, so that the halves' add (y += half_part over the runs' rows) and the combine of the rows summed
+       apart are one launch (neither writes the other's rows). */
     const unsigned char *row_apart;
     size_t row_apart_bytes;
 } pfk_spmv_args;

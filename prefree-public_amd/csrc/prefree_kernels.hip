@@ -18,7 +18,7 @@
 //    1024-nnz tiles dealt to the XCDs by first column, partials added in order.
 //  * k_combine<T, LONG>  (hybrid plans with x halves)  y = first half's row
 //    sums + second half's over the runs' rows, and the dense or long rows'
-//    combine, in one launch; k_rows_halves_add the add alone.
+//    combine, in one launch.
 //  * k_flat<T, K, MODE>  (PF_FLAT 1024 / 2048, rows longer than 256 nnz)  The
 //    same nnz tiles with rows cut at tile edges; k_fixup combines the pieces.
 //    With the x-window schedule (sched_tile) tiles go to the XCDs by the part
@@ -116,7 +116,7 @@ struct Args {
     int *__restrict__ err;
     int *__restrict__ sched;      // split-row FLAT x-window schedule (see k_flat), or null
     long long sched_cap;          // tiles per XCD list
-    T *__restrict__ y2;           // x-halves runs: the second half's row sums (k_rows_halves_add adds them to y)
+    T *__restrict__ y2;           // x-halves runs: the second half's row sums (k_combine adds them to y)
     int ovf_cap;                  // row-aligned tiles: longest row (at most kAlignRowMax); 0 = unknown
 };
 
@@ -2310,13 +2310,6 @@ __global__ __launch_bounds__(kBS) void k_dense_sorted(const int *__restrict__ co
 }
 
 // x-halves runs: y = (first half's row sum) + (second half's), in that order.
-template <typename T>
-__global__ __launch_bounds__(kBS) void k_rows_halves_add(T *__restrict__ y, const T *__restrict__ y2, int m)
-{
-    for (long long r = (long long)blockIdx.x * kBS + threadIdx.x; r < m; r += (long long)gridDim.x * kBS)
-        y[r] = T(acc_t<T>(y[r]) + acc_t<T>(y2[r]));
-}
-
 // ---- k_long: long rows of a hybrid plan in long mode -------------------------
 //
 // A matrix whose long rows (over PFK_ALIGN_ROW_MAX nnz) are not all dense rows
@@ -2426,8 +2419,7 @@ __global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
 }
 
 // Hybrid plans with x halves: the first hblocks workgroups form y = y + y2
-// over the rows not summed apart (apart[r] == 0), as k_rows_halves_add does,
-// and the others combine the rows summed apart, one wave per row, as
+// over the rows not summed apart (apart[r] == 0), and the others combine the rows summed apart, one wave per row, as
 // k_dense_sum (LONG false) or k_long_sum (LONG true) do; neither part writes
 // the other's rows, so one launch does both.
 template <typename T, bool LONG>
@@ -3632,21 +3624,11 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     else
         hipLaunchKernelGGL((k_rows<T, K, kFlatSearch, false, true>), rgrid, dim3(kBS), 0, S(rs), r, a->run_map, nullptr, rt);
     if (a->ntiles > 0) PFK_LAUNCHED("k_rows (runs)");
-    // y = first half + second half over every row (a dense or long row's y is
-    // written after it, by its own combine)
-    const auto halves_add = [&]() -> int {
-        if (a->ntiles > 0 && halves) {
-            hipLaunchKernelGGL((k_rows_halves_add<T>), dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream), r.y,
-                               r.y2, a->m);
-            PFK_LAUNCHED("k_rows_halves_add");
-        }
-        return PF_OK;
-    };
-    // With the rows summed apart marked, the halves' add joins their combine (one launch at the end)
-    const bool fuse = a->ntiles > 0 && halves && a->row_apart;
+    // With x halves, y = first half + second half over the runs' rows joins the
+    // combine of the rows summed apart (one launch at the end)
+    const bool fuse = a->ntiles > 0 && halves;
     const int hblocks = fuse ? (int)grid_for(a->m, kBS, 8192) : 0;
     const unsigned sblocks = (unsigned)((a->n_dense + kWaves - 1) / kWaves);
-    if (!fork && !fuse) PFK_TRY(halves_add());
     if (a->long_mode) {
         const LongArgs L{reinterpret_cast<const int4 *>(a->long_tiles), a->long_deal, a->long_row_tiles,
                          a->dense_rows, a->n_dense, a->n_long_tiles, a->long_part};
@@ -3660,7 +3642,6 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
             PFK_LAUNCHED("k_combine");
             return PF_OK;
         }
-        if (fork) PFK_TRY(halves_add());
         hipLaunchKernelGGL((k_long_sum<T>), dim3(sblocks), dim3(kBS), 0, S(stream), r, L);
         PFK_LAUNCHED("k_long_sum");
         return PF_OK;
@@ -3682,7 +3663,6 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
         PFK_LAUNCHED("k_combine");
         return PF_OK;
     }
-    if (fork) PFK_TRY(halves_add());
     hipLaunchKernelGGL((k_dense_sum<T>), dim3(sblocks), dim3(kBS), 0, S(stream), r, d);
     PFK_LAUNCHED("k_dense_sum");
     return PF_OK;
@@ -3748,7 +3728,7 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
          !room(a->dense_seg, a->dense_seg_bytes, nd * (nw + 1) * 4, "dense segment bounds")) ||
         (a->x_halves && !room(a->half_part, a->half_part_bytes, (long long)a->m * (dtype == PF_F64 ? 8 : 4),
                               "x-halves row sums")) ||
-        (a->row_apart && !room(a->row_apart, a->row_apart_bytes, (long long)a->m, "rows summed apart")))
+        (a->x_halves && !room(a->row_apart, a->row_apart_bytes, (long long)a->m, "rows summed apart")))
         return PF_ERR_INVALID;
     if (dtype == PF_F64) return a->tile == 1024 ? launch_hybrid<double, 1024>(a, stream) : launch_hybrid<double, 2048>(a, stream);
     return a->tile == 1024 ? launch_hybrid<float, 1024>(a, stream) : launch_hybrid<float, 2048>(a, stream);

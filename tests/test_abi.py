@@ -361,8 +361,8 @@ def test_hybrid_long_mode_tables_checked(field, value, what):
     K = pf.klib()
     K.pfk_spmv_hybrid.argtypes = [ctypes.c_int, ctypes.POINTER(pf.SpmvArgs), ctypes.c_void_p]
     a = _hyb_args(**{field: value})
-    if field == "row_apart_bytes":  # one byte per row (m = 1000), checked when the table is given
-        a.row_apart = 0x30000
+    if field == "row_apart_bytes":  # with x halves, one byte per row (m = 1000) is required
+        a.row_apart, a.x_halves, a.half_part, a.half_part_bytes = 0x30000, 1, 0x30000, 8000
     assert K.pfk_spmv_hybrid(pf.F64, ctypes.byref(a), None) == 1
     assert what in K.pfk_last_error()
 
