@@ -386,16 +386,12 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
             return out
 
         own = search_time(None)
-        best = own
         if (info["variant_name"] == "flat" and info["row_aligned"] and info["tile"] == 1024 and not info.get("hybrid")
                 and info["ntiles"] >= 2048):
-            alt = search_time(2048)
-            if alt["kernel_ms"] < own["kernel_ms"]:
-                best = dict(alt, same_tile=own)
-            else:
-                best = dict(own, tile_2048=alt)
-        rec["search"] = dict(best, what="every call searches row_ptr for each tile's rows inside the tile kernel; "
-                                        "vs_recorded_rows against the hot plan's recorded-rows time")
+            own = dict(own, tile_2048=search_time(2048))
+        rec["search"] = dict(own, what="every call searches row_ptr for each tile's rows inside the tile kernel, with "
+                                       "the plan's own tile (tile_2048: the same with 2048-nnz tiles); "
+                                       "vs_recorded_rows against the hot plan's recorded-rows time")
 
     # The drop-in boundary (preFreeSpMV) takes host buffers: one SpMV including
     # the host->device copies of the CSR and x, planning and the copy of y back.
@@ -611,6 +607,28 @@ def main():
         "configs": records,
     }
     print(json.dumps(result), flush=True)
+    print_summary(records)
+
+
+def print_summary(records):
+    """One short line per configuration on stderr, after the JSON line: a reader of the end of the output
+    sees every configuration even when the start of the long JSON line is cut off."""
+    def f(v, fmt):
+        return format(v, fmt) if isinstance(v, (int, float)) else "-"
+
+    for name, r in records.items():
+        rot, cold, srch = r.get("rotated") or {}, r.get("cold") or {}, r.get("search") or {}
+        roof, par, cpu = r["roofline"], r.get("parity") or {}, r.get("cpu_baseline") or {}
+        ratio = roof["traffic"] / roof["algorithmic_bytes"] if roof.get("traffic") else None
+        plan = r["variant"] + f"-{r['tile']}" + ("-rows" if r["row_aligned"] else "") + (
+            ("-long" if r["long_tiles"] else "-dense") + ("-halves" if r["x_halves"] else "") if r["hybrid"] else "")
+        print(f"summary {name}: plan={plan} kernel_us={f(r['kernel_ms'] * 1e3, '.2f')} "
+              f"frac={f(roof['frac'], '.4f')} rotated_frac={f(rot.get('frac'), '.4f')} "
+              f"cold_frac={f(cold.get('frac'), '.4f')} search_x={f(srch.get('vs_recorded_rows'), '.3f')} "
+              f"traffic_ratio={f(ratio, '.2f')} plan_ms={f(r['plan_ms'], '.3f')} "
+              f"parity={'ok' if par.get('ok') else ('FAIL' if par else '-')} "
+              f"max_err={f(par.get('max_rownorm_err_vs_cpu'), '.1e')} gpu_gflops={f(r['gflops'], '.1f')} "
+              f"cpu_gflops={f(cpu.get('value'), '.1f')}", file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":

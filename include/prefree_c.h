@@ -239,14 +239,17 @@ const char *pf_tuning_table(void);
 int pf_spmv(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
             int m, int n, int nnz, int dtype, int variant, void *stream);
 
-/* No counterpart in the reference: pf_spmv for callers that cannot allocate device memory (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments, result and
- * errors as pf_spmv, but no hipMalloc / hipFree and no allocating library call: the row statistics and
- * the plan's workspace live in a fixed 8 MiB device array of the library (PFK_SCRATCH_BYTES, one per
- * device, kept until the process ends).  Matrices whose workspace does not fit are refused with
- * PF_ERR_UNSUPPORTED before any launch (about 230M nnz for fp64 FLAT 2048-nnz tiles, 120M for
- * 1024-nnz tiles; pf_last_error gives the bytes needed).  Synchronises `stream`.  Calls that overlap on
- * one device (two streams, two host threads) share that array and race: order them. */
+/* No counterpart in the reference: pf_spmv for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, result and errors as pf_spmv, but no
+ * hipMalloc / hipFree and no allocating library call: the row statistics and the plan's workspace live in
+ * a fixed 8 MiB device array of the library (PFK_SCRATCH_BYTES, one per device, kept until the process
+ * ends).  Matrices whose workspace does not fit are refused with PF_ERR_UNSUPPORTED before any launch
+ * (about 230M nnz for fp64 FLAT 2048-nnz tiles, 120M for 1024-nnz tiles; pf_last_error gives the bytes
+ * needed).  It copies the row statistics to the host and synchronises `stream` twice, so it must not be
+ * called on a stream that is capturing a HIP graph: a caller who captures makes a plan before the capture
+ * (pf_plan_create) and captures pf_plan_execute.  Calls on one device from several host threads are
+ * serialised by a per-device lock in this library, since they share the one array; each call has
+ * finished with it when it returns. */
 int pf_spmv_noalloc(const int *d_row_ptr, const int *d_col, const void *d_val, const void *d_x, void *d_y,
                     int m, int n, int nnz, int dtype, int variant, void *stream);
 

@@ -118,9 +118,10 @@ typedef struct pfk_spmv_args {
        row guess_a * v + guess_b, 64 rows apart by 1; else on v * m / nnz, guess_spread apart.  Any values give
        the same rows (a round that does not bracket the key is followed by wider ones). */
     double guess_a, guess_b;
-    /* Hybrid plans with x halves (required then): [m] bytes, 1 for the rows summed apart (dense_rows), 0 for the
-       others, so that the halves' add (y += half_part over the runs' rows) and the combine of the rows summed
-       apart are one launch (neither writes the other's rows). */
+    /* Hybrid plans with x halves (required then): [m] bytes, 1 for the rows summed apart (dense_rows), 0 for
+       every other row, so that the halves' add (y += half_part over the runs' rows) and the combine of the rows
+       summed apart are one launch (neither writes the other's rows).  A row summed apart whose byte is not 1 is
+       left unwritten and sets the error flag; a run row marked 1 loses its second half's sum (not detected). */
     const unsigned char *row_apart;
     size_t row_apart_bytes;
 } pfk_spmv_args;
@@ -209,10 +210,10 @@ int pfk_probe_gather(int dtype, const int *idx, long long count, const void *x, 
                      long long out_len, int policy, void *stream);
 
 /* No counterpart in the reference.  Device scratch for pf_spmv_noalloc, the entry point for callers that
- * cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc): a
- * file-scope __device__ array of PFK_SCRATCH_BYTES bytes, 256-byte aligned, one copy per device, held
- * until the process ends.  Writes the current device's address of it (looked up once per device with
- * hipGetSymbolAddress) and its size.  Every user on one device shares the same bytes. */
+ * cannot allocate (serving loops, harnesses that forbid hipMalloc): a file-scope __device__ array of
+ * PFK_SCRATCH_BYTES bytes, 256-byte aligned, one copy per device, held until the process ends.  Writes the
+ * current device's address of it (looked up once per device with hipGetSymbolAddress) and its size.
+ * Every user on one device shares the same bytes. */
 #define PFK_SCRATCH_BYTES (8u << 20)
 int pfk_scratch(void **ptr, size_t *bytes);
 
@@ -234,6 +235,7 @@ int pfk_event_record(void *e, void *s);
 int pfk_event_sync(void *e);
 int pfk_event_elapsed_ms(float *ms, void *start, void *stop);
 int pfk_device_count(int *n);
+int pfk_get_device(int *dev);  /* the calling thread's current device */
 int pfk_device_name(char *buf, int len);
 const char *pfk_last_error(void);
 

@@ -2309,7 +2309,6 @@ __global__ __launch_bounds__(kBS) void k_dense_sorted(const int *__restrict__ co
         atomicAdd(counters + 1, 1);
 }
 
-// x-halves runs: y = (first half's row sum) + (second half's), in that order.
 // ---- k_long: long rows of a hybrid plan in long mode -------------------------
 //
 // A matrix whose long rows (over PFK_ALIGN_ROW_MAX nnz) are not all dense rows
@@ -2418,10 +2417,13 @@ __global__ __launch_bounds__(kBS) void k_long_sum(Args<T> a, LongArgs L)
     long_sum_row<T>(a, L, blockIdx.x * kWaves + (int)threadIdx.x / kWave, threadIdx.x & (kWave - 1));
 }
 
-// Hybrid plans with x halves: the first hblocks workgroups form y = y + y2
-// over the rows not summed apart (apart[r] == 0), and the others combine the rows summed apart, one wave per row, as
-// k_dense_sum (LONG false) or k_long_sum (LONG true) do; neither part writes
-// the other's rows, so one launch does both.
+// Hybrid plans with x halves: y = (first half's row sum) + (second half's),
+// in that order.  The first hblocks workgroups form y = y + y2 over the rows
+// not summed apart (apart[r] == 0), and the others combine the rows summed
+// apart, one wave per row, as k_dense_sum (LONG false) or k_long_sum (LONG
+// true) do; neither part writes the other's rows, so one launch does both.
+// A row summed apart whose apart byte is not 1 would be written by both parts:
+// the combining wave skips it and sets the error flag.
 template <typename T, bool LONG>
 __global__ __launch_bounds__(kBS) void k_combine(Args<T> a, DenseArgs d, LongArgs L,
                                                  const unsigned char *__restrict__ apart, int hblocks)
@@ -2432,10 +2434,18 @@ __global__ __launch_bounds__(kBS) void k_combine(Args<T> a, DenseArgs d, LongArg
         return;
     }
     const int i = ((int)blockIdx.x - hblocks) * kWaves + (int)threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (i >= (LONG ? L.nrows : d.nd))
+        return;  // whole wave
+    const int r = LONG ? L.rows[i] : d.rows[i];
+    if (r >= 0 && r < a.m && apart[r] != 1) {  // whole wave
+        if (lane == 0) atomicOr(a.err, 1);
+        return;
+    }
     if constexpr (LONG)
-        long_sum_row<T>(a, L, i, threadIdx.x & (kWave - 1));
+        long_sum_row<T>(a, L, i, lane);
     else
-        dense_sum_row<T>(a, d, i, threadIdx.x & (kWave - 1));
+        dense_sum_row<T>(a, d, i, lane);
 }
 
 // Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
@@ -4054,6 +4064,8 @@ int pfk_event_elapsed_ms(float *ms, void *start, void *stop)
 }
 
 int pfk_device_count(int *n) { PFK_HIP(hipGetDeviceCount(n)); return PF_OK; }
+
+int pfk_get_device(int *dev) { PFK_HIP(hipGetDevice(dev)); return PF_OK; }
 
 int pfk_device_name(char *buf, int len)
 {

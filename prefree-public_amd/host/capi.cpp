@@ -746,8 +746,16 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
     // rows the runs never write (the long rows) keep a zero second-half sum
     if (st == PF_OK) st = pfk_fill_zero(p->half_part, b_half, stream);
+    // exactly one byte set per row summed apart, 0 for every other row (the combine relies on it)
     std::vector<unsigned char> apart((size_t)p->m, 0);
-    for (long long i = 0; i < nd; ++i) apart[(size_t)rows[(size_t)i]] = 1;
+    long long marked = 0;
+    for (long long i = 0; i < nd; ++i) {
+        unsigned char &b = apart[(size_t)rows[(size_t)i]];
+        marked += b == 0 ? 1 : 0;
+        b = 1;
+    }
+    if (st == PF_OK && marked != nd)
+        return fail(PF_ERR_KERNEL, "hybrid plan: the planning scan listed a row twice");
     if (st == PF_OK && p->m > 0) st = pfk_memcpy_h2d(p->row_apart, apart.data(), apart.size(), stream);
     if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
     if (st == PF_OK && lng) {
@@ -890,6 +898,12 @@ int check_csr_stats(const pf_row_stats &s, int nnz)
 // Bytes of pf_spmv_noalloc's scratch taken by the row statistics block; the
 // workspace starts after it, 256-byte aligned.
 constexpr size_t kNoallocStatsBytes = 512;
+
+// pf_spmv_noalloc's calls on one device share its one scratch array: a lock
+// per device (the kernel layer keeps scratch for devices 0..63) serialises
+// calls from several host threads.
+constexpr int kNoallocDevices = 64;
+std::mutex g_noalloc_mu[kNoallocDevices];
 
 }  // namespace
 
@@ -1252,6 +1266,10 @@ int pf_spmv_noalloc(const int *d_row_ptr, const int *d_col, const void *d_val, c
     size_t scr_bytes = 0;
     PF_TRY(pfk_scratch(&scr, &scr_bytes), "scratch");
     if (scr_bytes < kNoallocStatsBytes + 256) return fail(PF_ERR_UNSUPPORTED, "scratch too small");
+    int dev = 0;
+    PF_TRY(pfk_get_device(&dev), "current device");
+    if (dev < 0 || dev >= kNoallocDevices) return fail(PF_ERR_UNSUPPORTED, "device index beyond the scratch table");
+    std::lock_guard<std::mutex> scratch_lock(g_noalloc_mu[dev]);  // held until the stream is synchronised below
     pf_plan p;  // on the stack: no allocation of any kind
     p.m = m;
     p.n = n;

@@ -66,3 +66,51 @@ def test_noalloc_matches_pf_spmv(pair, variant, dtype):
         if kat:
             assert np.array_equal(got, oracle.spmv_serial(rp, col, val, x))
 
+
+
+def test_noalloc_two_host_threads():
+    """Two host threads call pf_spmv_noalloc at once on their own streams and matrices, several times each:
+    the per-device lock orders their use of the one scratch array, so every result equals pf_spmv's."""
+    import threading
+
+    f = _noalloc()
+    jobs = []
+    for cfg, scale in ((3, 200000), (5, 20000)):
+        rp, col, v = pf.synth_csr(cfg, seed=7, scale_n=scale, dtypes=("f64",))
+        x = pf.synth_x(cfg, len(rp) - 1, seed=7, dtypes=("f64",))["f64"]
+        want = _reference(rp, col, v["f64"], x, "f64", "auto")
+        m, n, nnz = len(rp) - 1, len(x), len(col)
+        bufs = (dev(rp), dev(col), dev(v["f64"]), dev(x))
+        y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+        jobs.append((bufs, y, m, n, nnz, want, torch.cuda.Stream()))
+    torch.cuda.synchronize()
+    rounds = 6
+    start = threading.Barrier(len(jobs))
+    failures = []
+
+    def worker(k):
+        (d_rp, d_col, d_val, d_x), y, m, n, nnz, want, s = jobs[k]
+        try:
+            for it in range(rounds):
+                y.fill_(float("nan"))
+                torch.cuda.synchronize()
+                start.wait()
+                st = f(d_rp.data_ptr(), d_col.data_ptr(), d_val.data_ptr(), d_x.data_ptr(), y.data_ptr(), m, n, nnz,
+                       pf.dtype_code("f64"), pf.variant_code("auto"), s.cuda_stream)
+                if st != 0:
+                    failures.append(f"thread {k} call {it}: status {st}")
+                    continue
+                got = y.cpu().numpy()  # the call synchronised its stream before returning
+                if not np.array_equal(got, want):
+                    failures.append(f"thread {k} call {it}: {np.count_nonzero(got != want)} rows differ")
+        except Exception as e:  # reported below; a thread's exception would otherwise be lost
+            failures.append(f"thread {k}: {e!r}")
+            start.abort()
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not failures, failures
