@@ -79,6 +79,8 @@ def kernel_name(info):
         return "k_wave"
     if v == "prefree":
         return "k_prefree"
+    if info["row_aligned"] and info.get("band_w"):
+        return "k_band"
     return {256: "k_flow", 4096: "k_tiles"}.get(info["tile"], "k_rows" if info["row_aligned"] else "k_flat")
 
 
@@ -197,6 +199,22 @@ class Stepper:
         return host_ms, ev_ms, median, desc
 
 
+def prewarm(pf, torch):
+    """One plan and call on a small matrix before anything is timed: the process's first use of the kernel
+    library loads its code and sets up the device, a cost no later plan pays (it would otherwise land in the
+    first configuration's plan_ms)."""
+    import numpy as np
+
+    rp, col, vals = pf.synth_csr(2, seed=1, scale_n=64, dtypes=("f64",))
+    dev = torch.device("cuda:0")
+    m = len(rp) - 1
+    d = [torch.from_numpy(a).to(dev) for a in (rp, col, vals["f64"], np.ones(m))]
+    y = torch.empty(m, dtype=torch.float64, device=dev)
+    with pf.Plan(d[0], d[1], m, m, len(col), "f64", "auto") as p:
+        p.execute(d[0], d[1], d[2], d[3], y)
+    torch.cuda.synchronize()
+
+
 def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
     """One configuration: every leg of the module docstring.  Returns its record."""
     import numpy as np
@@ -236,11 +254,16 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
             p.set_hybrid(False)
         if args.x_halves >= 0 and p.info.hybrid:
             p.set_x_halves(args.x_halves)
+        if args.band == 0 and p.info.band_w:
+            p.set_band(False)
+        elif args.band == 1 and not p.info.band_w:
+            p.set_band(True)
         return p
 
     t_plan = time.perf_counter()
     plan = make_plan()
     t_plan = (time.perf_counter() - t_plan) * 1e3
+    plan_wall, plan_gpu = plan.timing
     info = plan.info.as_dict()
     deterministic = info["variant_name"] != "prefree"   # PREFREE adds tile-boundary rows with atomics
 
@@ -269,7 +292,8 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
     gbs = bytes_eff / (ev_ms * 1e6)
     key = f"C{cfg}-{dt}-{info['variant_name']}-{info['tile']}" + (
         f"-r{info['run_tiles']}" if info["variant_name"] == "adaptive" else "") + (
-        "-rows" if info["row_aligned"] else "") + (("-long" if info["long_tiles"] else "-hybrid") if info["hybrid"] else "")
+        "-rows" if info["row_aligned"] else "") + ("-band" if info.get("band_w") else "") + (
+        ("-long" if info["long_tiles"] else "-hybrid") if info["hybrid"] else "")
     traffic = traffic_from_profiles(key)
     rec = {
         "workload": WORKLOADS[cfg] + {"f64": "", "f32": " (fp32)", "f16": " (fp16)"}[dt],
@@ -280,10 +304,17 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         "row_aligned": bool(info["row_aligned"]), "x_windows": bool(info["x_windows"]),
         "xcd_chunk_nnz": info["chunk_nnz"] if info["variant_name"] == "flat" else None,
         "split_row_combine": bool(info["needs_fixup"]) and not info["hybrid"], "plan_ms": round(t_plan, 3),
+        "plan_split": {"create_ms": round(plan_wall, 3), "gpu_ms": round(plan_gpu, 3),
+                       "host_ms": round(plan_wall - plan_gpu, 3),
+                       "what": "pf_plan_create's wall time (statistics, column check, selection, workspace, hybrid "
+                               "tables), the event-timed GPU time of its kernels, and the rest (host work: "
+                               "allocation, copies, synchronisation); paid once per sparsity pattern, not in "
+                               "cdPre or the timed steps"},
         "ladder": info["ladder"] if info["variant_name"] == "prefree" else None,
         "hybrid": bool(info["hybrid"]), "dense_rows": info["dense_rows"] if info["hybrid"] else None,
         "long_tiles": info["long_tiles"] if info["hybrid"] and info["long_tiles"] else None,
         "x_halves": bool(info["x_halves"]) if info["hybrid"] else None,
+        "band_w": info["band_w"] or None,
         "tuning_table": os.path.relpath(os.path.realpath(pf.tuning_table()), REPO) if pf.tuning_table() else None,
         "steps": steps, "warmup": warmup,
         "launch": ("one captured HIP graph of the timed steps" if use_graph else "eager launches from Python")
@@ -510,6 +541,8 @@ def main():
                     help="FLAT 1024/2048: nnz per XCD chunk of tiles (0 = one chunk per XCD); -1 = the plan's choice")
     ap.add_argument("--hybrid", type=int, default=-1, choices=[-1, 0, 1],
                     help="plans with dense rows: 0 = split-row tiles instead of the hybrid path; -1 = the plan's choice")
+    ap.add_argument("--band", type=int, default=-1, choices=[-1, 0, 1],
+                    help="row-aligned plans with a band: force the band kernel off (0) or on (1); -1 = AUTO's rule")
     ap.add_argument("--x-halves", type=int, default=-1, choices=[-1, 0, 1],
                     help="hybrid plans: run tiles once per half of x (1) or once (0); -1 = the plan's choice")
     ap.add_argument("--ladder", type=int, default=0, choices=[0, 1, 2, 3, 4, 5],
@@ -555,6 +588,7 @@ def main():
         head = todo[0]
     else:
         todo, head = ALL_CONFIGS, HEADLINE
+    prewarm(pf, torch)
     records = {}
     for cfg, dt in todo:
         is_head = (cfg, dt) == head
@@ -590,7 +624,9 @@ def main():
                  f"{h['cfg']}: {h['values']}"),
         "config": {k: h[k] for k in ("workload", "cfg", "rows", "cols", "nnz", "seed", "variant", "tile", "tiles",
                                      "run_tiles", "row_aligned", "x_windows", "xcd_chunk_nnz", "split_row_combine",
-                                     "hybrid", "dense_rows", "long_tiles", "x_halves", "plan_ms", "tuning_table")},
+                                     "hybrid", "dense_rows", "long_tiles", "x_halves", "band_w", "plan_ms",
+                                     "plan_split",
+                                     "tuning_table")},
         "gbps_effective": h["gbps_effective"],
         "pct_peak_hbm": h["pct_peak_hbm"],
         "bytes_model": h["bytes_model"],
@@ -621,11 +657,13 @@ def print_summary(records):
         roof, par, cpu = r["roofline"], r.get("parity") or {}, r.get("cpu_baseline") or {}
         ratio = roof["traffic"] / roof["algorithmic_bytes"] if roof.get("traffic") else None
         plan = r["variant"] + f"-{r['tile']}" + ("-rows" if r["row_aligned"] else "") + (
+            f"-band{r['band_w']}" if r.get("band_w") else "") + (
             ("-long" if r["long_tiles"] else "-dense") + ("-halves" if r["x_halves"] else "") if r["hybrid"] else "")
         print(f"summary {name}: plan={plan} kernel_us={f(r['kernel_ms'] * 1e3, '.2f')} "
               f"frac={f(roof['frac'], '.4f')} rotated_frac={f(rot.get('frac'), '.4f')} "
               f"cold_frac={f(cold.get('frac'), '.4f')} search_x={f(srch.get('vs_recorded_rows'), '.3f')} "
               f"traffic_ratio={f(ratio, '.2f')} plan_ms={f(r['plan_ms'], '.3f')} "
+              f"plan_gpu_ms={f(r['plan_split']['gpu_ms'], '.3f')} "
               f"parity={'ok' if par.get('ok') else ('FAIL' if par else '-')} "
               f"max_err={f(par.get('max_rownorm_err_vs_cpu'), '.1e')} gpu_gflops={f(r['gflops'], '.1f')} "
               f"cpu_gflops={f(cpu.get('value'), '.1f')}", file=sys.stderr, flush=True)

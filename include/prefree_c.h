@@ -115,6 +115,10 @@ typedef struct pf_plan_info {
                                 is centred on row guess_a * key + guess_b with a spacing of 1 (the line of
                                 pf_row_stats, chosen when at most m / 256 rows lie over 28 rows from it); 0:
                                 key * m / nnz with guess_spread */
+    int band_w;              /* row-aligned FLAT plans, fp64 / fp32: > 0 when calls after the first run the band
+                                kernel, which keeps x[first row - band_w, last row + band_w) of each step of 4096
+                                nnz in LDS (85% or more of the columns lie within +-band_w of their row); 0: the
+                                tiles' own kernel.  See pf_plan_set_band. */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;
@@ -143,6 +147,19 @@ int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m
 int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n,
                          int nnz, int dtype, int variant, int tile, void *stream);
 int pf_plan_get_info(const pf_plan *plan, pf_plan_info *out);
+/* Row-aligned FLAT plans of fp64 / fp32 matrices whose x exceeds one XCD's L2 (4 MB) and whose columns lie
+ * within +-w of their row for 85% or more of the nnz (w a power of two from 64 to 16384 that fits the band
+ * kernel's LDS ring): planning measures the band (pfk_band_stats) and, for matrices of under 4 nnz per row
+ * on average, turns the band kernel on.  band 1 turns it on for any such plan, 0 off; PF_ERR_UNSUPPORTED for
+ * a plan without a band.  Same y either way (bit for bit). */
+int pf_plan_set_band(pf_plan *plan, int band);
+
+/* Planning time of a plan made by pf_plan_create / pf_plan_create_tuned: plan_ms is the wall time of the
+ * call (statistics, column check, selection, workspace, hybrid tables; the reference pays its pre-pass in
+ * cdPre instead), plan_gpu_ms the event-timed GPU time of its kernels (-1 when events were unavailable;
+ * 0 for plans made otherwise, e.g. by the tuner).  The rest of plan_ms is host work: allocation, copies,
+ * synchronisation and the host's share of the hybrid tables. */
+int pf_plan_get_timing(const pf_plan *plan, double *plan_ms, double *plan_gpu_ms);
 /* Tuning: consecutive tiles per wave64 of the ADAPTIVE kernel (1..256). */
 int pf_plan_set_run_tiles(pf_plan *plan, int run_tiles);
 /* Tuning: cache policy of the ADAPTIVE col/val stream (1 = ordinary loads, 0 = non-temporal). */

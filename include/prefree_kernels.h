@@ -124,7 +124,20 @@ typedef struct pfk_spmv_args {
        left unwritten and sets the error flag; a run row marked 1 loses its second half's sum (not detected). */
     const unsigned char *row_apart;
     size_t row_apart_bytes;
+    /* Row-aligned FLAT 1024/2048 plans whose row map is recorded (map_ready 1), fp64 / fp32: when band_w > 0
+       the step runs the band kernel instead of the tiles' recorded-rows kernel: steps of PFK_BAND_STEP / tile
+       tiles, each workgroup keeping x[first row - band_w, last row + band_w) of its step in an LDS ring of
+       PFK_BAND_RING entries and gathering only the columns outside it from memory.  Any columns give the same
+       sums (rows of at most 16 nnz in nnz order, bit-identical to the recorded-rows kernel); band_w only
+       decides what stays in LDS.  0 < band_w <= PFK_BAND_RING / 2. */
+    int band_w;
 } pfk_spmv_args;
+
+/* The band kernel: nnz per step (whole tiles of the row map), x entries of its LDS ring, and the band widths
+ * its planning statistic counts (64 << i for i < PFK_BAND_WIDTHS). */
+#define PFK_BAND_STEP 4096
+#define PFK_BAND_RING 12288
+#define PFK_BAND_WIDTHS 9
 
 /* nnz per long-row tile of a hybrid plan in long mode. */
 #define PFK_LONG_TILE 1024
@@ -189,9 +202,23 @@ int pfk_flow_resident_waves(int dtype, long long *waves);
 /* Workgroups a FLAT 1024/2048 launch without a schedule uses for ntiles tiles and chunk_nnz. */
 long long pfk_flat_grid(long long ntiles, int tile, long long chunk_nnz);
 
-/* Row statistics.  d_out: 46 unsigned long long (layout in prefree_kernels.hip). */
+/* Row statistics.  d_out: PFK_STATS_WORDS unsigned long long (layout in prefree_kernels.hip; the first 46
+ * are those of pf_row_stats, in its order of fields after m and nnz). */
+#define PFK_STATS_WORDS 50
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,
                   unsigned long long *d_out, void *stream);
+/* The planning scan: pfk_row_stats, and in the same launches every row over PFK_ALIGN_ROW_MAX nnz listed as
+ * int4 (row, first nnz, end, 0) in `list` (the first `cap` of them, in no particular order; d_out[46] counts
+ * them all), with the column descents col[j] > col[j+1] inside listed rows counted in d_out[47]; d_out[48]
+ * is nonzero when that count is incomplete (a list over cap, or a range of col meeting too many listed
+ * rows).  col is read once.  list: cap int4, 16-byte aligned. */
+int pfk_plan_scan(const int *row_ptr, const int *col, int m, int n, long long nnz, unsigned long long *d_out,
+                  void *list, int cap, void *stream);
+
+/* Planning statistic of the band kernel, no counterpart in the reference: out[i] (PFK_BAND_WIDTHS unsigned
+ * long long, zeroed by the call) = the nnz whose column lies within +-(64 << i) of their row.  A thread per row:
+ * for matrices whose rows hold at most PFK_ALIGN_ROW_MAX nnz. */
+int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream);
 
 /* Tile descriptors of ADAPTIVE (merged=1) / FLAT (merged=0) for every tile:
  * d_out[8*t + 0..5] = first row, row count, first nnz, end nnz, head split, tail split. */

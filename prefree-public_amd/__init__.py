@@ -65,7 +65,7 @@ class PlanInfo(ctypes.Structure):
                 ("workspace_bytes", ctypes.c_size_t), ("row_aligned", ctypes.c_int), ("x_windows", ctypes.c_int),
                 ("chunk_nnz", ctypes.c_longlong), ("ladder", ctypes.c_int), ("hybrid", ctypes.c_int),
                 ("dense_rows", ctypes.c_longlong), ("x_halves", ctypes.c_int), ("long_tiles", ctypes.c_int),
-                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double)]
+                ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double), ("band_w", ctypes.c_int)]
 
     def as_dict(self):
         d = {k: getattr(self, k) for k, _ in self._fields_}
@@ -113,7 +113,7 @@ class SpmvArgs(ctypes.Structure):
                 ("long_part_bytes", ctypes.c_size_t), ("ovf_cap", ctypes.c_int),
                 ("aux_stream", ctypes.c_void_p), ("ev_fork", ctypes.c_void_p), ("ev_join", ctypes.c_void_p),
                 ("guess_a", ctypes.c_double), ("guess_b", ctypes.c_double),
-                ("row_apart", ctypes.c_void_p), ("row_apart_bytes", ctypes.c_size_t)]
+                ("row_apart", ctypes.c_void_p), ("row_apart_bytes", ctypes.c_size_t), ("band_w", ctypes.c_int)]
 
 
 _lib = None
@@ -144,6 +144,8 @@ def lib() -> ctypes.CDLL:
         _sig(L.pf_plan_create, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _vp])
         _sig(L.pf_plan_create_tuned, [ctypes.POINTER(_vp), _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
         _sig(L.pf_plan_get_info, [_vp, ctypes.POINTER(PlanInfo)])
+        _sig(L.pf_plan_get_timing, [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)])
+        _sig(L.pf_plan_set_band, [_vp, _i])
         _sig(L.pf_plan_set_run_tiles, [_vp, _i])
         _sig(L.pf_plan_set_keep_cached, [_vp, _i])
         _sig(L.pf_plan_set_row_aligned, [_vp, _i])
@@ -285,6 +287,13 @@ class Plan:
         return i
 
     @property
+    def timing(self):
+        """(plan_ms, plan_gpu_ms): wall time of the plan's creation and the GPU time of its kernels."""
+        a, b = ctypes.c_double(), ctypes.c_double()
+        _check(lib().pf_plan_get_timing(self._h, ctypes.byref(a), ctypes.byref(b)), "pf_plan_get_timing")
+        return a.value, b.value
+
+    @property
     def stats(self) -> RowStats:
         s = RowStats()
         _check(lib().pf_plan_get_stats(self._h, ctypes.byref(s)), "pf_plan_get_stats")
@@ -315,6 +324,10 @@ class Plan:
     def set_ladder(self, ladder):
         """pf_plan_set_ladder: PREFREE reduction ladder 1..5 (the reference tuner's code)."""
         _check(lib().pf_plan_set_ladder(self._h, int(ladder)), "pf_plan_set_ladder")
+
+    def set_band(self, band):
+        """pf_plan_set_band: the band kernel on (True) or off (False) for calls after the first."""
+        _check(lib().pf_plan_set_band(self._h, int(bool(band))), "pf_plan_set_band")
 
     def set_hybrid(self, hybrid):
         """pf_plan_set_hybrid: switch a hybrid plan to split-row tiles (False) and back (True)."""

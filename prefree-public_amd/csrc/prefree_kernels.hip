@@ -1993,6 +1993,338 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
     rows_reduce<T, K, PRIO ? kAuxNt : kAuxDev>(a, d, s_prod, s_rp, L);
 }
 
+// ---- k_band: row-aligned steps with the x band staged in an LDS ring -------
+//
+// For row-aligned plans whose columns lie mostly within +-w of their own row
+// (a banded matrix with outliers: C4's columns within +-4096 of the diagonal,
+// 10% anywhere).  In k_rows every tile gathers its band from L1 / L2, one
+// cache-line request per gather lane, and those requests bound the kernel.
+// Here one workgroup of 1024 threads per CU walks a contiguous range of steps
+// (about PFK_BAND_STEP nnz of whole rows each: `group` tiles of the plan's
+// recorded row map) and keeps x[f - w, l + w) of its current step (rows
+// [f, l)) in an LDS ring, x[c] at slot c mod PFK_BAND_RING.  Consecutive steps
+// share most of their band, so between steps only the entries the next step
+// adds are loaded (about as many as its rows): each band entry of x is read
+// about once per workgroup, and a gather inside the window is an LDS read.
+// Columns outside the window are gathered from memory.  Three steps are in
+// flight: the col / val stream of step s + 2, the outside gathers, ring
+// entries and row bounds of step s + 1, and the products and row sums of step
+// s.  Every load is issued by every lane (a lane with nothing to read uses an
+// offset the range check turns into zeros), so the compiler's wait counts
+// stay exact across the pipeline.  Rows of at most kThreadMax nnz are summed
+// by one lane in nnz order (bit-identical to spmv_serial), longer rows (at
+// most PFK_ALIGN_ROW_MAX) by a wave.  The plan's first call, which searches
+// rows and records the map, runs k_rows; later calls run this kernel.
+constexpr int kBandBS = 1024;
+constexpr int kBandWaves = kBandBS / kWave;
+constexpr int kBandPer = 5;                         // elements per thread: a step and its last row's overflow
+constexpr int kBandSlots = kBandPer * kBandBS;
+constexpr int kBandRing = PFK_BAND_RING;            // x entries in the ring
+constexpr int kBandRp = 2 * kBandBS;                // row bounds staged per step (rows + 1)
+constexpr int kBandExt = 2 * kBandBS;               // ring entries prefetched per step
+constexpr int kBandList = kBandSlots / (kThreadMax + 1) + 1;  // rows longer than kThreadMax in a step, at most
+static_assert(kBandSlots >= PFK_BAND_STEP + PFK_ALIGN_ROW_MAX, "a step's products fit its slots");
+
+struct BandArgs {
+    const int2 *__restrict__ map;  // the plan's row map: (first row, row_ptr there) of each tile, ntiles + 1
+    int w;                         // band half width (columns)
+    int group;                     // tiles of the map per step
+    int nsteps;
+    int per;                       // steps per workgroup
+};
+
+// A step: rows [f, l), nnz [A, B), and the window [lo, hi) of x the ring holds
+// while it is processed.  Windows only move forward and span at most
+// kBandRing entries, so the ring holds any window, and a window keeps the
+// entries it shares with the one before.
+struct BandStep {
+    int f, l, A, B, lo, hi;
+};
+
+// Step s from the row map (s outside [begin, end): an empty step).  A map
+// entry that does not describe whole rows of at most kBandSlots nnz sets the
+// error flag and makes the step empty.
+__device__ __forceinline__ BandStep band_step(const BandArgs &b, long long ntiles, int s, int begin, int end, int m,
+                                              int nnz, int *err)
+{
+    BandStep d{0, 0, 0, 0, 0, 0};
+    if (s < begin || s >= end)
+        return d;
+    const long long t0 = (long long)s * b.group;
+    const long long t1 = min(t0 + b.group, ntiles);
+    // scalar loads (through the constant address space, at wave-uniform addresses): they complete on a
+    // counter of their own, so reading the map does not wait for the vector loads in flight
+    typedef const int __attribute__((address_space(4))) cint;
+    const auto smap = [&](long long t) {
+        const unsigned long long q = reinterpret_cast<unsigned long long>(b.map + t);
+        const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)q);  // each half unsigned (zero-extended)
+        const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(q >> 32));
+        const cint *e = (const cint *)(((unsigned long long)hi << 32) | (unsigned long long)lo);
+        return make_int2(e[0], e[1]);
+    };
+    const int2 e0 = smap(t0), e1 = smap(t1);
+    const bool ok = e0.x >= 0 && e0.x <= e1.x && e1.x <= m && e0.y >= 0 && e0.y <= e1.y && e1.y <= nnz &&
+                    e1.y - e0.y <= kBandSlots;
+    if (!ok) {
+        if (threadIdx.x == 0) atomicOr(err, 1);
+        return d;
+    }
+    d.f = e0.x;
+    d.l = e1.x;
+    d.A = e0.y;
+    d.B = e1.y;
+    return d;
+}
+
+// The window of step d after step p: x[f - w, l + w) clipped to [0, n), never
+// behind p's window, and at most kBandRing entries (the lowest dropped).
+__device__ __forceinline__ void band_window(BandStep &d, const BandStep &p, int n, int w)
+{
+    if (d.l == d.f) {  // no rows: keep the window
+        d.lo = p.lo;
+        d.hi = p.hi;
+        return;
+    }
+    const long long hi = max(min((long long)d.l + w, (long long)n), (long long)p.hi);
+    long long lo = max((long long)d.f - w, (long long)p.lo);
+    lo = min(max(lo, 0LL), hi);
+    lo = max(lo, hi - kBandRing);
+    d.lo = (int)lo;
+    d.hi = (int)hi;
+}
+
+template <typename T>
+__device__ __forceinline__ void band_load_cv(const Args<T> &a, const BandStep &d, int (&c)[kBandPer],
+                                             T (&v)[kBandPer])
+{
+    const int nq = d.B - d.A;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + d.A, (long long)nq * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + d.A, (long long)nq * (long long)sizeof(T));
+#pragma unroll
+    for (int k = 0; k < kBandPer; ++k) {
+        const int q = k * kBandBS + (int)threadIdx.x;
+        c[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, q * 4, 0, kAuxNt);
+        v[k] = buf_load(rv, (uint32_t)(q * (int)sizeof(T)), (T *)nullptr);
+    }
+}
+
+// Inside step d's window: an LDS read; otherwise a gather from memory.
+__device__ __forceinline__ bool band_in(int c, const BandStep &d)
+{
+    return (unsigned)(c - d.lo) < (unsigned)(d.hi - d.lo);
+}
+
+template <typename T>
+__device__ __forceinline__ void band_gather_out(const Args<T> &a, const BandStep &d, const int (&c)[kBandPer],
+                                                T (&xo)[kBandPer])
+{
+    const int nq = d.B - d.A;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
+#pragma unroll
+    for (int k = 0; k < kBandPer; ++k) {
+        const int q = k * kBandBS + (int)threadIdx.x;
+        const bool g = q < nq && !band_in(c[k], d);
+        xo[k] = buf_load(rx, g ? (uint32_t)c[k] * (uint32_t)sizeof(T) : kOob, (T *)nullptr);
+    }
+}
+
+// y[i] of a step through a resource over its rows, non-temporal (y is not read again).
+__device__ __forceinline__ void band_store(__amdgpu_buffer_rsrc_t r, int i, double v)
+{
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, i * 8, 0, kAuxNt);
+}
+
+__device__ __forceinline__ void band_store(__amdgpu_buffer_rsrc_t r, int i, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, i * 4, 0, kAuxNt);
+}
+
+template <typename T>
+__device__ __forceinline__ void band_row_bounds(const Args<T> &a, const BandStep &d, int (&rr)[2])
+{
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(a.rp + d.f, (long long)min(d.l - d.f + 1, kBandRp) * 4);
+    rr[0] = (int)__builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, 0, 0);
+    rr[1] = (int)__builtin_amdgcn_raw_buffer_load_b32(r, ((int)threadIdx.x + kBandBS) * 4, 0, 0);
+}
+
+// One step's registers in the pipeline: its descriptor, col / val, the
+// outside gathers, the ring entries it adds ([e, e + ne), the first kBandExt
+// of them prefetched) and its first kBandRp row bounds.  Three stages rotate
+// by name (the loop is unrolled three times), so no register holding a load
+// in flight is ever copied, which would wait for the load.
+template <typename T>
+struct BandStage {
+    BandStep d;
+    int c[kBandPer];
+    T v[kBandPer];
+    T xo[kBandPer];
+    T xe[2];
+    int e, ne;
+    int rr[2];
+};
+
+// Step s + 2 into nn (col / val), step s + 1 in nx (outside gathers, ring
+// entries, row bounds), and, with PROCESS, step s in cu summed.  The two
+// iterations before a workgroup's first step run without PROCESS, so the
+// pipeline fills with the loads in the order of every later iteration.
+template <bool PROCESS, typename T>
+__device__ __forceinline__ void band_iter(const Args<T> &a, const BandArgs &b, int s, int s0, int s1, T *s_ring,
+                                          acc_t<T> *s_prod, int *s_rp, int *s_list, int &s_nlist,
+                                          BandStage<T> &cu, BandStage<T> &nx, BandStage<T> &nn)
+{
+    using P = acc_t<T>;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int n = a.n;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)n * (long long)sizeof(T));
+    // ---- step s + 2: col / val
+    nn.d = band_step(b, a.ntiles, s + 2, s0, s1, a.m, a.nnz, a.err);
+    band_window(nn.d, nx.d, n, b.w);
+    band_load_cv(a, nn.d, nn.c, nn.v);
+    // the loads keep this order in every iteration (step s + 2's stream first), so the counted waits for
+    // each step's loads are the same on every path into the loop
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- step s + 1: outside gathers, the ring entries it adds, its row bounds
+    band_gather_out(a, nx.d, nx.c, nx.xo);
+    nx.e = max(cu.d.hi, nx.d.lo);
+    nx.ne = nx.d.hi - nx.e;
+    {
+        const __amdgpu_buffer_rsrc_t re = make_rsrc(a.x + nx.e, (long long)min(nx.ne, kBandExt) * (long long)sizeof(T));
+        nx.xe[0] = buf_load(re, (uint32_t)(tid * (int)sizeof(T)), (T *)nullptr);
+        nx.xe[1] = buf_load(re, (uint32_t)((tid + kBandBS) * (int)sizeof(T)), (T *)nullptr);
+    }
+    band_row_bounds(a, nx.d, nx.rr);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!PROCESS)
+        return;
+
+    // ---- step s: the ring entries it adds and its row bounds into LDS (every
+    // read of the previous step's entries and bounds ended at its last barrier)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = j * kBandBS + tid;
+        if (i < cu.ne) s_ring[(unsigned)(cu.e + i) % (unsigned)kBandRing] = cu.xe[j];
+        s_rp[i] = cu.rr[j];
+    }
+    for (int c = cu.e + kBandExt + tid; c < cu.e + cu.ne; c += kBandBS)  // a window that moves further (rare)
+        s_ring[(unsigned)c % (unsigned)kBandRing] = buf_load(rx, (uint32_t)c * (uint32_t)sizeof(T), (T *)nullptr);
+    lds_sync();
+    if (tid == 0) s_nlist = 0;  // every wave read the previous step's count before the barrier above
+    // products: inside the window from the ring, outside from the gathers
+    const BandStep d = cu.d;
+    const int nq = d.B - d.A;
+#pragma unroll
+    for (int k = 0; k < kBandPer; ++k) {
+        const int q = k * kBandBS + tid;
+        // both values read, then one chosen (a choice between the two addresses would put xo in memory)
+        const T xr = s_ring[(unsigned)cu.c[k] % (unsigned)kBandRing];
+        const T xv = band_in(cu.c[k], d) ? xr : cu.xo[k];
+        if (q < nq) s_prod[q] = P(cu.v[k]) * P(xv);
+    }
+    lds_sync();
+    // row sums of rows [f, l): bounds from LDS, or from row_ptr past kBandRp - 1 rows
+    const int nr = d.l - d.f;
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y + d.f, (long long)nr * (long long)sizeof(T));
+    bool bad = false;
+    const auto row = [&](int i, int ra, int rb) {
+        ra -= d.A;
+        rb -= d.A;
+        if (ra < 0 || rb < ra || rb > nq) {  // row_ptr changed after planning: stay inside the step
+            bad = true;
+            ra = min(max(ra, 0), nq);
+            rb = min(max(rb, ra), nq);
+        }
+        if (rb - ra <= kThreadMax) {
+            P acc = P(0);
+            for (int j = ra; j < rb; ++j)
+                acc += s_prod[j];
+            band_store(ry, i, T(acc));
+        } else {
+            // disjoint rows of over kThreadMax products: at most kBandList of them (more only with a row_ptr
+            // changed after planning, whose rows were clamped above and are reported)
+            const int k = atomicAdd(&s_nlist, 1);
+            if (k < kBandList) {
+                s_list[3 * k] = i;
+                s_list[3 * k + 1] = ra;
+                s_list[3 * k + 2] = rb;
+            } else {
+                bad = true;
+            }
+        }
+    };
+    const int nfast = min(nr, kBandRp - 1);
+    for (int i = tid; i < nfast; i += kBandBS)  // bounds from LDS
+        row(i, s_rp[i], s_rp[i + 1]);
+    for (int i = nfast + tid; i < nr; i += kBandBS)  // a step of more rows (empty ones): bounds from row_ptr
+        row(i, a.rp[d.f + i], a.rp[d.f + i + 1]);
+    if (bad) atomicOr(a.err, 1);
+    lds_sync();
+    const int nl = min(s_nlist, kBandList);
+    for (int k = wave; k < nl; k += kBandWaves) {
+        const int i = s_list[3 * k], ra = s_list[3 * k + 1], rb = s_list[3 * k + 2];
+        P acc = P(0);
+        for (int j = ra + lane; j < rb; j += kWave)
+            acc += s_prod[j];
+        acc = wave_sum(acc);
+        if (lane == 0) band_store(ry, i, T(acc));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBandBS) void k_band(Args<T> a, BandArgs b)
+{
+    __shared__ __attribute__((aligned(16))) T s_ring[kBandRing];
+    __shared__ __attribute__((aligned(16))) acc_t<T> s_prod[kBandSlots];
+    __shared__ int s_rp[kBandRp];
+    __shared__ int s_list[3 * kBandList];
+    __shared__ int s_nlist;
+    const int s0 = (int)blockIdx.x * b.per;
+    const int s1 = min(b.nsteps, s0 + b.per);
+    if (s0 >= s1)
+        return;  // whole workgroup
+    // The pipeline fills with two iterations that only load (steps s0 and s0 + 1; the steps before s0 are
+    // empty, with an empty window, so step s0 brings its whole window into the ring).  Steps past s1 are
+    // empty too (no loads, no rows), so every trip of the loop runs three.
+    BandStage<T> X{}, Y{}, Z{};
+    band_iter<false>(a, b, s0 - 2, s0, s1, s_ring, s_prod, s_rp, s_list, s_nlist, Y, Z, X);
+    band_iter<false>(a, b, s0 - 1, s0, s1, s_ring, s_prod, s_rp, s_list, s_nlist, Z, X, Y);
+    for (int s = s0; s < s1; s += 3) {
+        band_iter<true>(a, b, s, s0, s1, s_ring, s_prod, s_rp, s_list, s_nlist, X, Y, Z);
+        band_iter<true>(a, b, s + 1, s0, s1, s_ring, s_prod, s_rp, s_list, s_nlist, Y, Z, X);
+        band_iter<true>(a, b, s + 2, s0, s1, s_ring, s_prod, s_rp, s_list, s_nlist, Z, X, Y);
+    }
+}
+
+// Planning statistic of the band kernel: out[i] = the nnz whose column lies
+// within +-(64 << i) of their row, i < PFK_BAND_WIDTHS.  A thread per row
+// (row-aligned plans: rows of at most PFK_ALIGN_ROW_MAX nnz).
+__global__ __launch_bounds__(kBS) void k_band_stats(const int *__restrict__ rp, const int *__restrict__ col, int m,
+                                                    unsigned long long *__restrict__ out)
+{
+    __shared__ unsigned long long s_c[PFK_BAND_WIDTHS];
+    const int tid = threadIdx.x;
+    if (tid < PFK_BAND_WIDTHS) s_c[tid] = 0;
+    __syncthreads();
+    unsigned int cnt[PFK_BAND_WIDTHS];
+#pragma unroll
+    for (int i = 0; i < PFK_BAND_WIDTHS; ++i) cnt[i] = 0;
+    for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
+        const int a0 = rp[r], a1 = rp[r + 1];
+        for (int j = a0; j < a1; ++j) {
+            const long long d = llabs((long long)col[j] - r);
+#pragma unroll
+            for (int i = 0; i < PFK_BAND_WIDTHS; ++i) cnt[i] += d <= (64ll << i) ? 1u : 0u;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PFK_BAND_WIDTHS; ++i)
+        if (cnt[i]) atomicAdd(&s_c[i], (unsigned long long)cnt[i]);
+    __syncthreads();
+    if (tid < PFK_BAND_WIDTHS && s_c[tid]) atomicAdd(out + tid, s_c[tid]);
+}
+
 // ---- k_dense: dense rows by x windows staged in LDS (hybrid plans) -----------
 //
 // A dense row (at least the plan's dense_min nnz, columns sorted) sweeps all of
@@ -3158,8 +3490,12 @@ __global__ __launch_bounds__(kBS) void k_probe_gather(const int *__restrict__ id
 enum StatSlot {
     kStMax = 0, kStMin = 1, kStEmpty = 2, kStDec = 3, kStFirst = 4, kStLast = 5, kStBadCol = 6,
     kStHist = 7, kStOverAlign = 40, kStMaxShort = 41, kStGuessDev = 42, kStLineQ1 = 43, kStLineQ3 = 44,
-    kStLineFar = 45, kStCount = 46
+    kStLineFar = 45,
+    // planning scan only (pfk_plan_scan): long rows appended to its list, column descents found inside them,
+    // and a flag set when the descents could not all be checked
+    kStLongListed = 46, kStLongDesc = 47, kStLongUnchecked = 48, kStCount = 49
 };
+static_assert(kStCount <= PFK_STATS_WORDS, "statistics block of the C ABI");
 
 __global__ void k_stats_init(unsigned long long *out)
 {
@@ -3168,8 +3504,12 @@ __global__ void k_stats_init(unsigned long long *out)
         out[i] = (i == kStMin) ? ~0ull : 0ull;
 }
 
+// Row statistics; with a list (the planning scan), every row over
+// PFK_ALIGN_ROW_MAX nnz is also appended to it as (row, first nnz, end, 0),
+// the first `cap` of them (out[kStLongListed] counts them all).
 __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, int m,
-                                                   unsigned long long *__restrict__ out)
+                                                   unsigned long long *__restrict__ out, int4 *__restrict__ list,
+                                                   int cap)
 {
     __shared__ unsigned int s_hist[33];
     __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev, s_far;
@@ -3204,6 +3544,10 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
         lempty += (u == 0);
         lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
         if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
+        if (list && u > (unsigned)PFK_ALIGN_ROW_MAX) {  // rare: one atomic per long row
+            const unsigned long long k = atomicAdd(out + kStLongListed, 1ull);
+            if (k < (unsigned long long)cap) list[k] = make_int4((int)r, rp[r], rp[r] + (int)u, 0);
+        }
         atomicAdd(&s_hist[u == 0 ? 0 : 32 - __clz(u)], 1u);
     }
     atomicMax(&s_max, lmax);
@@ -3234,19 +3578,87 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     }
 }
 
+// Column range check, col streamed once as 16-byte loads, each workgroup over
+// a contiguous range of nnz.  With a list (the planning scan, after
+// k_row_stats filled it), it also counts the descents col[j] > col[j + 1]
+// with j and j + 1 inside one listed long row (a hybrid plan's dense rows need
+// sorted columns), so planning reads col once.  A workgroup whose range meets
+// more listed rows than it holds, or a list that overflowed, sets
+// out[kStLongUnchecked] instead of counting.
+constexpr int kColRowsCap = 64;  // listed rows one workgroup's range may meet
+
 __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, long long nnz, int n,
-                                                   unsigned long long *__restrict__ out)
+                                                   unsigned long long *__restrict__ out, const int4 *__restrict__ list,
+                                                   int cap)
 {
-    unsigned int bad = 0;
-    for (long long j = (long long)blockIdx.x * kBS + threadIdx.x; j < nnz; j += (long long)gridDim.x * kBS) {
-        const int c = __builtin_nontemporal_load(col + j);
-        bad += (c < 0 || c >= n);
+    __shared__ int s_nrows, s_over;
+    __shared__ int2 s_rows[kColRowsCap];  // nnz ranges [first, end) of the listed rows this range meets
+    const int tid = threadIdx.x;
+    const long long per = ((nnz + gridDim.x - 1) / gridDim.x + 1023) & ~1023ll;  // whole vectors per lane
+    const long long j0 = (long long)blockIdx.x * per;
+    const long long j1 = min(nnz, j0 + per);
+    if (j0 >= nnz)
+        return;  // whole workgroup
+    if (tid == 0) { s_nrows = 0; s_over = 0; }
+    __syncthreads();
+    if (list) {
+        const unsigned long long listed = out[kStLongListed];
+        const int nl = (int)min(listed, (unsigned long long)cap);
+        if (listed > (unsigned long long)cap && blockIdx.x == 0 && tid == 0) atomicOr(out + kStLongUnchecked, 1ull);
+        for (int i = tid; i < nl; i += kBS) {
+            const int4 e = list[i];
+            if ((long long)e.y < j1 && (long long)e.z > j0) {
+                const int k = atomicAdd(&s_nrows, 1);
+                if (k < kColRowsCap) s_rows[k] = make_int2(e.y, e.z);
+                else s_over = 1;
+            }
+        }
+        __syncthreads();
+        if (s_over && tid == 0) atomicOr(out + kStLongUnchecked, 1ull);
+    }
+    const int nrows = s_over ? 0 : min(s_nrows, kColRowsCap);
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(col + j0, (j1 - j0) * 4);
+    // the entry after the range, for the descent at its last position (zero past nnz: unused there)
+    const __amdgpu_buffer_rsrc_t rn = make_rsrc(col + j0, min(nnz - j0, j1 - j0 + 1) * 4);
+    unsigned int bad = 0, desc = 0;
+    const int nvec = (int)((j1 - j0 + 3) / 4);
+    for (int v0 = tid; v0 < nvec; v0 += 4 * kBS) {
+        u32x4 c[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)  // four loads in flight per lane; vectors past the range read zeros
+            c[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, (v0 + u * kBS) * 16, 0, kAuxNt);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const long long jb = j0 + 4ll * (v0 + u * kBS);
+            const int e[4] = {(int)c[u].x, (int)c[u].y, (int)c[u].z, (int)c[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                bad += (jb + i < j1 && (e[i] < 0 || e[i] >= n)) ? 1u : 0u;
+            if (nrows > 0 && jb < j1) {  // descents inside listed rows (rare: sorted rows have none)
+                const int nx = (int)__builtin_amdgcn_raw_buffer_load_b32(rn, (int)(jb - j0 + 4) * 4, 0, 0);
+                const int f[5] = {e[0], e[1], e[2], e[3], nx};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const long long j = jb + i;
+                    if (j + 1 < nnz && j + 1 <= j1 && j < j1 && f[i] > f[i + 1]) {
+                        for (int k = 0; k < nrows; ++k)
+                            desc += (s_rows[k].x <= j && j + 1 < s_rows[k].y) ? 1u : 0u;
+                    }
+                }
+            }
+        }
     }
     if (__ballot(bad != 0)) {
         for (int o = 32; o > 0; o >>= 1)
             bad += __shfl_down(bad, o);
-        if ((threadIdx.x & (kWave - 1)) == 0 && bad)
+        if ((tid & (kWave - 1)) == 0 && bad)
             atomicAdd(out + kStBadCol, (unsigned long long)bad);
+    }
+    if (__ballot(desc != 0)) {
+        for (int o = 32; o > 0; o >>= 1)
+            desc += __shfl_down(desc, o);
+        if ((tid & (kWave - 1)) == 0 && desc)
+            atomicAdd(out + kStLongDesc, (unsigned long long)desc);
     }
 }
 
@@ -3505,14 +3917,39 @@ int launch_flow(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
+// The band kernel over a recorded row map: one workgroup per CU, each over a
+// contiguous range of steps of PFK_BAND_STEP / K tiles.
+template <typename T, int K>
+int launch_band(const pfk_spmv_args *a, void *stream)
+{
+    static_assert(PFK_BAND_STEP % K == 0, "whole tiles per step");
+    Args<T> r = make_args<T>(a);
+    BandArgs b;
+    b.map = reinterpret_cast<const int2 *>(a->row_map);
+    b.w = a->band_w;
+    b.group = PFK_BAND_STEP / K;
+    const long long nsteps = (a->ntiles + b.group - 1) / b.group;
+    const long long wgs = std::min<long long>(nsteps, std::max(1, device_cus()));
+    b.per = (int)((nsteps + wgs - 1) / wgs);
+    b.nsteps = (int)nsteps;
+    const long long grid = (nsteps + b.per - 1) / b.per;
+    hipLaunchKernelGGL((k_band<T>), dim3((unsigned)grid), dim3(kBandBS), 0, S(stream), r, b);
+    PFK_LAUNCHED("k_band");
+    return PF_OK;
+}
+
 // k_flat (split rows) or k_rows (row-aligned tiles): search (and record the
-// row map when the plan has one) or, once the map is recorded, read it.
+// row map when the plan has one) or, once the map is recorded, read it (or run
+// the band kernel over it).
 template <typename T, int K>
 int launch_flat(const pfk_spmv_args *a, int *dbg, void *stream)
 {
     Args<T> r = make_args<T>(a);
     chunk_shape(r.ntiles, K, a->chunk_nnz, r.xch, r.g8);
     const long long grid = r.g8 * kXcds;
+    if constexpr (!__is_same(T, half_t)) {
+        if (a->row_aligned && !dbg && a->row_map && a->map_ready && a->band_w > 0) return launch_band<T, K>(a, stream);
+    }
     if (a->row_aligned) {
         if (dbg)
             hipLaunchKernelGGL((k_rows<T, K, kFlatDesc>), dim3((unsigned)grid), dim3(kBS), 0, S(stream), r, nullptr,
@@ -3678,6 +4115,27 @@ int launch_hybrid(const pfk_spmv_args *a, void *stream)
     return PF_OK;
 }
 
+// Row statistics, and with a list the planning scan's long rows and descents.
+int launch_stats(const int *row_ptr, const int *col, int m, int n, long long nnz, unsigned long long *d_out,
+                 int4 *list, int cap, void *stream)
+{
+    if (!row_ptr || !d_out || m < 0 || nnz < 0 || cap < 0) return PF_ERR_INVALID;
+    hipLaunchKernelGGL(k_stats_init, dim3(1), dim3(64), 0, S(stream), d_out);
+    PFK_LAUNCHED("k_stats_init");
+    if (m > 0) {
+        const unsigned grid = grid_for(m, kBS, 2048);
+        hipLaunchKernelGGL(k_row_stats, dim3(grid), dim3(kBS), 0, S(stream), row_ptr, m, d_out, list, cap);
+        PFK_LAUNCHED("k_row_stats");
+    }
+    if (col && nnz > 0) {
+        // about 16 vectors of 4 nnz per lane and workgroup, at most 4096 workgroups
+        const unsigned grid = grid_for((nnz + 15) / 16, kBS * 4, 4096);
+        hipLaunchKernelGGL(k_col_check, dim3(grid), dim3(kBS), 0, S(stream), col, nnz, n, d_out, list, cap);
+        PFK_LAUNCHED("k_col_check");
+    }
+    return PF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -3696,6 +4154,12 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
     if (!a) return PF_ERR_INVALID;
     if (a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, !a->row_aligned) || !ws_ok(dtype, a, !a->row_aligned)) return PF_ERR_INVALID;
+    if (a->band_w < 0 || a->band_w > PFK_BAND_RING / 2 ||
+        (a->band_w > 0 && (dtype == PF_F16 || !a->row_aligned || !a->row_map))) {
+        snprintf(g_err, sizeof g_err, "band width %d: 0..%d, for row-aligned fp64 / fp32 plans with a row map",
+                 a->band_w, PFK_BAND_RING / 2);
+        return PF_ERR_INVALID;
+    }
     return dtype == PF_F64 ? dispatch_flat<double>(a, stream)
          : dtype == PF_F32 ? dispatch_flat<float>(a, stream)
          : dtype == PF_F16 ? dispatch_flat<half_t>(a, stream) : PF_ERR_INVALID;
@@ -3889,20 +4353,28 @@ int pfk_adaptive_long_row_min(int dtype, int tile)
 int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nnz,
                   unsigned long long *d_out, void *stream)
 {
-    if (!row_ptr || !d_out || m < 0 || nnz < 0) return PF_ERR_INVALID;
-    hipLaunchKernelGGL(k_stats_init, dim3(1), dim3(64), 0, S(stream), d_out);
-    PFK_LAUNCHED("k_stats_init");
+    return launch_stats(row_ptr, col, m, n, nnz, d_out, nullptr, 0, stream);
+}
+
+int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream)
+{
+    if (!row_ptr || !out || m < 0 || (m > 0 && !col)) return PF_ERR_INVALID;
+    hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(kBS), 0, S(stream), reinterpret_cast<uint32_t *>(out),
+                       (size_t)(2 * PFK_BAND_WIDTHS));
+    PFK_LAUNCHED("k_fill_zero");
     if (m > 0) {
-        const unsigned grid = grid_for(m, kBS, 2048);
-        hipLaunchKernelGGL(k_row_stats, dim3(grid), dim3(kBS), 0, S(stream), row_ptr, m, d_out);
-        PFK_LAUNCHED("k_row_stats");
-    }
-    if (col && nnz > 0) {
-        const unsigned grid = grid_for(nnz, kBS, 4096);
-        hipLaunchKernelGGL(k_col_check, dim3(grid), dim3(kBS), 0, S(stream), col, nnz, n, d_out);
-        PFK_LAUNCHED("k_col_check");
+        hipLaunchKernelGGL(k_band_stats, dim3(grid_for(m, kBS, 4096)), dim3(kBS), 0, S(stream), row_ptr, col, m, out);
+        PFK_LAUNCHED("k_band_stats");
     }
     return PF_OK;
+}
+
+int pfk_plan_scan(const int *row_ptr, const int *col, int m, int n, long long nnz, unsigned long long *d_out,
+                  void *list, int cap, void *stream)
+{
+    if (!col && nnz > 0) return PF_ERR_INVALID;
+    if (cap > 0 && !list) return PF_ERR_INVALID;
+    return launch_stats(row_ptr, col, m, n, nnz, d_out, static_cast<int4 *>(list), cap, stream);
 }
 
 int pfk_debug_tile_desc(int dtype, int merged_keys, const pfk_spmv_args *a, int *d_out, void *stream)

@@ -11,6 +11,7 @@
 #include <cstring>
 #include <dlfcn.h>
 #include <fstream>
+#include <chrono>
 #include <mutex>
 #include <sstream>
 #include <stdexcept>
@@ -438,6 +439,8 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
 
 struct pf_plan {
     int m = 0, n = 0, nnz = 0;
+    double plan_ms = 0.0, plan_gpu_ms = 0.0;  // planning: wall time, and GPU time of its kernels (events)
+    int band_avail = 0;                        // band width the band kernel may use (0: the plan has no band)
     pf_plan_info info{};
     pf_row_stats stats{};
     void *ws = nullptr;
@@ -595,6 +598,33 @@ long long rows_at_least_pow2(const pf_row_stats &s, int j)
 // checked columns (the planning scan reads col) when those rows may all be
 // dense (the histogram allows it) or x exceeds one XCD's L2 (long mode);
 // try_hybrid decides.
+// What the planning scan (pfk_plan_scan) found about the long rows: the list
+// on the device (the first `cap` of them), how many there are, and whether
+// the descents inside them were all counted (then `desc` is their number).
+struct PlanScan {
+    const int *list = nullptr;  // int4 (row, first nnz, end, 0) per long row, in no particular order
+    long long cap = 0, listed = 0, desc = 0;
+    bool checked = false;
+    bool complete() const { return list && listed <= cap && checked; }
+};
+
+// Events around the GPU work of planning: their sum is the plan's GPU time.
+struct PlanTimer {
+    void *e[2] = {nullptr, nullptr};
+    double gpu_ms = 0.0;
+    bool ok = false;
+    explicit PlanTimer() { ok = pfk_event_create(&e[0]) == PF_OK && pfk_event_create(&e[1]) == PF_OK; }
+    ~PlanTimer() { pfk_event_destroy(e[0]); pfk_event_destroy(e[1]); }
+    void start(void *stream) { if (ok) ok = pfk_event_record(e[0], stream) == PF_OK; }
+    void stop(void *stream)  // after the work it times has been synchronised
+    {
+        float ms = 0.f;
+        if (ok) ok = pfk_event_record(e[1], stream) == PF_OK && pfk_event_sync(e[1]) == PF_OK &&
+                     pfk_event_elapsed_ms(&ms, e[0], e[1]) == PF_OK;
+        if (ok) gpu_ms += ms;
+    }
+};
+
 bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_plan_info &info, const int *d_col)
 {
     if (!d_col || (dtype != PF_F64 && dtype != PF_F32) || info.variant != PF_FLAT || info.row_aligned ||
@@ -613,21 +643,39 @@ bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_pl
 // and x exceeds one XCD's L2, they are cut into tiles dealt to the XCDs by
 // their first column (long mode).  The rows between them are cut into runs of
 // row-aligned tiles.  Leaves the plan as it is (split-row tiles) otherwise.
-int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
+int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream, const PlanScan *scan,
+               PlanTimer *timer)
 {
     const int dtype = p->info.dtype;
     const long long cap = p->stats.n_long_rows;
-    int *tmp = nullptr;
-    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&tmp), (size_t)(2 + 3 * cap) * sizeof(int)), "long-row scan buffer");
     std::vector<int> list((size_t)(3 * cap));
     int cnt[2] = {0, 0};
-    int st = pfk_fill_zero(tmp, 2 * sizeof(int), stream);
-    if (st == PF_OK) st = pfk_dense_scan(d_row_ptr, d_col, p->m, PFK_ALIGN_ROW_MAX + 1, tmp + 2, (int)cap, tmp, stream);
-    if (st == PF_OK) st = pfk_memcpy_d2h(cnt, tmp, sizeof cnt, stream);
-    if (st == PF_OK) st = pfk_memcpy_d2h(list.data(), tmp + 2, list.size() * sizeof(int), stream);
-    if (st == PF_OK) st = pfk_stream_sync(stream);
-    pfk_free(tmp);
-    if (st != PF_OK) return from_kernel_layer(st, "long-row scan");
+    int st = PF_OK;
+    if (scan && scan->complete() && scan->listed == cap) {
+        // the planning scan listed every long row and counted the descents inside them: no second pass over col
+        std::vector<int> l4((size_t)(4 * cap));
+        st = pfk_memcpy_d2h(l4.data(), scan->list, l4.size() * sizeof(int), stream);
+        if (st == PF_OK) st = pfk_stream_sync(stream);
+        if (st != PF_OK) return from_kernel_layer(st, "long-row list");
+        for (long long k = 0; k < cap; ++k)
+            for (int j = 0; j < 3; ++j) list[(size_t)(3 * k + j)] = l4[(size_t)(4 * k + j)];
+        cnt[0] = (int)cap;
+        cnt[1] = scan->desc > 0 ? 1 : 0;
+    } else {
+        int *tmp = nullptr;
+        PF_TRY(pfk_malloc(reinterpret_cast<void **>(&tmp), (size_t)(2 + 3 * cap) * sizeof(int)),
+               "long-row scan buffer");
+        if (timer) timer->start(stream);
+        st = pfk_fill_zero(tmp, 2 * sizeof(int), stream);
+        if (st == PF_OK)
+            st = pfk_dense_scan(d_row_ptr, d_col, p->m, PFK_ALIGN_ROW_MAX + 1, tmp + 2, (int)cap, tmp, stream);
+        if (st == PF_OK) st = pfk_memcpy_d2h(cnt, tmp, sizeof cnt, stream);
+        if (st == PF_OK) st = pfk_memcpy_d2h(list.data(), tmp + 2, list.size() * sizeof(int), stream);
+        if (st == PF_OK) st = pfk_stream_sync(stream);
+        if (st == PF_OK && timer) timer->stop(stream);
+        pfk_free(tmp);
+        if (st != PF_OK) return from_kernel_layer(st, "long-row scan");
+    }
     if (cnt[0] != cap) return PF_OK;  // row_ptr and the statistics disagree: stay split-row
 
     // Long rows ascending, and the runs of rows between them.
@@ -758,6 +806,7 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
         return fail(PF_ERR_KERNEL, "hybrid plan: the planning scan listed a row twice");
     if (st == PF_OK && p->m > 0) st = pfk_memcpy_h2d(p->row_apart, apart.data(), apart.size(), stream);
     if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
+    if (st == PF_OK && timer) timer->start(stream);
     if (st == PF_OK && lng) {
         // deal: the tiles ordered by their first column, XCD k taking the k-th eighth
         st = pfk_memcpy_h2d(p->long_tiles, lt.data(), lt.size() * 4, stream);
@@ -777,6 +826,7 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
         }
     }
     if (st == PF_OK) st = pfk_stream_sync(stream);
+    if (st == PF_OK && timer) timer->stop(stream);
     if (st != PF_OK) return from_kernel_layer(st, "hybrid tables");
     if (!p->aux_stream) {  // without them the kernels run in sequence on the caller's stream
         if (pfk_stream_create(&p->aux_stream) != PF_OK) p->aux_stream = nullptr;
@@ -794,12 +844,49 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream)
     return PF_OK;
 }
 
+// The band kernel for a row-aligned plan: measures how many columns lie
+// within +-w of their row (w = 64 << i) and keeps the smallest w that holds 85%
+// of the nnz and, with two steps' rows, fits the kernel's LDS ring.  On by
+// default for matrices of under 4 nnz per row on average (each row's x entry
+// is then a large part of the stream, and the band's gathers cost most).
+int try_band(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream, PlanTimer *timer)
+{
+    const pf_plan_info &in = p->info;
+    const long long m = p->m, n = p->n, nnz = p->nnz;
+    if (in.variant != PF_FLAT || !in.row_aligned || !uses_row_map(in.variant, in.tile) ||
+        (in.dtype != PF_F64 && in.dtype != PF_F32) || n * value_bytes(in.dtype) <= kXcdL2Bytes ||
+        nnz < 64LL * PFK_BAND_STEP || m < 1)
+        return PF_OK;
+    unsigned long long *d = nullptr;
+    unsigned long long h[PFK_BAND_WIDTHS];
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), sizeof h), "band statistic");
+    if (timer) timer->start(stream);
+    int st = pfk_band_stats(d_row_ptr, d_col, p->m, d, stream);
+    if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
+    if (st == PF_OK) st = pfk_stream_sync(stream);
+    if (st == PF_OK && timer) timer->stop(stream);
+    pfk_free(d);
+    if (st != PF_OK) return from_kernel_layer(st, "band statistic");
+    const long long rows_per_step = (PFK_BAND_STEP * m + nnz - 1) / nnz;
+    for (int i = 0; i < PFK_BAND_WIDTHS; ++i) {
+        const long long w = 64LL << i;
+        if (2 * w + 2 * rows_per_step > PFK_BAND_RING) break;
+        if ((double)h[i] >= 0.85 * (double)nnz) {
+            p->band_avail = (int)w;
+            break;
+        }
+    }
+    p->info.band_w = (p->band_avail > 0 && nnz < 4 * m) ? p->band_avail : 0;
+    return PF_OK;
+}
+
 // The plan for a validated matrix with known statistics (shared by plan
 // creation and the tuner's candidates): workspace allocated and initialised.
 // With columns given, PF_AUTO and PF_FLAT plans of the default tile also try
 // the hybrid path.
 int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nnz, int dtype, int variant, int tile,
-               void *stream, pf_plan **plan, const int *d_col = nullptr)
+               void *stream, pf_plan **plan, const int *d_col = nullptr, const PlanScan *scan = nullptr,
+               PlanTimer *timer = nullptr)
 {
     bool allow_hybrid = true;
     pf_plan_info info;
@@ -819,10 +906,13 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
         return from_kernel_layer(rc, "plan workspace");
     }
     plan_carve(p, w);
+    if (timer) timer->start(stream);
     rc = plan_init(p, d_row_ptr, stream);
     if (rc == PF_OK) rc = pfk_stream_sync(stream);
+    if (rc == PF_OK && timer) timer->stop(stream);
+    if (rc == PF_OK && d_col) rc = try_band(p, d_row_ptr, d_col, stream, timer);
     if (rc == PF_OK && want_hybrid && hybrid_candidate(s, n, dtype, p->info, d_col)) {
-        rc = try_hybrid(p, d_row_ptr, d_col, stream);
+        rc = try_hybrid(p, d_row_ptr, d_col, stream, scan, timer);
         if (rc != PF_OK) {
             pfk_free(p->ws_hyb);
             pfk_free(p->ws);
@@ -856,16 +946,25 @@ int check_matrix_args(const int *d_row_ptr, const int *d_col, int m, int n, int 
     return PF_OK;
 }
 
-// Row statistics of a device CSR through a caller-supplied block of 46
+// Row statistics of a device CSR through a caller-supplied block of PFK_STATS_WORDS
 // unsigned long long (synchronises `stream`).
+void decode_stats(const unsigned long long *h, const int *d_col, int m, long long nnz, pf_row_stats *out);
+
 int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int m, int n, long long nnz,
               pf_row_stats *out, void *stream)
 {
-    unsigned long long h[46];
+    unsigned long long h[PFK_STATS_WORDS];
     int st = pfk_row_stats(d_row_ptr, d_col, m, n, nnz, d, stream);
     if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
     if (st == PF_OK) st = pfk_stream_sync(stream);
     if (st != PF_OK) return from_kernel_layer(st, "row statistics");
+    decode_stats(h, d_col, m, nnz, out);
+    return PF_OK;
+}
+
+// pf_row_stats from the statistics block (the layout of prefree_kernels.hip).
+void decode_stats(const unsigned long long *h, const int *d_col, int m, long long nnz, pf_row_stats *out)
+{
     std::memset(out, 0, sizeof *out);
     out->m = m;
     out->nnz = nnz;
@@ -883,7 +982,6 @@ int stats_via(unsigned long long *d, const int *d_row_ptr, const int *d_col, int
     out->line_q1_row_ptr = (long long)h[43];
     out->line_q3_row_ptr = (long long)h[44];
     out->line_far_rows = (long long)h[45];
-    return PF_OK;
 }
 
 int check_csr_stats(const pf_row_stats &s, int nnz)
@@ -894,6 +992,10 @@ int check_csr_stats(const pf_row_stats &s, int nnz)
                                     std::to_string(s.n_decreasing) + " bad_cols=" + std::to_string(s.n_bad_cols));
     return PF_OK;
 }
+
+// Long rows the planning scan lists; a matrix with more of them scans again
+// when it tries the hybrid path.
+constexpr int kScanListCap = 4096;
 
 // Bytes of pf_spmv_noalloc's scratch taken by the row statistics block; the
 // workspace starts after it, 256-byte aligned.
@@ -935,7 +1037,7 @@ int pf_row_stats_compute(const int *d_row_ptr, const int *d_col, int m, int n, l
     if (!out || !d_row_ptr || m < 0 || n < 0 || nnz < 0)
         return fail(PF_ERR_INVALID, "pf_row_stats_compute: bad argument");
     unsigned long long *d = nullptr;
-    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), 46 * sizeof(unsigned long long)), "stats buffer");
+    PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), PFK_STATS_WORDS * sizeof(unsigned long long)), "stats buffer");
     const int st = stats_via(d, d_row_ptr, d_col, m, n, nnz, out, stream);
     pfk_free(d);
     return st;
@@ -962,19 +1064,75 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
 {
     if (!plan) return fail(PF_ERR_INVALID, "plan is NULL");
     *plan = nullptr;
+    const auto t0 = std::chrono::steady_clock::now();
     int st = check_matrix_args(d_row_ptr, d_col, m, n, nnz, dtype, variant);
     if (st != PF_OK) return st;
     pf_row_stats s;
     std::memset(&s, 0, sizeof s);
     s.m = m;
     s.nnz = nnz;
-    if (m > 0) {
+    PlanTimer timer;
+    PlanScan scan;
+    void *buf = nullptr;
+    if (m > 0 && d_col) {
+        // the planning scan: statistics, column check and the long rows (with the descents inside them) in one
+        // pass over row_ptr and one over col
+        const size_t stats_b = (PFK_STATS_WORDS * sizeof(unsigned long long) + 255) & ~(size_t)255;
+        PF_TRY(pfk_malloc(&buf, stats_b + (size_t)kScanListCap * 16), "planning scan buffer");
+        unsigned long long h[PFK_STATS_WORDS];
+        auto *d = static_cast<unsigned long long *>(buf);
+        int *list = reinterpret_cast<int *>(static_cast<char *>(buf) + stats_b);
+        timer.start(stream);
+        st = pfk_plan_scan(d_row_ptr, d_col, m, n, nnz, d, list, kScanListCap, stream);
+        if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
+        if (st == PF_OK) st = pfk_stream_sync(stream);
+        if (st == PF_OK) timer.stop(stream);
+        if (st != PF_OK) {
+            pfk_free(buf);
+            return from_kernel_layer(st, "planning scan");
+        }
+        decode_stats(h, d_col, m, nnz, &s);
+        scan.list = list;
+        scan.cap = kScanListCap;
+        scan.listed = (long long)h[46];
+        scan.desc = (long long)h[47];
+        scan.checked = h[48] == 0;
+    } else if (m > 0) {
         st = pf_row_stats_compute(d_row_ptr, d_col, m, n, nnz, &s, stream);
         if (st != PF_OK) return st;
-        st = check_csr_stats(s, nnz);
-        if (st != PF_OK) return st;
     }
-    return plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan, d_col);
+    if (m > 0) {
+        st = check_csr_stats(s, nnz);
+        if (st != PF_OK) {
+            pfk_free(buf);
+            return st;
+        }
+    }
+    st = plan_build(s, d_row_ptr, m, n, nnz, dtype, variant, tile, stream, plan, d_col, &scan, &timer);
+    pfk_free(buf);
+    if (st == PF_OK) {
+        (*plan)->plan_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        (*plan)->plan_gpu_ms = timer.ok ? timer.gpu_ms : -1.0;
+    }
+    return st;
+}
+
+int pf_plan_set_band(pf_plan *plan, int band)
+{
+    if (!plan || (band != 0 && band != 1)) return fail(PF_ERR_INVALID, "band must be 0 or 1");
+    if (band && (plan->band_avail <= 0 || !plan->info.row_aligned))
+        return fail(PF_ERR_UNSUPPORTED, "this plan has no band (row-aligned FLAT, fp64 / fp32, x over 4 MB, "
+                                        "85% of the columns within a band that fits the LDS ring)");
+    plan->info.band_w = band ? plan->band_avail : 0;
+    return PF_OK;
+}
+
+int pf_plan_get_timing(const pf_plan *plan, double *plan_ms, double *plan_gpu_ms)
+{
+    if (!plan || !plan_ms || !plan_gpu_ms) return fail(PF_ERR_INVALID, "NULL plan or output");
+    *plan_ms = plan->plan_ms;
+    *plan_gpu_ms = plan->plan_gpu_ms;
+    return PF_OK;
 }
 
 int pf_plan_create(pf_plan **plan, const int *d_row_ptr, const int *d_col, int m, int n, int nnz, int dtype,
@@ -1017,6 +1175,7 @@ int pf_plan_set_row_aligned(pf_plan *plan, int row_aligned)
     plan->info.row_aligned = row_aligned;
     plan->info.needs_fixup = row_aligned ? 0 : (plan->info.ntiles > 1);
     if (row_aligned) plan->info.x_windows = 0;
+    else plan->info.band_w = 0;  // the band kernel runs row-aligned steps only
     return PF_OK;
 }
 
@@ -1130,6 +1289,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     // no row of a row-aligned tile is longer than this (longer rows take other plans), so the tile kernel can
     // load a tile's overflow with its nominal range
     a.ovf_cap = plan->info.row_aligned ? (int)std::min<long long>(PFK_ALIGN_ROW_MAX, plan->stats.max_row_len) : 0;
+    a.band_w = plan->info.band_w;  // used once the row map is recorded
     const int dt = plan->info.dtype;
     if (plan->hybrid) {
         a.ntiles = plan->run_tiles;

@@ -1,0 +1,154 @@
+"""The band kernel (k_band) on the GPU, through the C ABI.
+
+Row-aligned FLAT plans of matrices whose columns lie mostly within +-w of their row keep each step's band of
+x in an LDS ring (pf_plan_set_band; on by default for matrices of under 4 nnz per row).  The plan's first
+call searches rows with the tiles' kernel and records the row map; later calls run the band kernel.  Checked
+against the CPU oracle and against the tiles' own kernel on the same plan:
+
+* known-answer values bit for bit; U[-1,1] values within 1e-12 (fp64) / 1e-5 (fp32) of sum |a_ij x_j|;
+* the band kernel's y equals the tiles' kernel's y bit for bit (both sum each row in nnz order);
+* scaled C4 and C2, banded matrices with outliers, bands wider and narrower than the columns' spread,
+  steps of very many empty rows (windows that jump), rectangular x, fp64 and fp32;
+* graph replays of a band plan equal its eager calls;
+* pf_plan_set_band is refused for a plan without a band.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import prefree_amd as pf
+from gpu_util import NP, TORCH, assert_parity, dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _banded(m, lam, w, outliers, seed, n=None):
+    """m rows of Poisson(lam) nnz; columns within +-w of the row, a share `outliers` anywhere; sorted per row."""
+    rng = np.random.default_rng(seed)
+    n = n or m
+    lengths = rng.poisson(lam, size=m)
+    rp = np.zeros(m + 1, dtype=np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    row = np.repeat(np.arange(m, dtype=np.int64), lengths)
+    lo, hi = np.maximum(0, row - w), np.minimum(n - 1, row + w)
+    near = lo + (rng.random(len(row)) * (hi - lo + 1)).astype(np.int64)
+    col = np.where(rng.random(len(row)) < outliers, rng.integers(0, n, len(row)), near)
+    col = col[np.lexsort((col, row))]
+    return rp.astype(np.int32), col.astype(np.int32), n
+
+
+def _cases():
+    out = []
+    rp, col, _ = pf.synth_csr(4, seed=3, scale_n=1500000, dtypes=())
+    out.append(("C4", rp, col, len(rp) - 1))
+    rp, col, _ = pf.synth_csr(2, seed=3, scale_n=1100, dtypes=())
+    out.append(("C2", rp, col, len(rp) - 1))
+    out.append(("banded_w1024_o12",) + _banded(1200000, 1.0, 1024, 0.12, seed=1))
+    out.append(("banded_w64",) + _banded(1200000, 1.5, 64, 0.0, seed=2))
+    out.append(("banded_w1024_dense",) + _banded(1100000, 2.0, 1024, 0.1, seed=3))
+    out.append(("wide_x",) + _banded(700000, 3.0, 2048, 0.05, seed=4, n=2100000))
+    rng = np.random.default_rng(9)
+    m = 3000000
+    lengths = np.where(rng.random(m) < 0.05, rng.integers(1, 40, m), 0)
+    lengths[:1000] = 30  # a dense start, then long runs of empty rows
+    rp = np.zeros(m + 1, dtype=np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    row = np.repeat(np.arange(m, dtype=np.int64), lengths)
+    col = np.clip(row + rng.integers(-1500, 1501, len(row)), 0, m - 1)
+    col = col[np.lexsort((col, row))]
+    out.append(("empty_runs", rp.astype(np.int32), col.astype(np.int32), m))
+    return out
+
+
+CASES = _cases()
+
+
+def _run(rp, col, val, x, dtype, band, repeat=3):
+    m, n, nnz = len(rp) - 1, len(x), len(col)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    y = torch.full((m,), float("nan"), dtype=TORCH[dtype], device="cuda:0")
+    outs = []
+    with pf.Plan(d_rp, d_col, m, n, nnz, dtype, "flat") as p:
+        info = p.info.as_dict()
+        if band is not None:
+            p.set_band(band)
+        for _ in range(repeat):
+            y.fill_(float("nan"))
+            p.execute(d_rp, d_col, d_val, d_x, y)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        p.check()
+        info_after = p.info.as_dict()
+    return outs, info, info_after
+
+
+@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("case", range(len(CASES)), ids=[c[0] for c in CASES])
+def test_band_parity(case, dtype):
+    name, rp, col, n = CASES[case]
+    assert int(np.diff(rp).max()) <= 256
+    rng = np.random.default_rng(case)
+    for kat in (True, False):
+        if kat:
+            val, x = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
+        else:
+            val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
+            x = rng.uniform(-1, 1, n).astype(NP[dtype])
+        outs, info, after = _run(rp, col, val, x, dtype, True)
+        assert info["row_aligned"] == 1 and after["band_w"] > 0, (name, info, after)
+        for y in outs[1:]:  # the band kernel's calls: the same as the first, searching call of the tiles' kernel
+            assert np.array_equal(y, outs[0]), name
+        assert_parity(rp, col, val, x, outs[-1], dtype, exact=kat, what=f"{name}/{dtype}/kat={kat}")
+        tiles, _, _ = _run(rp, col, val, x, dtype, False, repeat=2)
+        assert np.array_equal(outs[-1], tiles[-1]), f"{name}: band and tiles kernels differ"
+
+
+def test_band_default_rule():
+    name, rp, col, n = CASES[0]  # C4: under 4 nnz per row, band on by default
+    d_rp, d_col = dev(rp), dev(col)
+    with pf.Plan(d_rp, d_col, len(rp) - 1, n, len(col), "f64", "auto") as p:
+        assert p.info.band_w == 4096, p.info.as_dict()
+    name, rp, col, n = CASES[1]  # C2: 5 nnz per row, off by default (the plan has a band to switch on)
+    d_rp, d_col = dev(rp), dev(col)
+    with pf.Plan(d_rp, d_col, len(rp) - 1, n, len(col), "f64", "auto") as p:
+        assert p.info.band_w == 0
+        p.set_band(True)
+        assert p.info.band_w > 0
+    torch.cuda.synchronize()
+
+
+def test_band_refused_without_band():
+    rp, col, _ = pf.synth_csr(2, seed=3, scale_n=300, dtypes=())  # x of 720 KB: no band
+    with pf.Plan(dev(rp), dev(col), len(rp) - 1, len(rp) - 1, len(col), "f64", "auto") as p:
+        with pytest.raises(pf.PrefreeError) as e:
+            p.set_band(True)
+        assert e.value.status == 5
+    torch.cuda.synchronize()
+
+
+def test_band_graph_replays():
+    name, rp, col, n = CASES[0]
+    m = len(rp) - 1
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device="cuda:0")
+    s = torch.cuda.Stream()
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "auto", stream=s) as p:
+        assert p.info.band_w > 0
+        with torch.cuda.stream(s):
+            p.execute(d_rp, d_col, d_val, d_x, y, stream=s)  # the first call records the map
+            p.execute(d_rp, d_col, d_val, d_x, y, stream=s)
+        s.synchronize()
+        eager = y.cpu().numpy()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            p.execute(d_rp, d_col, d_val, d_x, y, stream=torch.cuda.current_stream())
+        for _ in range(3):
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(y.cpu().numpy(), eager)
+        p.check(stream=s)
+    assert np.array_equal(eager, oracle.spmv_serial(rp, col, val, x))
