@@ -6,21 +6,29 @@
 // test_cdspmv.cpp:22-54) and print the lines the reference's tuner parses
 // ("our_perf: ... ms, our_pre: ... ms").
 //
-// Differences, all deliberate: the vendor comparison (cuSPARSE in the
-// reference) is not run; "m = .., n = .., nnz = .." is printed (the reference
-// tuner looks for "nnz =" but the harness never printed it); the wall time of
-// the whole preFreeSpMV call (allocation, host<->device copies, planning,
-// warm-up and timed launches) is printed as our_total; a failed check exits
-// with status 1 instead of printing "Success!" regardless.
+// The vendor comparison runs first, as in the reference (cuSPARSE there,
+// test_cdspmv.cpp:155-267, 307): rocSPARSE's default algorithm, 200 warm-up
+// and 4000 timed calls (PREFREE_ITERS overrides the count), printed as the
+// "cusparse_perf: ... ms, cusparse_pre: ... ms" line the reference's tuner
+// parses beside our_perf (scripts/profile_and_generate.py:293-303), followed
+// by a "vendor:" line naming rocSPARSE; cusparse_pre is rocSPARSE's analysis
+// stage.  fp64 and fp32; --no-vendor skips it.
+//
+// Differences, all deliberate: "m = .., n = .., nnz = .." is printed (the
+// reference tuner looks for "nnz =" but the harness never printed it); the
+// wall time of the whole preFreeSpMV call (allocation, host<->device copies,
+// planning, warm-up and timed launches) is printed as our_total; a failed
+// check exits with status 1 instead of printing "Success!" regardless.
 //
 // --f16 runs the reference's fp16 build (valT = half, include/common.h:43-46):
 // values are IEEE binary16 (pf_half), the sequential check rounds every product
 // and every sum to binary16 as the reference's half operators do, and the
 // relative tolerance is the reference's 1e-1 (test_cdspmv.cpp:37-52).
 //
-// usage: cdspmv <matrix.mtx> [--f32|--f16] [--variant auto|prefree|adaptive|flat] [--no-check]
+// usage: cdspmv <matrix.mtx> [--f32|--f16] [--variant auto|prefree|adaptive|flat] [--no-check] [--no-vendor]
 #include "PreFree.h"
 #include "prefree_c.h"
+#include "vendor_spmv.h"
 
 #include <chrono>
 #include <cmath>
@@ -117,8 +125,34 @@ int check(const T *ref, const T *ours, int n, double tol)
     return bad;
 }
 
+// The vendor line: rocSPARSE for fp64 / fp32 (none for fp16).
+struct Vendor {
+    bool ran = false;
+    double ms = 0, pre_ms = 0;
+    std::string why;
+};
+
 template <typename T>
-int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_check)
+Vendor run_vendor(const T *val, const int *rp, const int *col, const T *x, int m, int n, int nnz)
+{
+    Vendor v;
+    if constexpr (sizeof(T) == 2) {
+        v.why = "no fp16 vendor SpMV in this harness";
+    } else {
+        std::vector<T> y((size_t)m);
+        const char *it = std::getenv("PREFREE_ITERS");
+        const int iters = (it && *it) ? std::atoi(it) : 4000;
+        char why[256] = "";
+        if (vendor_spmv(val, rp, col, x, y.data(), m, n, nnz, 200, iters, &v.ms, &v.pre_ms, why, sizeof why) == 0)
+            v.ran = true;
+        else
+            v.why = why;
+    }
+    return v;
+}
+
+template <typename T>
+int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_check, bool do_vendor)
 {
     std::vector<T> val((size_t)nnz), x((size_t)n), y((size_t)m, from_float<T>(0.0f)), ys((size_t)m, from_float<T>(0.0f));
     init_vec(val.data(), nnz);
@@ -126,6 +160,7 @@ int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_chec
     std::printf("INIT DONE\n");
     std::printf("m = %d, n = %d, nnz = %d\n", m, n, nnz);
 
+    const Vendor vendor = do_vendor ? run_vendor(val.data(), rp, col, x.data(), m, n, nnz) : Vendor{};
     double cd_time = 0, cd_pre = 0;
     const auto t0 = std::chrono::steady_clock::now();
     preFreeSpMV(val.data(), rp, col, x.data(), y.data(), m, n, nnz, &cd_time, &cd_pre);
@@ -135,6 +170,13 @@ int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_chec
     const long long data1 = ((long long)nnz + n + m) * vb + (long long)nnz * 4 + ((long long)m + 1) * 4;
     const long long data2 = (2LL * nnz + m) * vb + (long long)nnz * 4 + ((long long)m + 1) * 4;
     std::printf("our_perf:%8.4lf ms, our_pre:%8.4lf ms\n", cd_time, cd_pre);
+    if (vendor.ran) {
+        std::printf("cusparse_perf:%8.4lf ms, cusparse_pre:%8.4lf ms\n", vendor.ms, vendor.pre_ms);
+        std::printf("vendor: rocSPARSE (rocsparse_v2_spmv, default algorithm) on this GPU; cusparse_pre is its "
+                    "analysis stage\n");
+    } else if (do_vendor) {
+        std::printf("vendor: not run (%s)\n", vendor.why.c_str());
+    }
     if (cd_time > 0)
         std::printf("our_gflops:%8.4lf, our_bandwidth1:%8.4lf GB/s, our_bandwidth2:%8.4lf GB/s\n",
                     2.0 * nnz / (cd_time * 1e6), data1 / (cd_time * 1e6), data2 / (cd_time * 1e6));
@@ -152,18 +194,20 @@ int run(const char *path, int m, int n, int nnz, int *rp, int *col, bool do_chec
 int main(int argc, char **argv)
 {
     const char *path = nullptr;
-    bool f32 = false, f16 = false, do_check = true;
+    bool f32 = false, f16 = false, do_check = true, do_vendor = true;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
         if (a == "--f32") f32 = true, f16 = false;
         else if (a == "--f16") f16 = true, f32 = false;
         else if (a == "--no-check") do_check = false;
+        else if (a == "--no-vendor") do_vendor = false;
         else if (a == "--variant" && i + 1 < argc) setenv("PREFREE_VARIANT", argv[++i], 1);
         else if (a == "-h" || a == "--help") path = nullptr, i = argc;
         else if (!path) path = argv[i];
     }
     if (!path) {
-        std::printf("Run the code by './cdspmv matrix.mtx [--f32|--f16] [--variant auto|prefree|adaptive|flat] [--no-check]'.\n");
+        std::printf("Run the code by './cdspmv matrix.mtx [--f32|--f16] [--variant auto|prefree|adaptive|flat] "
+                    "[--no-check] [--no-vendor]'.\n");
         return 0;
     }
     std::printf("\n===%s===\n\n", path);
@@ -175,9 +219,9 @@ int main(int argc, char **argv)
         std::fprintf(stderr, "cdspmv: cannot read %s: %s\n", path, pf_mtx_last_error());
         return 2;
     }
-    const int rc = f16 ? run<pf_half>(path, m, n, nnz, rp, col, do_check)
-                 : f32 ? run<float>(path, m, n, nnz, rp, col, do_check)
-                       : run<double>(path, m, n, nnz, rp, col, do_check);
+    const int rc = f16 ? run<pf_half>(path, m, n, nnz, rp, col, do_check, do_vendor)
+                 : f32 ? run<float>(path, m, n, nnz, rp, col, do_check, do_vendor)
+                       : run<double>(path, m, n, nnz, rp, col, do_check, do_vendor);
     pf_host_free(rp);
     pf_host_free(col);
     pf_host_free(val);

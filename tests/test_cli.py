@@ -58,6 +58,10 @@ def test_cli_laplacian_passes_check(tmp_path, prec, variant):
     m = re.search(r"our_perf:\s*([0-9.]+) ms, our_pre:\s*([0-9.]+) ms", r.stdout)
     assert m and float(m.group(1)) > 0
     assert f"nnz = {len(col)}" in r.stdout
+    # the vendor line the reference's tuner parses (scripts/profile_and_generate.py:299-300), from rocSPARSE
+    v = re.search(r"cusparse_perf:\s*([0-9.]+) ms, cusparse_pre:\s*([0-9.]+) ms", r.stdout)
+    assert v and float(v.group(1)) > 0 and float(v.group(2)) >= 0, r.stdout
+    assert "vendor: rocSPARSE" in r.stdout
 
 
 @pytest.mark.gpu

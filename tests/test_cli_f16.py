@@ -10,7 +10,8 @@ binary16 conversions and that SpMV are checked here:
     over the whole range, zeros, infinities, overflow and subnormals;
   * the sequential SpMV: bit for bit against oracle.spmv_serial_f16 on random
     CSR, including rows that overflow to infinity.
-A small driver compiled here includes cdspmv.cpp with its main renamed.
+A small driver compiled here includes cdspmv.cpp with its main renamed (and the
+vendor SpMV, which the fp16 paths never call, stubbed).
 """
 import os
 import subprocess
@@ -31,6 +32,11 @@ DRIVER = r'''
 #undef main
 #include <cstdio>
 #include <vector>
+// the fp16 paths run no vendor SpMV; these stand in for host/vendor_rocsparse.cpp, not linked here
+int vendor_spmv(const double *, const int *, const int *, const double *, double *, int, int, int, int, int,
+                double *, double *, char *why, int why_len) { std::snprintf(why, why_len, "not linked"); return 1; }
+int vendor_spmv(const float *, const int *, const int *, const float *, float *, int, int, int, int, int,
+                double *, double *, char *why, int why_len) { std::snprintf(why, why_len, "not linked"); return 1; }
 // usage: drv widen OUT | drv narrow IN OUT | drv spmv IN OUT
 int main(int argc, char **argv)
 {
