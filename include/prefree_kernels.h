@@ -215,9 +215,11 @@ int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nn
 int pfk_plan_scan(const int *row_ptr, const int *col, int m, int n, long long nnz, unsigned long long *d_out,
                   void *list, int cap, void *stream);
 
-/* Planning statistic of the band kernel, no counterpart in the reference: out[i] (PFK_BAND_WIDTHS unsigned
- * long long, zeroed by the call) = the nnz whose column lies within +-(64 << i) of their row.  A thread per row:
- * for matrices whose rows hold at most PFK_ALIGN_ROW_MAX nnz. */
+/* Planning statistic of the band kernel, no counterpart in the reference, over a sample of the rows (every
+ * PFK_BAND_SAMPLE-th block of 256 rows): out[i] = the sampled nnz whose column lies within +-(64 << i) of their
+ * row (i < PFK_BAND_WIDTHS), out[PFK_BAND_WIDTHS] = the sampled nnz; PFK_BAND_WIDTHS + 1 unsigned long long,
+ * zeroed by the call.  A thread per row: for matrices whose rows hold at most PFK_ALIGN_ROW_MAX nnz. */
+#define PFK_BAND_SAMPLE 8
 int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream);
 
 /* Tile descriptors of ADAPTIVE (merged=1) / FLAT (merged=0) for every tile:

@@ -135,6 +135,14 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"native library {LIB_PATH} is missing: run __graft_entry__.build() "
                                "(make -C prefree-public_amd)")
+        # One HIP runtime per process: the library needs libamdhip64.so.7, which torch's own HIP libraries
+        # also provide under that name.  Loaded after torch, the library binds to torch's runtime; loaded
+        # first, it brings in the system one, torch then loads its own copy beside it (its libraries ask for
+        # the unversioned name), and whichever of the two starts second finds no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         _sig(L.pf_version, [])
         _sig(L.pf_status_string, [_i], ctypes.c_char_p)
@@ -201,6 +209,7 @@ def klib() -> ctypes.CDLL:
         _sig(K.pfk_flat_grid, [ctypes.c_longlong, _i, ctypes.c_longlong], ctypes.c_longlong)
         _sig(K.pfk_device_name, [ctypes.c_char_p, _i])
         _sig(K.pfk_probe_gather, [_i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _vp])
+        _sig(K.pfk_band_stats, [_vp, _vp, _i, _vp, _vp])
         _sig(K.pfk_last_error, [], ctypes.c_char_p)
         _klib = K
     return _klib
@@ -400,6 +409,16 @@ def prefree_rows(row_ptr, m, nnz, tile, out, stream=None):
     """pfk_debug_prefree_rows: in-kernel first row of every tile (ntiles+1 entries, last = m)."""
     _check(klib().pfk_debug_prefree_rows(_p(row_ptr), m, nnz, tile, _p(out), _s(stream)),
            "pfk_debug_prefree_rows")
+
+
+def band_stats(row_ptr, col, m, out, stream=None):
+    """pfk_band_stats: over every BAND_SAMPLE-th block of 256 rows, out[i] = the nnz with |col - row| <= 64 << i
+    (i < BAND_WIDTHS), out[BAND_WIDTHS] = the sampled nnz; `out` int64[BAND_WIDTHS + 1]."""
+    _check(klib().pfk_band_stats(_p(row_ptr), _p(col), int(m), _p(out), _s(stream)), "pfk_band_stats")
+
+
+BAND_WIDTHS = 9   # PFK_BAND_WIDTHS
+BAND_SAMPLE = 8   # PFK_BAND_SAMPLE
 
 
 def adaptive_long_row_min(dtype, tile) -> int:

@@ -2300,18 +2300,27 @@ __global__ __launch_bounds__(kBandBS) void k_band(Args<T> a, BandArgs b)
 // Planning statistic of the band kernel: out[i] = the nnz whose column lies
 // within +-(64 << i) of their row, i < PFK_BAND_WIDTHS.  A thread per row
 // (row-aligned plans: rows of at most PFK_ALIGN_ROW_MAX nnz).
+// A sample: the rows of every PFK_BAND_SAMPLE-th block of kBS rows, spread over
+// the whole matrix; out[PFK_BAND_WIDTHS] counts the sampled nnz.  The count
+// only chooses w (the band kernel gives the same sums for any w), so a sample
+// serves, at an eighth of the reads.
 __global__ __launch_bounds__(kBS) void k_band_stats(const int *__restrict__ rp, const int *__restrict__ col, int m,
                                                     unsigned long long *__restrict__ out)
 {
-    __shared__ unsigned long long s_c[PFK_BAND_WIDTHS];
+    __shared__ unsigned long long s_c[PFK_BAND_WIDTHS + 1];
     const int tid = threadIdx.x;
-    if (tid < PFK_BAND_WIDTHS) s_c[tid] = 0;
+    if (tid <= PFK_BAND_WIDTHS) s_c[tid] = 0;
     __syncthreads();
-    unsigned int cnt[PFK_BAND_WIDTHS];
+    unsigned int cnt[PFK_BAND_WIDTHS + 1];
 #pragma unroll
-    for (int i = 0; i < PFK_BAND_WIDTHS; ++i) cnt[i] = 0;
-    for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
+    for (int i = 0; i <= PFK_BAND_WIDTHS; ++i) cnt[i] = 0;
+    for (long long blk = (long long)blockIdx.x * PFK_BAND_SAMPLE; blk * kBS < m;
+         blk += (long long)gridDim.x * PFK_BAND_SAMPLE) {
+        const long long r = blk * kBS + tid;
+        if (r >= m)
+            continue;
         const int a0 = rp[r], a1 = rp[r + 1];
+        cnt[PFK_BAND_WIDTHS] += (unsigned)max(a1 - a0, 0);
         for (int j = a0; j < a1; ++j) {
             const long long d = llabs((long long)col[j] - r);
 #pragma unroll
@@ -2319,10 +2328,10 @@ __global__ __launch_bounds__(kBS) void k_band_stats(const int *__restrict__ rp, 
         }
     }
 #pragma unroll
-    for (int i = 0; i < PFK_BAND_WIDTHS; ++i)
+    for (int i = 0; i <= PFK_BAND_WIDTHS; ++i)
         if (cnt[i]) atomicAdd(&s_c[i], (unsigned long long)cnt[i]);
     __syncthreads();
-    if (tid < PFK_BAND_WIDTHS && s_c[tid]) atomicAdd(out + tid, s_c[tid]);
+    if (tid <= PFK_BAND_WIDTHS && s_c[tid]) atomicAdd(out + tid, s_c[tid]);
 }
 
 // ---- k_dense: dense rows by x windows staged in LDS (hybrid plans) -----------
@@ -3507,23 +3516,46 @@ __global__ void k_stats_init(unsigned long long *out)
 // Row statistics; with a list (the planning scan), every row over
 // PFK_ALIGN_ROW_MAX nnz is also appended to it as (row, first nnz, end, 0),
 // the first `cap` of them (out[kStLongListed] counts them all).
-__global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, int m,
-                                                   unsigned long long *__restrict__ out, int4 *__restrict__ list,
-                                                   int cap)
+constexpr int kStatsBS = 1024;  // k_row_stats: one workgroup of 16 waves per CU
+constexpr int kStatsRows = 8;   // rows per lane and pass: row_ptr[r0, r0 + 8] as two 16-byte loads and one 4-byte load
+constexpr int kStatsBins = 8;   // histogram bins a lane counts in registers (rows of under 128 nnz)
+
+template <typename Op>
+__device__ __forceinline__ unsigned int wave_reduce_u32(unsigned int v, Op op)
+{
+    v = op(v, dpp<kDppXor1>(v));
+    v = op(v, dpp<kDppXor2>(v));
+    v = op(v, dpp<kDppHalfMirror>(v));
+    v = op(v, dpp<kDppMirror>(v));
+    v = op(v, (unsigned int)__builtin_amdgcn_ds_swizzle((int)v, swizzle_xor_pattern<16>()));
+    return op((unsigned int)__builtin_amdgcn_readlane((int)v, 0), (unsigned int)__builtin_amdgcn_readlane((int)v, 32));
+}
+
+// Each workgroup takes a contiguous range of rows; its lanes read row_ptr in
+// groups of kStatsRows rows.  Every statistic is reduced over the wave before
+// it meets LDS, and over the workgroup before it meets memory: a few global
+// atomics per workgroup, with one workgroup per CU.
+__global__ __launch_bounds__(kStatsBS) void k_row_stats(const int *__restrict__ rp, int m,
+                                                        unsigned long long *__restrict__ out,
+                                                        int4 *__restrict__ list, int cap)
 {
     __shared__ unsigned int s_hist[33];
     __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev, s_far;
     const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
     if (tid < 33) s_hist[tid] = 0;
     if (tid == 0) {
         s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; s_dev = 0; s_far = 0;
     }
     __syncthreads();
-    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0, lshort = 0;
+    unsigned int lmax = 0, lmin = 0xFFFFFFFFu, lempty = 0, ldec = 0, lover = 0, lshort = 0, lfar = 0;
+    unsigned int hc[kStatsBins];
+#pragma unroll
+    for (int i = 0; i < kStatsBins; ++i) hc[i] = 0;
     // distance in rows between row r and where the matrix's mean density puts row_ptr[r] (the row
     // searches' first guess), largest over the rows; 0 when row_ptr[m] is not positive
     const int total = rp[m];
-    const double per = total > 0 ? (double)m / (double)total : 0.0;
+    const double per_nnz = total > 0 ? (double)m / (double)total : 0.0;
     double ldev = 0.0;
     // rows more than 28 rows from the line through (row_ptr[m / 4], m / 4) and (row_ptr[3m / 4], 3m / 4), the
     // row-aligned tiles' alternative first guess (every row counts when the line is undefined)
@@ -3532,43 +3564,85 @@ __global__ __launch_bounds__(kBS) void k_row_stats(const int *__restrict__ rp, i
     const bool line = m >= 4 && p3 > p1;
     const double la = line ? (double)(q3 - q1) / ((double)p3 - (double)p1) : 0.0;
     const double lb = line ? (double)q1 - la * (double)p1 : 0.0;
-    unsigned int lfar = 0;
-    for (long long r = (long long)blockIdx.x * kBS + tid; r < m; r += (long long)gridDim.x * kBS) {
-        if (total > 0) ldev = fmax(ldev, fabs((double)r - (double)rp[r] * per));
-        lfar += !line || fabs((double)r - (la * (double)rp[r] + lb)) > 28.0;
-        int len = rp[r + 1] - rp[r];
-        if (len < 0) { ++ldec; len = 0; }
-        const unsigned int u = (unsigned int)len;
-        lmax = max(lmax, u);
-        lmin = min(lmin, u);
-        lempty += (u == 0);
-        lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
-        if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
-        if (list && u > (unsigned)PFK_ALIGN_ROW_MAX) {  // rare: one atomic per long row
-            const unsigned long long k = atomicAdd(out + kStLongListed, 1ull);
-            if (k < (unsigned long long)cap) list[k] = make_int4((int)r, rp[r], rp[r] + (int)u, 0);
+    const long long per = (((long long)m + gridDim.x - 1) / gridDim.x + kStatsRows - 1) / kStatsRows * kStatsRows;
+    const long long rb = (long long)blockIdx.x * per;
+    const long long re = min((long long)m, rb + per);
+    if (rb < re) {
+        // row_ptr[rb, re]: entries past it read zeros (only for rows past re, which are skipped)
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(rp + rb, (re - rb + 1) * 4);
+        const int ng = (int)((re - rb + kStatsRows - 1) / kStatsRows);
+        for (int g = tid; g < ng; g += kStatsBS) {
+            const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32, 0, kAuxNt);
+            const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32 + 16, 0, kAuxNt);
+            const int v8 = (int)__builtin_amdgcn_raw_buffer_load_b32(rr, g * 32 + 32, 0, 0);
+            const int e[kStatsRows + 1] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w,
+                                           (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w, v8};
+#pragma unroll
+            for (int i = 0; i < kStatsRows; ++i) {
+                const long long r = rb + (long long)g * kStatsRows + i;
+                if (r >= re)
+                    break;
+                if (total > 0) ldev = fmax(ldev, fabs((double)r - (double)e[i] * per_nnz));
+                lfar += !line || fabs((double)r - (la * (double)e[i] + lb)) > 28.0;
+                int len = e[i + 1] - e[i];
+                if (len < 0) { ++ldec; len = 0; }
+                const unsigned int u = (unsigned int)len;
+                lmax = max(lmax, u);
+                lmin = min(lmin, u);
+                lempty += (u == 0);
+                lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
+                if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
+                if (list && u > (unsigned)PFK_ALIGN_ROW_MAX) {  // rare: one atomic per long row
+                    const unsigned long long k = atomicAdd(out + kStLongListed, 1ull);
+                    if (k < (unsigned long long)cap) list[k] = make_int4((int)r, e[i], e[i] + (int)u, 0);
+                }
+                const int bin = u == 0 ? 0 : 32 - __clz(u);
+                if (bin < kStatsBins) {
+#pragma unroll
+                    for (int k = 0; k < kStatsBins; ++k) hc[k] += bin == k ? 1u : 0u;
+                } else {
+                    atomicAdd(&s_hist[bin], 1u);  // rows of 128 nnz or more
+                }
+            }
         }
-        atomicAdd(&s_hist[u == 0 ? 0 : 32 - __clz(u)], 1u);
     }
-    atomicMax(&s_max, lmax);
-    atomicMin(&s_min, lmin);
-    atomicAdd(&s_empty, lempty);
-    atomicAdd(&s_dec, ldec);
-    atomicAdd(&s_over, lover);
-    atomicMax(&s_short, lshort);
-    atomicMax(&s_dev, (unsigned int)fmin(ceil(ldev), 4294967295.0));
-    atomicAdd(&s_far, lfar);
+    const auto add = [](unsigned int x, unsigned int y) { return x + y; };
+    const auto mx = [](unsigned int x, unsigned int y) { return max(x, y); };
+    const auto mn = [](unsigned int x, unsigned int y) { return min(x, y); };
+#pragma unroll
+    for (int k = 0; k < kStatsBins; ++k) {
+        const unsigned int c = wave_reduce_u32(hc[k], add);
+        if (lane == 0 && c) atomicAdd(&s_hist[k], c);
+    }
+    lmax = wave_reduce_u32(lmax, mx);
+    lmin = wave_reduce_u32(lmin, mn);
+    lempty = wave_reduce_u32(lempty, add);
+    ldec = wave_reduce_u32(ldec, add);
+    lover = wave_reduce_u32(lover, add);
+    lshort = wave_reduce_u32(lshort, mx);
+    lfar = wave_reduce_u32(lfar, add);
+    const unsigned int udev = wave_reduce_u32((unsigned int)fmin(ceil(ldev), 4294967295.0), mx);
+    if (lane == 0) {
+        atomicMax(&s_max, lmax);
+        atomicMin(&s_min, lmin);
+        atomicAdd(&s_empty, lempty);
+        atomicAdd(&s_dec, ldec);
+        atomicAdd(&s_over, lover);
+        atomicMax(&s_short, lshort);
+        atomicMax(&s_dev, udev);
+        atomicAdd(&s_far, lfar);
+    }
     __syncthreads();
     if (tid < 33 && s_hist[tid]) atomicAdd(out + kStHist + tid, (unsigned long long)s_hist[tid]);
     if (tid == 0) {
         atomicMax(out + kStMax, (unsigned long long)s_max);
         atomicMin(out + kStMin, (unsigned long long)s_min);
-        atomicAdd(out + kStEmpty, (unsigned long long)s_empty);
-        atomicAdd(out + kStDec, (unsigned long long)s_dec);
-        atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
+        if (s_empty) atomicAdd(out + kStEmpty, (unsigned long long)s_empty);
+        if (s_dec) atomicAdd(out + kStDec, (unsigned long long)s_dec);
+        if (s_over) atomicAdd(out + kStOverAlign, (unsigned long long)s_over);
         atomicMax(out + kStMaxShort, (unsigned long long)s_short);
         atomicMax(out + kStGuessDev, (unsigned long long)s_dev);
-        atomicAdd(out + kStLineFar, (unsigned long long)s_far);
+        if (s_far) atomicAdd(out + kStLineFar, (unsigned long long)s_far);
         if (blockIdx.x == 0) {
             out[kStFirst] = (unsigned long long)(long long)rp[0];
             out[kStLast] = (unsigned long long)(long long)rp[m];
@@ -3624,9 +3698,15 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
     const int nvec = (int)((j1 - j0 + 3) / 4);
     for (int v0 = tid; v0 < nvec; v0 += 4 * kBS) {
         u32x4 c[4];
+        int nx[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int u = 0; u < 4; ++u)  // four loads in flight per lane; vectors past the range read zeros
             c[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, (v0 + u * kBS) * 16, 0, kAuxNt);
+        if (nrows > 0) {  // workgroup-uniform: the entry after each vector, issued with the vectors
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                nx[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rn, (v0 + u * kBS) * 16 + 16, 0, 0);
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const long long jb = j0 + 4ll * (v0 + u * kBS);
@@ -3635,8 +3715,7 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
             for (int i = 0; i < 4; ++i)
                 bad += (jb + i < j1 && (e[i] < 0 || e[i] >= n)) ? 1u : 0u;
             if (nrows > 0 && jb < j1) {  // descents inside listed rows (rare: sorted rows have none)
-                const int nx = (int)__builtin_amdgcn_raw_buffer_load_b32(rn, (int)(jb - j0 + 4) * 4, 0, 0);
-                const int f[5] = {e[0], e[1], e[2], e[3], nx};
+                const int f[5] = {e[0], e[1], e[2], e[3], nx[u]};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const long long j = jb + i;
@@ -4123,8 +4202,12 @@ int launch_stats(const int *row_ptr, const int *col, int m, int n, long long nnz
     hipLaunchKernelGGL(k_stats_init, dim3(1), dim3(64), 0, S(stream), d_out);
     PFK_LAUNCHED("k_stats_init");
     if (m > 0) {
-        const unsigned grid = grid_for(m, kBS, 2048);
-        hipLaunchKernelGGL(k_row_stats, dim3(grid), dim3(kBS), 0, S(stream), row_ptr, m, d_out, list, cap);
+        // a workgroup per CU (fewer for small m), each row range within a buffer resource's reach
+        const long long rows_wg = (long long)kStatsBS * kStatsRows;
+        long long grid = std::min<long long>(((long long)m + rows_wg - 1) / rows_wg, std::max(1, device_cus()));
+        grid = std::max<long long>(grid, ((long long)m + (1ll << 26) - 1) >> 26);
+        hipLaunchKernelGGL(k_row_stats, dim3((unsigned)grid), dim3(kStatsBS), 0, S(stream), row_ptr, m, d_out, list,
+                           cap);
         PFK_LAUNCHED("k_row_stats");
     }
     if (col && nnz > 0) {
@@ -4360,10 +4443,12 @@ int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long
 {
     if (!row_ptr || !out || m < 0 || (m > 0 && !col)) return PF_ERR_INVALID;
     hipLaunchKernelGGL(k_fill_zero, dim3(1), dim3(kBS), 0, S(stream), reinterpret_cast<uint32_t *>(out),
-                       (size_t)(2 * PFK_BAND_WIDTHS));
+                       (size_t)(2 * (PFK_BAND_WIDTHS + 1)));
     PFK_LAUNCHED("k_fill_zero");
     if (m > 0) {
-        hipLaunchKernelGGL(k_band_stats, dim3(grid_for(m, kBS, 4096)), dim3(kBS), 0, S(stream), row_ptr, col, m, out);
+        const long long blocks = (m + kBS - 1) / kBS;
+        hipLaunchKernelGGL(k_band_stats, dim3(grid_for(blocks, PFK_BAND_SAMPLE, 4096)), dim3(kBS), 0, S(stream),
+                           row_ptr, col, m, out);
         PFK_LAUNCHED("k_band_stats");
     }
     return PF_OK;

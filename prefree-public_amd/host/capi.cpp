@@ -828,7 +828,9 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     if (st == PF_OK) st = pfk_stream_sync(stream);
     if (st == PF_OK && timer) timer->stop(stream);
     if (st != PF_OK) return from_kernel_layer(st, "hybrid tables");
-    if (!p->aux_stream) {  // without them the kernels run in sequence on the caller's stream
+    // a second stream only where the runs run beside the dense rows (x within one XCD's L2; creating a
+    // stream costs milliseconds); without it the kernels run in sequence on the caller's stream
+    if (!p->aux_stream && xb <= kXcdL2Bytes) {
         if (pfk_stream_create(&p->aux_stream) != PF_OK) p->aux_stream = nullptr;
         if (p->aux_stream && (pfk_event_create_fence(&p->ev_fork) != PF_OK ||
                               pfk_event_create_fence(&p->ev_join) != PF_OK)) {
@@ -844,9 +846,10 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     return PF_OK;
 }
 
-// The band kernel for a row-aligned plan: measures how many columns lie
-// within +-w of their row (w = 64 << i) and keeps the smallest w that holds 85%
-// of the nnz and, with two steps' rows, fits the kernel's LDS ring.  On by
+// The band kernel for a row-aligned plan: measures (on a sample of the rows)
+// how many columns lie within +-w of their row (w = 64 << i) and keeps the
+// smallest w that holds 85% of the nnz and, with two steps' rows, fits the
+// kernel's LDS ring.  On by
 // default for matrices of under 4 nnz per row on average (each row's x entry
 // is then a large part of the stream, and the band's gathers cost most).
 int try_band(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream, PlanTimer *timer)
@@ -858,7 +861,7 @@ int try_band(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream, P
         nnz < 64LL * PFK_BAND_STEP || m < 1)
         return PF_OK;
     unsigned long long *d = nullptr;
-    unsigned long long h[PFK_BAND_WIDTHS];
+    unsigned long long h[PFK_BAND_WIDTHS + 1];
     PF_TRY(pfk_malloc(reinterpret_cast<void **>(&d), sizeof h), "band statistic");
     if (timer) timer->start(stream);
     int st = pfk_band_stats(d_row_ptr, d_col, p->m, d, stream);
@@ -871,7 +874,7 @@ int try_band(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream, P
     for (int i = 0; i < PFK_BAND_WIDTHS; ++i) {
         const long long w = 64LL << i;
         if (2 * w + 2 * rows_per_step > PFK_BAND_RING) break;
-        if ((double)h[i] >= 0.85 * (double)nnz) {
+        if ((double)h[i] >= 0.85 * (double)h[PFK_BAND_WIDTHS]) {  // of the sampled nnz
             p->band_avail = (int)w;
             break;
         }

@@ -152,3 +152,26 @@ def test_band_graph_replays():
             assert np.array_equal(y.cpu().numpy(), eager)
         p.check(stream=s)
     assert np.array_equal(eager, oracle.spmv_serial(rp, col, val, x))
+
+
+def _band_stats_np(rp, col):
+    """pfk_band_stats restated: over the rows of every BAND_SAMPLE-th block of 256 rows, the nnz within
+    +-(64 << i) of their row, and the sampled nnz."""
+    m = len(rp) - 1
+    blk = np.arange(m) // 256
+    rows = np.flatnonzero(blk % pf.BAND_SAMPLE == 0)
+    lens = np.diff(rp.astype(np.int64))[rows]
+    row = np.repeat(rows.astype(np.int64), lens)
+    idx = np.concatenate([np.arange(rp[r], rp[r + 1]) for r in rows]) if len(row) else np.zeros(0, np.int64)
+    d = np.abs(col[idx].astype(np.int64) - row)
+    return [int((d <= (64 << i)).sum()) for i in range(pf.BAND_WIDTHS)] + [len(row)]
+
+
+@pytest.mark.parametrize("case", ["C2", "banded_w64", "empty_runs"])
+def test_band_stats_sample(case):
+    """The planning statistic equals its restatement over the same sample of rows."""
+    _, rp, col, n = [c for c in CASES if c[0] == case][0]
+    out = torch.zeros(pf.BAND_WIDTHS + 1, dtype=torch.int64, device="cuda")
+    pf.band_stats(dev(rp), dev(col), len(rp) - 1, out)
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == _band_stats_np(rp, col), case

@@ -16,15 +16,17 @@ def cases():
     for cfg, scale in ((1, 0), (2, 300), (3, 60000), (4, 400000), (5, 40000)):
         rp, col, _ = pf.synth_csr(cfg, seed=4, scale_n=scale, dtypes=())
         out.append((f"C{cfg}", rp, col, len(rp) - 1))
+    # more rows than the statistics' workgroups take at 8 rows per lane (a workgroup per CU, several passes)
+    rp, col, _ = pf.synth_csr(3, seed=5, scale_n=2600001, dtypes=())
+    out.append(("C3_2.6M", rp, col, len(rp) - 1))
     return out
 
 
 def expected(rp, col, n):
     m, nnz = len(rp) - 1, int(rp[-1])
     lens = np.diff(rp.astype(np.int64))
-    hist = np.zeros(33, dtype=np.int64)
-    for L in lens:
-        hist[0 if L == 0 else int(L).bit_length()] += 1
+    bits = np.where(lens > 0, np.frexp(lens.astype(np.float64))[1], 0)  # bit_length of each length
+    hist = np.bincount(bits, minlength=33).astype(np.int64)
     short = lens[lens <= ALIGN_MAX]
     dev = 0
     if m > 0 and nnz > 0:
@@ -46,7 +48,10 @@ def expected(rp, col, n):
                 line_far_rows=far, hist=hist)
 
 
-@pytest.mark.parametrize("name,rp,col,n", cases(), ids=[c[0] for c in cases()])
+CASES = cases()
+
+
+@pytest.mark.parametrize("name,rp,col,n", CASES, ids=[c[0] for c in CASES])
 def test_row_stats_match_numpy(name, rp, col, n):
     m, nnz = len(rp) - 1, int(rp[-1])
     s = pf.row_stats(dev(rp), dev(col) if nnz else None, m, n, nnz)
