@@ -187,7 +187,9 @@ int pf_plan_set_chunk_nnz(pf_plan *plan, long long chunk_nnz);
  * The tile size (pf_plan_create_tuned: 512 or 1024 nnz) is the reference's P_NNZ 4 or 8. */
 int pf_plan_set_ladder(pf_plan *plan, int ladder);
 /* Plans that PF_AUTO made hybrid (pf_plan_info.hybrid): 0 = split-row FLAT tiles instead, 1 = back to
- * hybrid.  Both give y within rounding of each other (the dense rows' partial sums differ in order). */
+ * hybrid.  Both give y within rounding of each other (the dense rows' partial sums differ in order).  A hybrid
+ * plan is built without the split-row workspace (pf_plan_info.workspace_bytes): the first switch to 0
+ * allocates and initialises it on the default stream and synchronises that stream. */
 int pf_plan_set_hybrid(pf_plan *plan, int hybrid);
 /* Hybrid plans: 1 = run tiles per half of x (see pf_plan_info.x_halves), 0 = once each. */
 int pf_plan_set_x_halves(pf_plan *plan, int x_halves);

@@ -443,7 +443,9 @@ struct pf_plan {
     int band_avail = 0;                        // band width the band kernel may use (0: the plan has no band)
     pf_plan_info info{};
     pf_row_stats stats{};
-    void *ws = nullptr;
+    void *ws = nullptr;        // the error flag, and (ws_split == nullptr) the split-row arrays after it
+    void *ws_split = nullptr;  // a hybrid plan's split-row arrays, allocated once pf_plan_set_hybrid(plan, 0) asks
+    bool split_ready = true;   // the split-row arrays exist (a hybrid plan is built without them)
     void *head = nullptr;
     void *tail = nullptr;
     int *owner = nullptr;
@@ -519,13 +521,13 @@ int plan_info(const pf_row_stats &s, int n, int dtype, int variant, int tile, pf
 
 // Points the plan's arrays into its workspace `w` (info.workspace_bytes bytes,
 // 256-byte aligned): error flag, head / tail slots, owners, row map, schedule.
-void plan_carve(pf_plan *p, void *w0)
+// The split-row arrays of a workspace block of info.workspace_bytes (its first
+// 256 bytes hold the error flag).
+void plan_carve_split(pf_plan *p, void *w0)
 {
     const pf_plan_info &info = p->info;
     char *w = static_cast<char *>(w0);
     const size_t total = info.workspace_bytes;
-    p->ws = w0;
-    p->err = reinterpret_cast<int *>(w);
     if (info.variant != PF_PREFREE) {
         const size_t vb = (size_t)slot_bytes(info.dtype);
         const size_t slots = ((size_t)info.ntiles * vb + 255) & ~(size_t)255;
@@ -546,17 +548,25 @@ void plan_carve(pf_plan *p, void *w0)
             p->sched_bytes = total - (owner_at + owners + map);
         }
     }
+    p->split_ready = true;
+}
+
+void plan_carve(pf_plan *p, void *w0)
+{
+    p->ws = w0;
+    p->err = static_cast<int *>(w0);
+    plan_carve_split(p, w0);
 }
 
 // Fresh workspace state on `stream` (fill kernels, no memset): error flag
 // clear, every owner slot "no split row" (a combine kernel never reads an
 // unset slot), and ADAPTIVE's split-row owner table, which depends on
 // row_ptr only.  Asynchronous.
-int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
+int plan_init_split(pf_plan *p, const int *d_row_ptr, void *stream)
 {
     const pf_plan_info &info = p->info;
-    int rc = pfk_fill_zero(p->err, 256, stream);
-    if (rc == PF_OK && p->owner) rc = pfk_fill_u32(p->owner, (size_t)info.ntiles, 0xFFFFFFFFu, stream);
+    int rc = PF_OK;
+    if (p->owner) rc = pfk_fill_u32(p->owner, (size_t)info.ntiles, 0xFFFFFFFFu, stream);
     if (rc == PF_OK && info.variant == PF_ADAPTIVE && info.needs_fixup) {
         pfk_spmv_args a;
         std::memset(&a, 0, sizeof a);
@@ -574,6 +584,35 @@ int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
         rc = pfk_adaptive_owners(info.dtype, &a, stream);
     }
     return rc;
+}
+
+int plan_init(pf_plan *p, const int *d_row_ptr, void *stream)
+{
+    const int rc = pfk_fill_zero(p->err, 256, stream);
+    return rc == PF_OK ? plan_init_split(p, d_row_ptr, stream) : rc;
+}
+
+// The split-row arrays of a plan built without them (a hybrid plan), in a
+// block of their own: the error flag stays where it is.  Synchronises the
+// default stream.
+int plan_add_split(pf_plan *p)
+{
+    if (p->split_ready) return PF_OK;
+    void *w = nullptr;
+    PF_TRY(pfk_malloc(&w, p->info.workspace_bytes), "split-row workspace");
+    plan_carve_split(p, w);
+    int rc = plan_init_split(p, nullptr, nullptr);  // FLAT: no row_ptr needed
+    if (rc == PF_OK) rc = pfk_stream_sync(nullptr);
+    if (rc != PF_OK) {
+        pfk_free(w);
+        p->head = p->tail = nullptr;
+        p->owner = p->row_map = p->sched = nullptr;
+        p->head_bytes = p->tail_bytes = p->owner_bytes = p->row_map_bytes = p->sched_bytes = 0;
+        p->split_ready = false;
+        return from_kernel_layer(rc, "split-row workspace");
+    }
+    p->ws_split = w;
+    return PF_OK;
 }
 
 // Dense-row threshold of a hybrid plan: a power of two at least 4096 and at
@@ -902,20 +941,40 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     p->nnz = nnz;
     p->info = info;
     p->stats = s;
+    // A hybrid candidate starts with the error flag alone: a hybrid plan runs without the split-row arrays
+    // (C5: their 7 MB took 0.3 ms to allocate), which come later if pf_plan_set_hybrid(plan, 0) asks.
+    const bool candidate = want_hybrid && hybrid_candidate(s, n, dtype, info, d_col);
     void *w = nullptr;
-    int rc = pfk_malloc(&w, info.workspace_bytes);
+    int rc = pfk_malloc(&w, candidate ? 256 : info.workspace_bytes);
     if (rc != PF_OK) {
         delete p;
         return from_kernel_layer(rc, "plan workspace");
     }
-    plan_carve(p, w);
+    if (candidate) {
+        p->ws = w;
+        p->err = static_cast<int *>(w);
+        p->split_ready = false;
+    } else {
+        plan_carve(p, w);
+    }
     if (timer) timer->start(stream);
-    rc = plan_init(p, d_row_ptr, stream);
+    rc = candidate ? pfk_fill_zero(p->err, 256, stream) : plan_init(p, d_row_ptr, stream);
     if (rc == PF_OK) rc = pfk_stream_sync(stream);
     if (rc == PF_OK && timer) timer->stop(stream);
-    if (rc == PF_OK && d_col) rc = try_band(p, d_row_ptr, d_col, stream, timer);
-    if (rc == PF_OK && want_hybrid && hybrid_candidate(s, n, dtype, p->info, d_col)) {
+    if (rc == PF_OK && d_col && !candidate) rc = try_band(p, d_row_ptr, d_col, stream, timer);
+    if (rc == PF_OK && candidate) {
         rc = try_hybrid(p, d_row_ptr, d_col, stream, scan, timer);
+        if (rc == PF_OK && !p->hybrid) {  // stays split-row: its arrays now
+            void *full = nullptr;
+            rc = pfk_malloc(&full, info.workspace_bytes);
+            if (rc == PF_OK) {
+                pfk_free(p->ws);
+                plan_carve(p, full);
+                rc = plan_init(p, d_row_ptr, stream);
+                if (rc == PF_OK) rc = pfk_stream_sync(stream);
+            }
+            if (rc != PF_OK) rc = from_kernel_layer(rc, "plan workspace");
+        }
         if (rc != PF_OK) {
             pfk_free(p->ws_hyb);
             pfk_free(p->ws);
@@ -1207,6 +1266,10 @@ int pf_plan_set_hybrid(pf_plan *plan, int hybrid)
     if (!plan || (hybrid != 0 && hybrid != 1)) return fail(PF_ERR_INVALID, "hybrid must be 0 or 1");
     if (hybrid && !plan->ws_hyb)
         return fail(PF_ERR_UNSUPPORTED, "this plan has no hybrid tables (its rows over 256 nnz are not summed apart)");
+    if (!hybrid) {
+        const int st = plan_add_split(plan);
+        if (st != PF_OK) return st;
+    }
     plan->hybrid = hybrid != 0;
     plan->info.hybrid = hybrid;
     plan->info.x_halves = hybrid ? (plan->x_halves ? 1 : 0) : plan->info.x_halves;
@@ -1341,6 +1404,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         if (plan->remember_rows) plan->hyb_map_ready = true;  // later calls read what this one recorded
         return PF_OK;
     }
+    if (!plan->split_ready) return fail(PF_ERR_KERNEL, "plan has no split-row workspace");
     if (a.sched && !plan->map_ready)  // the recording call starts from empty lists
         PF_TRY(pfk_fill_zero(a.sched, 16 * sizeof(int), stream), "schedule reset");
     switch (plan->info.variant) {
@@ -1384,6 +1448,10 @@ int pf_plan_destroy(pf_plan *plan)
         pfk_stream_destroy(plan->aux_stream);
     }
     int st = pfk_free(plan->ws);
+    if (plan->ws_split) {
+        const int st2 = pfk_free(plan->ws_split);
+        if (st == PF_OK) st = st2;
+    }
     if (plan->ws_hyb) {
         const int st2 = pfk_free(plan->ws_hyb);
         if (st == PF_OK) st = st2;
