@@ -189,6 +189,10 @@ int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *str
 /* ADAPTIVE planning step: owner_row[t] = the row whose split starts in tile t, else -1, for every
  * tile (a function of row_ptr and the tiling only; pfk_spmv_adaptive no longer writes it). */
 int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream);
+/* PREFREE zeroes y and runs the reference kernel; fp64/fp32 add each tile-boundary row's partials to y with
+ * atomics.  fp16 keeps them in fp32 instead, in head_slot / tail_slot (ntiles floats each: the partial of a
+ * tile's first / last row), with each tile's row range in owner_row (2 ints per tile); a second kernel adds a
+ * row's partials in tile order and stores it rounded to half once. */
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
 /* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count. */
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap);

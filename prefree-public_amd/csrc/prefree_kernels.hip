@@ -131,7 +131,8 @@ constexpr int adaptive_lmax(int K) { return (K == 238 || K == 494) ? 16 : (K <= 
 // ADAPTIVE tile sizes compiled in, per value type: X(type, dtype code, keys per tile).
 #define PF_ADAPTIVE_TILES(X) \
     X(double, PF_F64, 188) X(double, PF_F64, 238) X(double, PF_F64, 494) X(double, PF_F64, 512) \
-    X(float, PF_F32, 440) X(float, PF_F32, 494) X(float, PF_F32, 1024)
+    X(float, PF_F32, 440) X(float, PF_F32, 494) X(float, PF_F32, 1024) \
+    X(half_t, PF_F16, 440) X(half_t, PF_F16, 494) X(half_t, PF_F16, 1024)
 
 // Logical tile of this workgroup.  Workgroups go to the XCDs round robin
 // (XCD x = blockIdx % 8).  The tiles are cut into chunks of xch contiguous
@@ -804,7 +805,7 @@ __device__ __forceinline__ void wave_issue_cv(const Args<T> &a, const WaveDesc &
     const int base = d.A & ~3;
     const long long n = d.B > d.A ? d.B - base : 0;
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + base, n * 4);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + base, n * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + base, val_range_bytes<T>((int)n));
     const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
     for (int k = 0; k < VPT; ++k)
@@ -859,25 +860,26 @@ template <typename T, int K, int LMAX, bool DESC_ONLY, bool NT = true, int WPE =
 __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8))) void k_wave(Args<T> a, int *__restrict__ dbg)
 {
     using S = WaveShape<T, K, LMAX>;
+    using A = acc_t<T>;  // products and sums (fp32 in the fp16 mode)
     constexpr int VPT = S::kVPT, Q = S::kQ, RPL = S::kRPL, LCAP = S::kListCap, CAP = S::kRpCap;
     constexpr int NW = kWaveWG / kWave;
-    __shared__ __attribute__((aligned(16))) T s_prod_all[NW][DESC_ONLY ? 4 : S::kProd];
+    __shared__ __attribute__((aligned(16))) A s_prod_all[NW][DESC_ONLY ? 4 : S::kProd];
     __shared__ int s_rpb_all[NW][2][DESC_ONLY ? 4 : CAP];
     __shared__ int s_la_all[NW][LCAP], s_lb_all[NW][LCAP];
-    __shared__ T s_ls_all[NW][LCAP];
+    __shared__ A s_ls_all[NW][LCAP];
     // Row sums staged for the y stores: a buffer of their own when LDS allows
     // (one 4-nnz vector per lane), else the product buffer after the sums.
     constexpr bool YL = S::kVPT == 1 && !DESC_ONLY;
-    __shared__ __attribute__((aligned(16))) T s_y_all[NW][YL ? K + 1 : 1];
+    __shared__ __attribute__((aligned(16))) A s_y_all[NW][YL ? K + 1 : 1];
     __shared__ int s_li_all[NW][YL ? LCAP : 1];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    T *s_prod = s_prod_all[wave];
+    A *s_prod = s_prod_all[wave];
     int *s_la = s_la_all[wave];
     int *s_lb = s_lb_all[wave];
-    T *s_ls = s_ls_all[wave];
-    T *s_y = YL ? s_y_all[wave] : s_prod;
+    A *s_ls = s_ls_all[wave];
+    A *s_y = YL ? s_y_all[wave] : s_prod;
     int *s_li = s_li_all[wave];
 
     // Run of a.tpw consecutive tiles: XCD x owns runs [x*tx, (x+1)*tx), taken
@@ -894,8 +896,8 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
         return;
 
     const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(T));
-    const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rhead = make_rsrc_full(a.head, a.ntiles * (long long)sizeof(A));
+    const __amdgpu_buffer_rsrc_t rtail = make_rsrc_full(a.tail, a.ntiles * (long long)sizeof(A));
     int err = 0;
 
     uint32_t kb, ke;
@@ -955,9 +957,9 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
 #pragma unroll
             for (int k = 0; k < VPT; ++k) {
                 const int vec = lane + k * kWave;
-                T p[4];
+                A p[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) p[j] = vt[k][j] * xv[k][j];
+                for (int j = 0; j < 4; ++j) p[j] = A(vt[k][j]) * A(xv[k][j]);
                 store4(s_prod + 4 * vec, p);
             }
             __builtin_amdgcn_wave_barrier();
@@ -967,12 +969,12 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             // (YL) or are kept in registers until the products are consumed.
             const int jo = d.lo_row - (d.f - 1);  // block index of local row 0
             int tag[YL ? 1 : Q];
-            T sq[YL ? 1 : Q];
+            A sq[YL ? 1 : Q];
             int nl = 0;
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
                 const int i = lane + q * kWave;
-                if (!YL) { tag[q] = -1; sq[q] = T(0); }
+                if (!YL) { tag[q] = -1; sq[q] = A(0); }
                 if (q * kWave < d.nr) {
                     bool lng = false;
                     int a0 = 0, a1 = 0;
@@ -980,7 +982,7 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
                         a0 = max(s_rpb[jo + i], d.A) - base;
                         a1 = min(s_rpb[jo + i + 1], d.B) - base;
                         if (a1 - a0 <= kThreadMax) {
-                            T s = T(0);
+                            A s = A(0);
 #pragma unroll 4
                             for (int p = a0; p < a1; ++p)
                                 s += s_prod[p];
@@ -1007,7 +1009,7 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             // Pass 2: one listed row at a time, all 64 lanes, DPP sum.
             nl = min(nl, LCAP);
             for (int j = 0; j < nl; ++j) {
-                T s = T(0);
+                A s = A(0);
                 const int e1 = s_lb[j];
                 for (int p = s_la[j] + lane; p < e1; p += kWave)
                     s += s_prod[p];
@@ -1034,25 +1036,33 @@ __global__ __launch_bounds__(kWaveWG) __attribute__((amdgpu_waves_per_eu(WPE, 8)
             const int nw = d.nr - d.head - d.tail; // rows written to y
             const __amdgpu_buffer_rsrc_t ryt =
                 make_rsrc(a.y + (d.lo_row + r0), (long long)nw * (long long)sizeof(T));
-            constexpr int P = 16 / (int)sizeof(T);
+            if constexpr (__is_same(T, half_t)) {
+                // fp16: one 2-byte store per row (the range check drops whole dwords, so a 16-byte
+                // store ending in a half-covered dword would lose the last row)
+                for (int j = lane; j < nw; j += kWave)
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, T(s_y[r0 + j])), ryt,
+                                                          j * 2, 0, kStoreAux);
+            } else {
+                constexpr int P = 16 / (int)sizeof(T);
 #pragma unroll
-            for (int q = 0; q < S::kQS; ++q) {
-                // Slot 0 always issues; later slots only when the tile has the
-                // rows (wave-uniform branch), so most tiles issue one store.
-                if (q == 0 || q * kWave * P < nw) {
-                    const int j = (q * kWave + lane) * P;
-                    T w[P];
+                for (int q = 0; q < S::kQS; ++q) {
+                    // Slot 0 always issues; later slots only when the tile has the
+                    // rows (wave-uniform branch), so most tiles issue one store.
+                    if (q == 0 || q * kWave * P < nw) {
+                        const int j = (q * kWave + lane) * P;
+                        T w[P];
 #pragma unroll
-                    for (int p = 0; p < P; ++p) w[p] = T(0);
-                    if (j < nw) {
+                        for (int p = 0; p < P; ++p) w[p] = T(0);
+                        if (j < nw) {
 #pragma unroll
-                        for (int p = 0; p < P; ++p) w[p] = s_y[r0 + j + p < K + 1 ? r0 + j + p : 0];
+                            for (int p = 0; p < P; ++p) w[p] = T(s_y[r0 + j + p < K + 1 ? r0 + j + p : 0]);
+                        }
+                        buf_store16(ryt, j < nw ? (uint32_t)j * (uint32_t)sizeof(T) : kOob, w);
                     }
-                    buf_store16(ryt, j < nw ? (uint32_t)j * (uint32_t)sizeof(T) : kOob, w);
                 }
             }
             // Partials of split rows (rare; owner[] is built once per pattern).
-            const uint32_t tslot = (uint32_t)t * (uint32_t)sizeof(T);
+            const uint32_t tslot = (uint32_t)t * (uint32_t)sizeof(A);
             if (d.head) buf_store(rhead, lane == 0 ? tslot : kOob, s_y[0]);
             if (d.tail) buf_store(rtail, lane == 0 ? tslot : kOob, s_y[d.nr > 0 ? d.nr - 1 : 0]);
             __builtin_amdgcn_wave_barrier();
@@ -3139,26 +3149,40 @@ __device__ __forceinline__ T group_tree32(T v)
 }
 
 // One tile of the reference algorithm: products in LDS, rows [start, end).
+// Products and sums in acc_t<T> (fp32 in the fp16 mode).
 template <typename T, int TT>
 struct PfTile {
-    const T *s;
+    using A = acc_t<T>;
+    const A *s;
     const int *__restrict__ rp;
     T *__restrict__ y;
     int first, start, end;
+    A *__restrict__ head;  // fp16: the partial of row start, of row end - 1 (tail), slot `tile`
+    A *__restrict__ tail;
+    long long tile;
 
     __device__ __forceinline__ void range(int r, int &lo, int &hi) const
     {
         lo = max(0, rp[r] - first);
         hi = min(TT, rp[r + 1] - first);
     }
-    // Tile-boundary rows are shared with a neighbouring tile: atomicAdd;
-    // interior rows are stored (preFreeSpMV.cu:92-96, :139-146).
-    __device__ __forceinline__ void put(int r, T v) const
+    // A tile-boundary row's partial sum: atomicAdd to y (preFreeSpMV.cu:92-96,
+    // :139-146); fp16 keeps it in fp32 for k_prefree_join, which adds a row's
+    // partials in tile order and rounds to half once.
+    __device__ __forceinline__ void shared(int r, A v) const
+    {
+        if constexpr (__is_same(T, half_t))
+            (r == start ? head : tail)[tile] = v;
+        else
+            atomic_add(y + r, v);
+    }
+    // Interior rows are stored.
+    __device__ __forceinline__ void put(int r, A v) const
     {
         if (r == start || r == end - 1)
-            atomic_add(y + r, v);
+            shared(r, v);
         else
-            y[r] = v;
+            y[r] = T(v);
     }
 };
 
@@ -3169,7 +3193,7 @@ __device__ __forceinline__ void pf_red_thread(const PfTile<T, TT> &t)
     for (int r = t.start + (int)threadIdx.x; r < t.end; r += kPfBS) {
         int lo, hi;
         t.range(r, lo, hi);
-        T sum = T(0);
+        acc_t<T> sum = 0;
         for (int i = lo; i < hi; ++i)
             sum += t.s[i];
         t.put(r, sum);
@@ -3179,12 +3203,12 @@ __device__ __forceinline__ void pf_red_thread(const PfTile<T, TT> &t)
 // red_row_block (:30-69): strided lane sums, a 32-lane tree per half wave,
 // then the four half-wave results summed in order by thread 0.
 template <typename T, int TT>
-__device__ __forceinline__ void pf_red_block(const PfTile<T, TT> &t, T *s_warp)
+__device__ __forceinline__ void pf_red_block(const PfTile<T, TT> &t, acc_t<T> *s_warp)
 {
     const int tid = threadIdx.x;
     int lo, hi;
     t.range(t.start, lo, hi);
-    T v = T(0);
+    acc_t<T> v = 0;
     for (int j = lo + tid; j < hi; j += kPfBS)
         v += t.s[j];
     v = half_wave_tree(v);
@@ -3192,11 +3216,11 @@ __device__ __forceinline__ void pf_red_block(const PfTile<T, TT> &t, T *s_warp)
         s_warp[tid >> 5] = v;
     __syncthreads();
     if (tid == 0) {
-        T fin = T(0);
+        acc_t<T> fin = 0;
 #pragma unroll
         for (int w = 0; w < kPfBS / 32; ++w)
             fin += s_warp[w];
-        atomic_add(t.y + t.start, fin);
+        t.shared(t.start, fin);
     }
 }
 
@@ -3209,7 +3233,7 @@ __device__ __forceinline__ void pf_red_vector(const PfTile<T, TT> &t)
     for (int r = t.start + g; r < t.end; r += kPfBS / VS) {
         int lo, hi;
         t.range(r, lo, hi);
-        T v = T(0);
+        acc_t<T> v = 0;
         for (int i = lo + q; i < hi; i += VS)
             v += t.s[i];
         v = group_tree32<VS>(v);
@@ -3250,8 +3274,10 @@ __device__ __forceinline__ bool pf_imbalanced(const PfTile<T, TT> &t, int *s_fla
 // 96..127 sum the other rows one each, left to right.  Rows whose sum is 0.0
 // are not written (:326; y is zeroed before the launch).
 template <typename T, int TT>
-__device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_final, T *s_warp, int *s_li)
+__device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, acc_t<T> *s_final, acc_t<T> *s_warp,
+                                                  int *s_li)
 {
+    using A = acc_t<T>;
     constexpr int kLong = 96;
     const int tid = threadIdx.x;
     const int n = t.end - t.start;
@@ -3259,7 +3285,7 @@ __device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_f
         int len = -1;
         if (tid < n) {
             len = t.rp[t.start + tid + 1] - t.rp[t.start + tid];
-            s_final[tid] = T(0);
+            s_final[tid] = A(0);
         }
         int ml = len, mi = tid;
 #pragma unroll
@@ -3275,7 +3301,7 @@ __device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_f
     if (tid < kLong) {
         int lo, hi;
         t.range(t.start + li, lo, hi);
-        T v = T(0);
+        A v = A(0);
         for (int j = lo + tid; j < hi; j += kLong)
             v += t.s[j];
         v = half_wave_tree(v);
@@ -3287,8 +3313,8 @@ __device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_f
                 continue;
             int lo, hi;
             t.range(t.start + i, lo, hi);
-            const T *sp = t.s + lo;
-            T sum = T(0);
+            const A *sp = t.s + lo;
+            A sum = A(0);
             switch (hi - lo) {  // left to right, as the unrolled cases of :293-313
             case 0: break;
             case 1: sum = sp[0]; break;
@@ -3305,15 +3331,15 @@ __device__ __forceinline__ void pf_red_long_short(const PfTile<T, TT> &t, T *s_f
     }
     __syncthreads();
     if (tid < 32) {
-        T v = tid < kLong / 32 ? s_warp[tid] : T(0);
+        A v = tid < kLong / 32 ? s_warp[tid] : A(0);
         v = half_wave_tree(v);
         if (tid == 0)
             s_final[li] = v;
     }
     __syncthreads();
     if (tid < n) {
-        const T fs = s_final[tid];
-        if (fs != T(0))
+        const A fs = s_final[tid];
+        if (fs != A(0))
             t.put(t.start + tid, fs);
     }
 }
@@ -3339,12 +3365,14 @@ __device__ __forceinline__ int pf_vector_size(int n)
 template <typename T, int P, int CODE>
 __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
 {
+    using A = acc_t<T>;
     constexpr int TT = kPfBS * P;  // 512 nnz for P = 4 (preFreeSpMV.cu:587), 1024 for P = 8
     constexpr int VPT = P / 4;     // 4-nnz vectors per lane
-    __shared__ __attribute__((aligned(16))) T s_prod[TT];
+    constexpr bool F16 = __is_same(T, half_t);
+    __shared__ __attribute__((aligned(16))) A s_prod[TT];
     __shared__ int s_rows[2];
-    __shared__ T s_warp[kPfBS / 32];
-    __shared__ T s_final[32];
+    __shared__ A s_warp[kPfBS / 32];
+    __shared__ A s_final[32];
     __shared__ int s_flag, s_li;
 
     const int tid = threadIdx.x;
@@ -3354,6 +3382,10 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
     if (b >= a.ntiles)
         return;
     const int m = a.m;
+    if (F16 && tid == 0) {  // a boundary row this tile leaves unwritten adds zero (ordered by the barrier below)
+        a.head[b] = A(0);
+        a.tail[b] = A(0);
+    }
 
     // First row of this tile and of the next one (the pre-pass map, :3-28).
     const uint32_t first = (uint32_t)(b * TT);
@@ -3373,7 +3405,7 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
     // through a range-checked resource; positions past nnz give zero products.
     const int tile_nnz = min(TT, a.nnz - (int)first);
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + first, (long long)tile_nnz * 4);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + first, (long long)tile_nnz * (long long)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + first, val_range_bytes<T>(tile_nnz));
     const __amdgpu_buffer_rsrc_t rx = make_rsrc_full(a.x, (long long)a.n * (long long)sizeof(T));
     int c[VPT][4];
     T v[VPT][4];
@@ -3383,11 +3415,11 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int off = 4 * (tid + k * kPfBS);
-        T p[4];
+        A p[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            p[j] = v[k][j] * buf_load(rx, off + j < tile_nnz ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
-                                      (T *)nullptr);
+            p[j] = A(v[k][j]) * A(buf_load(rx, off + j < tile_nnz ? (uint32_t)c[k][j] * (uint32_t)sizeof(T) : kOob,
+                                           (T *)nullptr));
         store4(s_prod + off, p);
     }
     __syncthreads();
@@ -3398,7 +3430,11 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
     if (a.rp[end] % TT != 0 || end == start)
         end = min(end + 1, m);
     const int nrows = end - start;
-    const PfTile<T, TT> t{s_prod, a.rp, a.y, (int)first, start, end};
+    const PfTile<T, TT> t{s_prod, a.rp, a.y, (int)first, start, end, a.head, a.tail, b};
+    if (F16 && tid == 0) {  // the row range, for k_prefree_join
+        a.owner[2 * b] = start;
+        a.owner[2 * b + 1] = end;
+    }
 
     if constexpr (CODE == 1) {
         pf_red_thread(t);
@@ -3429,6 +3465,49 @@ __global__ __launch_bounds__(kPfBS) void k_prefree(Args<T> a)
             default: pf_red_vector<2>(t); break;
             }
         }
+    }
+}
+
+// fp16: the tile-boundary rows of k_prefree<half_t>.  One wave per tile b; a
+// row shared by tiles b, b+1, ... (its partials in their head or tail slots) is
+// summed by the wave of the first of them, 64 tiles per round (a DPP tree per
+// round, the rounds in tile order), in fp32, and stored to y rounded to half
+// once.  ranges[b] = (start, end) of tile b's rows.
+__global__ __launch_bounds__(kBS) void k_prefree_join(const int *__restrict__ ranges, const float *__restrict__ head,
+                                                      const float *__restrict__ tail, long long ntiles,
+                                                      half_t *__restrict__ y)
+{
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long b = (long long)blockIdx.x * (kBS / kWave) + threadIdx.x / kWave;
+    if (b >= ntiles)
+        return;  // whole wave
+    const int s0 = ranges[2 * b], e0 = ranges[2 * b + 1];
+    const int sp = b > 0 ? ranges[2 * b - 2] : -1, ep = b > 0 ? ranges[2 * b - 1] : -1;
+    if (e0 <= s0)
+        return;
+    for (int which = 0; which < 2; ++which) {
+        const int r = which == 0 ? s0 : e0 - 1;
+        if (which == 1 && r == s0)
+            break;  // a single row: one partial
+        if (b > 0 && ep > sp && (r == sp || r == ep - 1))
+            continue;  // an earlier tile's wave sums it
+        float acc = 0.f;
+        for (long long t0 = b; t0 < ntiles; t0 += kWave) {
+            const long long t = t0 + lane;
+            bool mem = false;
+            float v = 0.f;
+            if (t < ntiles) {
+                const int st = ranges[2 * t], et = ranges[2 * t + 1];
+                mem = et > st && (r == st || r == et - 1);
+                if (mem) v = r == st ? head[t] : tail[t];
+            }
+            const uint64_t mm = __ballot(mem);
+            const int run = mm == ~0ull ? kWave : __ffsll((long long)~mm) - 1;  // the tiles sharing r from t0 on
+            acc += wave_sum(lane < run ? v : 0.f);
+            if (run < kWave)
+                break;
+        }
+        if (lane == 0) y[r] = (half_t)acc;
     }
 }
 
@@ -3753,6 +3832,12 @@ __global__ __launch_bounds__(kBS) void k_fill_zero(uint32_t *__restrict__ p, siz
         p[i] = 0u;
 }
 
+__global__ __launch_bounds__(kBS) void k_fill_zero16(unsigned short *__restrict__ p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * kBS + threadIdx.x; i < n; i += (size_t)gridDim.x * kBS)
+        p[i] = 0;
+}
+
 // ---- scratch of the no-allocation entry point --------------------------------
 //
 // pf_spmv_noalloc takes its row statistics and plan workspace from this array
@@ -3850,12 +3935,6 @@ Args<T> make_args(const pfk_spmv_args *a)
     r.y2 = static_cast<T *>(a->half_part);
     r.ovf_cap = a->ovf_cap;
     return r;
-}
-
-int unsupported_f16(const char *variant)
-{
-    snprintf(g_err, sizeof g_err, "%s has no fp16 kernel (fp16 runs on FLAT tiles of 1024 or 2048 nnz)", variant);
-    return PF_ERR_UNSUPPORTED;
 }
 
 // A workspace buffer of `have` bytes where `need` are touched.
@@ -4105,6 +4184,12 @@ int launch_prefree(const pfk_spmv_args *a, void *stream)
     default: return PF_ERR_INVALID;
     }
     PFK_LAUNCHED("k_prefree");
+    if constexpr (__is_same(T, half_t)) {
+        hipLaunchKernelGGL(k_prefree_join, dim3((unsigned)((a->ntiles + 3) / 4)), dim3(kBS), 0, S(stream),
+                           static_cast<const int *>(a->owner_row), static_cast<const float *>(a->head_slot),
+                           static_cast<const float *>(a->tail_slot), a->ntiles, static_cast<half_t *>(a->y));
+        PFK_LAUNCHED("k_prefree_join");
+    }
     return PF_OK;
 }
 
@@ -4225,11 +4310,11 @@ extern "C" {
 
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream)
 {
-    if (dtype == PF_F16) return unsupported_f16("ADAPTIVE");
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
     if (!args_ok(a, true) || !ws_ok(dtype, a, true)) return PF_ERR_INVALID;
     return dtype == PF_F64 ? dispatch_adaptive<double>(a, stream)
-         : dtype == PF_F32 ? dispatch_adaptive<float>(a, stream) : PF_ERR_INVALID;
+         : dtype == PF_F32 ? dispatch_adaptive<float>(a, stream)
+         : dtype == PF_F16 ? dispatch_adaptive<half_t>(a, stream) : PF_ERR_INVALID;
 }
 
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
@@ -4375,9 +4460,10 @@ int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *str
         Args<float> r = make_args<float>(a);
         if (merged_keys) hipLaunchKernelGGL((k_fixup<float, true>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
         else hipLaunchKernelGGL((k_fixup<float, false>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
-    } else if (dtype == PF_F16 && !merged_keys) {
+    } else if (dtype == PF_F16) {
         Args<half_t> r = make_args<half_t>(a);
-        hipLaunchKernelGGL((k_fixup<half_t, false>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
+        if (merged_keys) hipLaunchKernelGGL((k_fixup<half_t, true>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
+        else hipLaunchKernelGGL((k_fixup<half_t, false>), dim3(grid), dim3(kBS), 0, S(stream), r, a->tile);
     } else {
         return PF_ERR_INVALID;
     }
@@ -4387,19 +4473,31 @@ int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *str
 
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream)
 {
-    if (dtype == PF_F16) return unsupported_f16("PREFREE");
-    if (dtype != PF_F64 && dtype != PF_F32) return PF_ERR_INVALID;  // before y is sized from it
+    if (dtype != PF_F64 && dtype != PF_F32 && dtype != PF_F16) return PF_ERR_INVALID;  // before y is sized from it
     if (a && a->m == 0 && a->nnz == 0) return PF_OK;
-    if (!args_ok(a, false)) return PF_ERR_INVALID;
+    if (!args_ok(a, dtype == PF_F16)) return PF_ERR_INVALID;
+    // fp16: fp32 partials of the tile-boundary rows (head, tail) and each tile's row range (owner_row, 2 ints)
+    if (dtype == PF_F16 && !(room(a->head_slot, a->head_bytes, a->ntiles * 4, "head slots") &&
+                             room(a->tail_slot, a->tail_bytes, a->ntiles * 4, "tail slots") &&
+                             room(a->owner_row, a->owner_bytes, a->ntiles * 8, "row ranges")))
+        return PF_ERR_INVALID;
     if (a->ladder < 0 || a->ladder > 5) {
         snprintf(g_err, sizeof g_err, "reduction ladder %d: the reference has codes 1..5", a->ladder);
         return PF_ERR_INVALID;
     }
     if (a->tile != 512 && a->tile != 1024) return PF_ERR_UNSUPPORTED;
-    const size_t ybytes = (size_t)a->m * (dtype == PF_F64 ? 8 : 4);
-    int st = pfk_fill_zero(a->y, ybytes, stream);  // the reference memsets y, preFreeSpMV.cu:644
+    // the reference memsets y, preFreeSpMV.cu:644
+    int st = PF_OK;
+    if (dtype == PF_F16) {
+        hipLaunchKernelGGL(k_fill_zero16, dim3(grid_for(a->m, kBS, 8192)), dim3(kBS), 0, S(stream),
+                           static_cast<unsigned short *>(a->y), (size_t)a->m);
+        PFK_LAUNCHED("k_fill_zero16");
+    } else {
+        st = pfk_fill_zero(a->y, (size_t)a->m * (dtype == PF_F64 ? 8 : 4), stream);
+    }
     if (st != PF_OK || a->nnz == 0) return st;
     if (dtype == PF_F64) return a->tile == 512 ? launch_prefree<double, 4>(a, stream) : launch_prefree<double, 8>(a, stream);
+    if (dtype == PF_F16) return a->tile == 512 ? launch_prefree<half_t, 4>(a, stream) : launch_prefree<half_t, 8>(a, stream);
     return a->tile == 512 ? launch_prefree<float, 4>(a, stream) : launch_prefree<float, 8>(a, stream);
 }
 
@@ -4413,9 +4511,9 @@ int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap)
     static const int pf_tiles[] = {512, 1024};   // k_prefree: 128 x P_NNZ
     const int *src;
     int n;
-    if (variant == PF_PREFREE && dtype != PF_F16) { src = pf_tiles; n = 2; }
+    if (variant == PF_PREFREE) { src = pf_tiles; n = 2; }
     else if (variant == PF_ADAPTIVE && dtype == PF_F64) { src = ad64; n = 4; }
-    else if (variant == PF_ADAPTIVE && dtype == PF_F32) { src = ad32; n = 3; }
+    else if (variant == PF_ADAPTIVE && (dtype == PF_F32 || dtype == PF_F16)) { src = ad32; n = 3; }  // fp16 as fp32
     else if (variant == PF_FLAT && dtype == PF_F64) { src = fl64; n = 4; }
     else if (variant == PF_FLAT && dtype == PF_F32) { src = fl32; n = 4; }
     else if (variant == PF_FLAT && dtype == PF_F16) { src = fl16; n = 2; }

@@ -426,6 +426,8 @@ int finish_info(const pf_row_stats &s, int dtype, int variant, int tile, pf_plan
         r.ntiles = nnz > 0 ? (nnz + tile - 1) / tile : 1;
         r.needs_fixup = 0;
         r.workspace_bytes = 256;
+        if (dtype == PF_F16)  // fp32 partials of each tile's boundary rows (head, tail) and its row range
+            r.workspace_bytes += (size_t)(2 * ((r.ntiles * 4 + 255) & ~255LL) + ((r.ntiles * 8 + 255) & ~255LL));
         r.ladder = 3;  // the reference's active ladder, preFreeSpMV.cu:466-483
     } else {
         return fail(PF_ERR_INVALID, "unknown variant");
@@ -547,6 +549,13 @@ void plan_carve_split(pf_plan *p, void *w0)
             p->row_map_bytes = map;
             p->sched_bytes = total - (owner_at + owners + map);
         }
+    } else if (info.dtype == PF_F16) {  // PREFREE fp16: boundary-row partials, then the tiles' row ranges
+        const size_t slots = ((size_t)info.ntiles * 4 + 255) & ~(size_t)255;
+        p->head = w + 256;
+        p->tail = w + 256 + slots;
+        p->owner = reinterpret_cast<int *>(w + 256 + 2 * slots);
+        p->head_bytes = p->tail_bytes = slots;
+        p->owner_bytes = total - (256 + 2 * slots);
     }
     p->split_ready = true;
 }

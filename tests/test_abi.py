@@ -219,19 +219,20 @@ def test_select_row_aligned_threshold():
         assert pf.select(make_stats(1000000, 20000000, 5), "f64", variant).row_aligned == 0
 
 
-def test_select_f16_is_flat_only():
-    """fp16 values: FLAT (2048 nnz per tile) for every matrix, row-aligned when rows fit; the other
-    variants have no fp16 kernels."""
+def test_select_f16_auto_is_flat():
+    """fp16 values: AUTO picks FLAT (2048 nnz per tile) for every matrix, row-aligned when rows fit;
+    ADAPTIVE (fp32's tiles) and PREFREE are there when asked for."""
     short = pf.select(make_stats(4194304, 20963328, 5), "f16", "auto")
     assert short.variant == pf.FLAT and short.tile == 2048 and short.row_aligned == 1 and short.needs_fixup == 0
     dense = pf.select(make_stats(1000000, 315647995, 499000), "f16", "auto")
     assert dense.variant == pf.FLAT and dense.tile == 2048 and dense.row_aligned == 0 and dense.needs_fixup == 1
     assert pf.supported_tiles("flat", "f16") == [1024, 2048]
-    assert pf.supported_tiles("adaptive", "f16") == [] and pf.supported_tiles("prefree", "f16") == []
-    for variant in ("adaptive", "prefree"):
-        with pytest.raises(pf.PrefreeError) as e:
-            pf.select(make_stats(1000, 5000, 5), "f16", variant)
-        assert e.value.status == 5
+    assert pf.supported_tiles("adaptive", "f16") == pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
+    assert pf.supported_tiles("prefree", "f16") == [512, 1024]
+    a = pf.select(make_stats(1000, 5000, 5), "f16", "adaptive")
+    assert a.variant == pf.ADAPTIVE and a.tile == 440
+    p = pf.select(make_stats(1000, 5000, 5), "f16", "prefree")
+    assert p.variant == pf.PREFREE and p.tile == 512 and p.ladder == 3
 
 
 def test_select_rejects_bad_arguments():

@@ -31,8 +31,6 @@ def plant(a, rng, frac):
 @pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
 @pytest.mark.parametrize("variant,row_aligned", [("auto", None), ("flat", 0), ("adaptive", None), ("prefree", None)])
 def test_special_values_match_oracle(variant, row_aligned, dtype):
-    if dtype == "f16" and variant in ("adaptive", "prefree"):
-        pytest.skip("fp16 runs on FLAT tiles only (the other entry points report PF_ERR_UNSUPPORTED)")
     checked = 0
     for name, rp, col, n in CASES:
         rng = np.random.default_rng(len(col) + 7)
