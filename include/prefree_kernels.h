@@ -176,6 +176,9 @@ int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *lis
 /* out[i] = col[idx[i]] for i < count (planning of long-row tiles: each tile's first column); every idx must lie
  * in [0, nnz). */
 int pfk_gather_cols(const int *col, long long nnz, const int *idx, int count, int *out, void *stream);
+/* Hybrid planning, no counterpart in the reference: flags[rows[i]] = 1 for each of `count` rows (rows outside
+ * [0, nflags) skipped); the other flags are left as they are (the caller zeroes them first). */
+int pfk_mark_rows(const int *rows, int count, unsigned char *flags, long long nflags, void *stream);
 
 /* Ints of an x-window schedule. */
 #define PFK_SCHED_INTS(ntiles, cap) (16 + 8 * (cap) + (ntiles))
@@ -223,7 +226,7 @@ int pfk_plan_scan(const int *row_ptr, const int *col, int m, int n, long long nn
  * PFK_BAND_SAMPLE-th block of 256 rows): out[i] = the sampled nnz whose column lies within +-(64 << i) of their
  * row (i < PFK_BAND_WIDTHS), out[PFK_BAND_WIDTHS] = the sampled nnz; PFK_BAND_WIDTHS + 1 unsigned long long,
  * zeroed by the call.  A thread per row: for matrices whose rows hold at most PFK_ALIGN_ROW_MAX nnz. */
-#define PFK_BAND_SAMPLE 8
+#define PFK_BAND_SAMPLE 16
 int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream);
 
 /* Tile descriptors of ADAPTIVE (merged=1) / FLAT (merged=0) for every tile:

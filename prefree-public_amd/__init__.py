@@ -418,7 +418,7 @@ def band_stats(row_ptr, col, m, out, stream=None):
 
 
 BAND_WIDTHS = 9   # PFK_BAND_WIDTHS
-BAND_SAMPLE = 8   # PFK_BAND_SAMPLE
+BAND_SAMPLE = 16  # PFK_BAND_SAMPLE
 
 
 def adaptive_long_row_min(dtype, tile) -> int:

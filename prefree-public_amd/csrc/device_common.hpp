@@ -87,6 +87,19 @@ __device__ __forceinline__ T group_sum(T v)
     return v;
 }
 
+// Reduction of a 32-bit value over all 64 lanes by an associative, commutative
+// op (sum, max, min); every lane receives the result.  Whole wave active.
+template <typename Op>
+__device__ __forceinline__ unsigned int wave_reduce_u32(unsigned int v, Op op)
+{
+    v = op(v, dpp<kDppXor1>(v));
+    v = op(v, dpp<kDppXor2>(v));
+    v = op(v, dpp<kDppHalfMirror>(v));
+    v = op(v, dpp<kDppMirror>(v));
+    v = op(v, (unsigned int)__builtin_amdgcn_ds_swizzle((int)v, swizzle_xor_pattern<16>()));
+    return op((unsigned int)__builtin_amdgcn_readlane((int)v, 0), (unsigned int)__builtin_amdgcn_readlane((int)v, 32));
+}
+
 // Key of row r: its first nnz index, plus r itself when tiles cut the merged
 // (row, nnz) sequence.  Strictly increasing in r for MERGE, non-decreasing otherwise.
 template <bool MERGE>

@@ -2313,35 +2313,52 @@ __global__ __launch_bounds__(kBandBS) void k_band(Args<T> a, BandArgs b)
 // A sample: the rows of every PFK_BAND_SAMPLE-th block of kBS rows, spread over
 // the whole matrix; out[PFK_BAND_WIDTHS] counts the sampled nnz.  The count
 // only chooses w (the band kernel gives the same sums for any w), so a sample
-// serves, at an eighth of the reads.
+// serves.  A workgroup per sampled block at a time: the block's row_ptr in
+// LDS, then a thread per nnz (coalesced col loads, its row found by bisection
+// in LDS), the counts reduced over the wave and the workgroup before a few
+// global atomics per workgroup (at most kBandStatsWg workgroups).
+constexpr int kBandStatsWg = 512;
+
 __global__ __launch_bounds__(kBS) void k_band_stats(const int *__restrict__ rp, const int *__restrict__ col, int m,
                                                     unsigned long long *__restrict__ out)
 {
-    __shared__ unsigned long long s_c[PFK_BAND_WIDTHS + 1];
+    __shared__ int s_rp[kBS + 1];
+    __shared__ unsigned int s_c[PFK_BAND_WIDTHS + 1];
     const int tid = threadIdx.x;
     if (tid <= PFK_BAND_WIDTHS) s_c[tid] = 0;
-    __syncthreads();
     unsigned int cnt[PFK_BAND_WIDTHS + 1];
 #pragma unroll
     for (int i = 0; i <= PFK_BAND_WIDTHS; ++i) cnt[i] = 0;
-    for (long long blk = (long long)blockIdx.x * PFK_BAND_SAMPLE; blk * kBS < m;
-         blk += (long long)gridDim.x * PFK_BAND_SAMPLE) {
-        const long long r = blk * kBS + tid;
-        if (r >= m)
-            continue;
-        const int a0 = rp[r], a1 = rp[r + 1];
-        cnt[PFK_BAND_WIDTHS] += (unsigned)max(a1 - a0, 0);
-        for (int j = a0; j < a1; ++j) {
-            const long long d = llabs((long long)col[j] - r);
+    const long long nblk = ((long long)m + kBS - 1) / kBS;
+    const long long nsamp = (nblk + PFK_BAND_SAMPLE - 1) / PFK_BAND_SAMPLE;
+    for (long long sb = blockIdx.x; sb < nsamp; sb += gridDim.x) {  // workgroup-uniform
+        const long long r0 = sb * PFK_BAND_SAMPLE * kBS;
+        const int nr = (int)min((long long)kBS, (long long)m - r0);
+        for (int i = tid; i <= nr; i += kBS) s_rp[i] = rp[r0 + i];  // row_ptr[r0, r0 + nr]
+        __syncthreads();
+        const int A = s_rp[0], B = s_rp[nr];
+        for (int j = A + tid; j < B; j += kBS) {
+            const int c = col[j];
+            int lo = 0, hi = nr;  // s_rp[lo] <= j < s_rp[hi]: lo ends as the row of nnz j
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_rp[mid] <= j) lo = mid; else hi = mid;
+            }
+            const long long d = llabs((long long)c - (r0 + lo));
+            cnt[PFK_BAND_WIDTHS] += 1u;
 #pragma unroll
             for (int i = 0; i < PFK_BAND_WIDTHS; ++i) cnt[i] += d <= (64ll << i) ? 1u : 0u;
         }
+        __syncthreads();  // s_rp is rewritten by the next block
     }
+    const auto add = [](unsigned int x, unsigned int y) { return x + y; };
 #pragma unroll
-    for (int i = 0; i <= PFK_BAND_WIDTHS; ++i)
-        if (cnt[i]) atomicAdd(&s_c[i], (unsigned long long)cnt[i]);
+    for (int i = 0; i <= PFK_BAND_WIDTHS; ++i) {
+        const unsigned int c = wave_reduce_u32(cnt[i], add);
+        if ((tid & (kWave - 1)) == 0 && c) atomicAdd(&s_c[i], c);
+    }
     __syncthreads();
-    if (tid <= PFK_BAND_WIDTHS && s_c[tid]) atomicAdd(out + tid, s_c[tid]);
+    if (tid <= PFK_BAND_WIDTHS && s_c[tid]) atomicAdd(out + tid, (unsigned long long)s_c[tid]);
 }
 
 // ---- k_dense: dense rows by x windows staged in LDS (hybrid plans) -----------
@@ -2800,6 +2817,16 @@ __global__ __launch_bounds__(kBS) void k_combine(Args<T> a, DenseArgs d, LongArg
 }
 
 // Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
+// flags[rows[i]] = 1 for every listed row inside the flags (planning).
+__global__ __launch_bounds__(kBS) void k_mark_rows(const int *__restrict__ rows, int count,
+                                                   unsigned char *__restrict__ flags, long long nflags)
+{
+    for (long long i = (long long)blockIdx.x * kBS + threadIdx.x; i < count; i += (long long)gridDim.x * kBS) {
+        const int r = rows[i];
+        if (r >= 0 && r < nflags) flags[r] = 1;
+    }
+}
+
 __global__ __launch_bounds__(kBS) void k_gather_cols(const int *__restrict__ col, long long nnz,
                                                      const int *__restrict__ idx, int count, int *__restrict__ out)
 {
@@ -3595,33 +3622,29 @@ __global__ void k_stats_init(unsigned long long *out)
 // Row statistics; with a list (the planning scan), every row over
 // PFK_ALIGN_ROW_MAX nnz is also appended to it as (row, first nnz, end, 0),
 // the first `cap` of them (out[kStLongListed] counts them all).
-constexpr int kStatsBS = 1024;  // k_row_stats: one workgroup of 16 waves per CU
-constexpr int kStatsRows = 8;   // rows per lane and pass: row_ptr[r0, r0 + 8] as two 16-byte loads and one 4-byte load
+constexpr int kStatsBS = 1024;  // k_row_stats: workgroups of 16 waves
+constexpr int kStatsRows = 8;   // rows per group: row_ptr[r0, r0 + 8] as two 16-byte loads and one 4-byte load
+constexpr int kStatsGroups = 1; // groups per lane and pass (4, with their loads in flight together: C4 56 -> 87 us)
 constexpr int kStatsBins = 8;   // histogram bins a lane counts in registers (rows of under 128 nnz)
 
-template <typename Op>
-__device__ __forceinline__ unsigned int wave_reduce_u32(unsigned int v, Op op)
-{
-    v = op(v, dpp<kDppXor1>(v));
-    v = op(v, dpp<kDppXor2>(v));
-    v = op(v, dpp<kDppHalfMirror>(v));
-    v = op(v, dpp<kDppMirror>(v));
-    v = op(v, (unsigned int)__builtin_amdgcn_ds_swizzle((int)v, swizzle_xor_pattern<16>()));
-    return op((unsigned int)__builtin_amdgcn_readlane((int)v, 0), (unsigned int)__builtin_amdgcn_readlane((int)v, 32));
-}
-
 // Each workgroup takes a contiguous range of rows; its lanes read row_ptr in
-// groups of kStatsRows rows.  Every statistic is reduced over the wave before
-// it meets LDS, and over the workgroup before it meets memory: a few global
-// atomics per workgroup, with one workgroup per CU.
+// groups of kStatsRows rows, kStatsGroups groups per pass (the workgroup's
+// passes are uniform, so it can synchronise inside them).  Every statistic is
+// reduced over the wave before it meets LDS, and over the workgroup before it
+// meets memory.  The long rows of a pass are listed with one global atomic per
+// workgroup pass (the list's counter is the one address every workgroup meets).
 __global__ __launch_bounds__(kStatsBS) void k_row_stats(const int *__restrict__ rp, int m,
                                                         unsigned long long *__restrict__ out,
                                                         int4 *__restrict__ list, int cap)
 {
+    constexpr int kWaves = kStatsBS / kWave;
     __shared__ unsigned int s_hist[33];
     __shared__ unsigned int s_max, s_min, s_empty, s_dec, s_over, s_short, s_dev, s_far;
+    __shared__ unsigned int s_wsum[kWaves];
+    __shared__ unsigned long long s_lbase;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
     if (tid < 33) s_hist[tid] = 0;
     if (tid == 0) {
         s_max = 0; s_min = 0xFFFFFFFFu; s_empty = 0; s_dec = 0; s_over = 0; s_short = 0; s_dev = 0; s_far = 0;
@@ -3644,45 +3667,91 @@ __global__ __launch_bounds__(kStatsBS) void k_row_stats(const int *__restrict__ 
     const double la = line ? (double)(q3 - q1) / ((double)p3 - (double)p1) : 0.0;
     const double lb = line ? (double)q1 - la * (double)p1 : 0.0;
     const long long per = (((long long)m + gridDim.x - 1) / gridDim.x + kStatsRows - 1) / kStatsRows * kStatsRows;
-    const long long rb = (long long)blockIdx.x * per;
+    const long long rb = min((long long)m, (long long)blockIdx.x * per);
     const long long re = min((long long)m, rb + per);
-    if (rb < re) {
-        // row_ptr[rb, re]: entries past it read zeros (only for rows past re, which are skipped)
-        const __amdgpu_buffer_rsrc_t rr = make_rsrc(rp + rb, (re - rb + 1) * 4);
-        const int ng = (int)((re - rb + kStatsRows - 1) / kStatsRows);
-        for (int g = tid; g < ng; g += kStatsBS) {
-            const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32, 0, kAuxNt);
-            const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32 + 16, 0, kAuxNt);
-            const int v8 = (int)__builtin_amdgcn_raw_buffer_load_b32(rr, g * 32 + 32, 0, 0);
-            const int e[kStatsRows + 1] = {(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w,
-                                           (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w, v8};
+    // row_ptr[rb, re]: entries past it read zeros (only for rows past re, which are skipped)
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(rp + rb, re > rb ? (re - rb + 1) * 4 : 0);
+    const int ng = (int)((re - rb + kStatsRows - 1) / kStatsRows);
+    for (int gb = 0; gb < ng; gb += kStatsGroups * kStatsBS) {  // the same passes for every thread
+        u32x4 v0[kStatsGroups], v1[kStatsGroups];
+        int v8[kStatsGroups];
+#pragma unroll
+        for (int q = 0; q < kStatsGroups; ++q) {  // groups past the range read zeros (and are skipped)
+            const int g = gb + tid + q * kStatsBS;
+            v0[q] = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32, 0, kAuxNt);
+            v1[q] = __builtin_amdgcn_raw_buffer_load_b128(rr, g * 32 + 16, 0, kAuxNt);
+            v8[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rr, g * 32 + 32, 0, 0);
+        }
+        unsigned int nlong = 0;  // this lane's rows over PFK_ALIGN_ROW_MAX in this pass
+#pragma unroll
+        for (int q = 0; q < kStatsGroups; ++q) {
+            const int g = gb + tid + q * kStatsBS;
+            const int e[kStatsRows + 1] = {(int)v0[q].x, (int)v0[q].y, (int)v0[q].z, (int)v0[q].w,
+                                           (int)v1[q].x, (int)v1[q].y, (int)v1[q].z, (int)v1[q].w, v8[q]};
+            const double rd0 = (double)(rb + (long long)g * kStatsRows);  // exact: rows are below 2^31
 #pragma unroll
             for (int i = 0; i < kStatsRows; ++i) {
                 const long long r = rb + (long long)g * kStatsRows + i;
-                if (r >= re)
-                    break;
-                if (total > 0) ldev = fmax(ldev, fabs((double)r - (double)e[i] * per_nnz));
-                lfar += !line || fabs((double)r - (la * (double)e[i] + lb)) > 28.0;
-                int len = e[i + 1] - e[i];
-                if (len < 0) { ++ldec; len = 0; }
-                const unsigned int u = (unsigned int)len;
-                lmax = max(lmax, u);
-                lmin = min(lmin, u);
-                lempty += (u == 0);
-                lover += (u > (unsigned)PFK_ALIGN_ROW_MAX);
-                if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
-                if (list && u > (unsigned)PFK_ALIGN_ROW_MAX) {  // rare: one atomic per long row
-                    const unsigned long long k = atomicAdd(out + kStLongListed, 1ull);
-                    if (k < (unsigned long long)cap) list[k] = make_int4((int)r, e[i], e[i] + (int)u, 0);
-                }
-                const int bin = u == 0 ? 0 : 32 - __clz(u);
-                if (bin < kStatsBins) {
+                if (r < re) {
+                    const double rd = rd0 + (double)i;
+                    if (total > 0) ldev = fmax(ldev, fabs(rd - (double)e[i] * per_nnz));
+                    lfar += !line || fabs(rd - (la * (double)e[i] + lb)) > 28.0;
+                    int len = e[i + 1] - e[i];
+                    if (len < 0) { ++ldec; len = 0; }
+                    const unsigned int u = (unsigned int)len;
+                    lmax = max(lmax, u);
+                    lmin = min(lmin, u);
+                    lempty += (u == 0);
+                    nlong += (u > (unsigned)PFK_ALIGN_ROW_MAX);
+                    if (u <= (unsigned)PFK_ALIGN_ROW_MAX) lshort = max(lshort, u);
+                    const int bin = u == 0 ? 0 : 32 - __clz(u);
+                    if (bin < kStatsBins) {
 #pragma unroll
-                    for (int k = 0; k < kStatsBins; ++k) hc[k] += bin == k ? 1u : 0u;
-                } else {
-                    atomicAdd(&s_hist[bin], 1u);  // rows of 128 nnz or more
+                        for (int k = 0; k < kStatsBins; ++k) hc[k] += bin == k ? 1u : 0u;
+                    } else {
+                        atomicAdd(&s_hist[bin], 1u);  // rows of 128 nnz or more
+                    }
                 }
             }
+        }
+        lover += nlong;
+        if (list && __syncthreads_or(nlong > 0)) {
+            // this pass's long rows: an exclusive scan of the lanes' counts over the workgroup, one global atomic
+            unsigned int incl = nlong;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const unsigned int t = (unsigned int)__shfl_up((int)incl, o);
+                incl += lane >= o ? t : 0u;
+            }
+            if (lane == kWave - 1) s_wsum[wave] = incl;
+            __syncthreads();
+            if (tid == 0) {
+                unsigned int run = 0;
+                for (int w = 0; w < kWaves; ++w) {
+                    const unsigned int c = s_wsum[w];
+                    s_wsum[w] = run;
+                    run += c;
+                }
+                s_lbase = atomicAdd(out + kStLongListed, (unsigned long long)run);
+            }
+            __syncthreads();
+            unsigned long long k = s_lbase + s_wsum[wave] + (incl - nlong);
+#pragma unroll
+            for (int q = 0; q < kStatsGroups; ++q) {
+                const int g = gb + tid + q * kStatsBS;
+                const int e[kStatsRows + 1] = {(int)v0[q].x, (int)v0[q].y, (int)v0[q].z, (int)v0[q].w,
+                                               (int)v1[q].x, (int)v1[q].y, (int)v1[q].z, (int)v1[q].w, v8[q]};
+#pragma unroll
+                for (int i = 0; i < kStatsRows; ++i) {
+                    const long long r = rb + (long long)g * kStatsRows + i;
+                    const int len = e[i + 1] - e[i];
+                    if (r < re && len > PFK_ALIGN_ROW_MAX) {
+                        if (k < (unsigned long long)cap) list[k] = make_int4((int)r, e[i], e[i + 1], 0);
+                        ++k;
+                    }
+                }
+            }
+            __syncthreads();  // s_wsum and s_lbase are read before the next pass writes them
         }
     }
     const auto add = [](unsigned int x, unsigned int y) { return x + y; };
@@ -3738,7 +3807,7 @@ __global__ __launch_bounds__(kStatsBS) void k_row_stats(const int *__restrict__ 
 // sorted columns), so planning reads col once.  A workgroup whose range meets
 // more listed rows than it holds, or a list that overflowed, sets
 // out[kStLongUnchecked] instead of counting.
-constexpr int kColRowsCap = 64;  // listed rows one workgroup's range may meet
+constexpr int kColRowsCap = 256;  // listed rows one workgroup's range may meet
 
 __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, long long nnz, int n,
                                                    unsigned long long *__restrict__ out, const int4 *__restrict__ list,
@@ -3746,6 +3815,7 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
 {
     __shared__ int s_nrows, s_over;
     __shared__ int2 s_rows[kColRowsCap];  // nnz ranges [first, end) of the listed rows this range meets
+    __shared__ int2 s_sorted[kColRowsCap];  // the same, by first nnz (disjoint ranges: distinct firsts)
     const int tid = threadIdx.x;
     const long long per = ((nnz + gridDim.x - 1) / gridDim.x + 1023) & ~1023ll;  // whole vectors per lane
     const long long j0 = (long long)blockIdx.x * per;
@@ -3768,6 +3838,14 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
         }
         __syncthreads();
         if (s_over && tid == 0) atomicOr(out + kStLongUnchecked, 1ull);
+        const int nr = s_over ? 0 : min(s_nrows, kColRowsCap);
+        for (int t = tid; t < nr; t += kBS) {  // rank sort: a descent then finds its row by bisection
+            const int2 me = s_rows[t];
+            int rank = 0;
+            for (int k = 0; k < nr; ++k) rank += s_rows[k].x < me.x ? 1 : 0;
+            s_sorted[rank] = me;
+        }
+        __syncthreads();
     }
     const int nrows = s_over ? 0 : min(s_nrows, kColRowsCap);
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(col + j0, (j1 - j0) * 4);
@@ -3775,16 +3853,22 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
     const __amdgpu_buffer_rsrc_t rn = make_rsrc(col + j0, min(nnz - j0, j1 - j0 + 1) * 4);
     unsigned int bad = 0, desc = 0;
     const int nvec = (int)((j1 - j0 + 3) / 4);
+    const int lane = tid & (kWave - 1);
     for (int v0 = tid; v0 < nvec; v0 += 4 * kBS) {
         u32x4 c[4];
         int nx[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int u = 0; u < 4; ++u)  // four loads in flight per lane; vectors past the range read zeros
             c[u] = __builtin_amdgcn_raw_buffer_load_b128(rc, (v0 + u * kBS) * 16, 0, kAuxNt);
-        if (nrows > 0) {  // workgroup-uniform: the entry after each vector, issued with the vectors
+        if (nrows > 0) {  // workgroup-uniform
+            // The entry after a lane's vector is the next lane's first (taken below with a lane shift)
+            // unless the lane is the wave's last or its vector ends the range: those read it here.
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                nx[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rn, (v0 + u * kBS) * 16 + 16, 0, 0);
+            for (int u = 0; u < 4; ++u) {
+                const long long je = j0 + 4ll * (v0 + u * kBS) + 4;
+                if (lane == kWave - 1 || je >= j1)
+                    nx[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rn, (v0 + u * kBS) * 16 + 16, 0, 0);
+            }
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -3793,14 +3877,21 @@ __global__ __launch_bounds__(kBS) void k_col_check(const int *__restrict__ col, 
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 bad += (jb + i < j1 && (e[i] < 0 || e[i] >= n)) ? 1u : 0u;
+            // lane + 1 holds vector v0 + u * kBS + 1, and is active whenever jb + 4 < j1 (that vector is in range)
+            const int next = nrows > 0 ? __shfl_down(e[0], 1) : 0;
             if (nrows > 0 && jb < j1) {  // descents inside listed rows (rare: sorted rows have none)
-                const int f[5] = {e[0], e[1], e[2], e[3], nx[u]};
+                const int nxu = (lane == kWave - 1 || jb + 4 >= j1) ? nx[u] : next;
+                const int f[5] = {e[0], e[1], e[2], e[3], nxu};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const long long j = jb + i;
                     if (j + 1 < nnz && j + 1 <= j1 && j < j1 && f[i] > f[i + 1]) {
-                        for (int k = 0; k < nrows; ++k)
-                            desc += (s_rows[k].x <= j && j + 1 < s_rows[k].y) ? 1u : 0u;
+                        int lo = 0, hi = nrows;  // the last listed row starting at or before j
+                        while (hi - lo > 1) {
+                            const int mid = (lo + hi) >> 1;
+                            if ((long long)s_sorted[mid].x <= j) lo = mid; else hi = mid;
+                        }
+                        desc += (s_sorted[lo].x <= j && j + 1 < s_sorted[lo].y) ? 1u : 0u;
                     }
                 }
             }
@@ -4288,7 +4379,7 @@ int launch_stats(const int *row_ptr, const int *col, int m, int n, long long nnz
     PFK_LAUNCHED("k_stats_init");
     if (m > 0) {
         // a workgroup per CU (fewer for small m), each row range within a buffer resource's reach
-        const long long rows_wg = (long long)kStatsBS * kStatsRows;
+        const long long rows_wg = (long long)kStatsBS * kStatsRows * kStatsGroups;  // rows of one pass
         long long grid = std::min<long long>(((long long)m + rows_wg - 1) / rows_wg, std::max(1, device_cus()));
         grid = std::max<long long>(grid, ((long long)m + (1ll << 26) - 1) >> 26);
         hipLaunchKernelGGL(k_row_stats, dim3((unsigned)grid), dim3(kStatsBS), 0, S(stream), row_ptr, m, d_out, list,
@@ -4385,6 +4476,16 @@ int pfk_dense_scan(const int *row_ptr, const int *col, int m, int dmin, int *lis
     hipLaunchKernelGGL(k_dense_sorted, dim3(64, (unsigned)std::min(cap, 4096)), dim3(kBS), 0, S(stream), col, list,
                        cap, counters);
     PFK_LAUNCHED("k_dense_sorted");
+    return PF_OK;
+}
+
+int pfk_mark_rows(const int *rows, int count, unsigned char *flags, long long nflags, void *stream)
+{
+    if (!rows || !flags || count < 0 || nflags < 0) return PF_ERR_INVALID;
+    if (count == 0) return PF_OK;
+    hipLaunchKernelGGL(k_mark_rows, dim3(grid_for(count, kBS, 1024)), dim3(kBS), 0, S(stream), rows, count, flags,
+                       nflags);
+    PFK_LAUNCHED("k_mark_rows");
     return PF_OK;
 }
 
@@ -4545,8 +4646,8 @@ int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long
     PFK_LAUNCHED("k_fill_zero");
     if (m > 0) {
         const long long blocks = (m + kBS - 1) / kBS;
-        hipLaunchKernelGGL(k_band_stats, dim3(grid_for(blocks, PFK_BAND_SAMPLE, 4096)), dim3(kBS), 0, S(stream),
-                           row_ptr, col, m, out);
+        hipLaunchKernelGGL(k_band_stats, dim3(grid_for(blocks, PFK_BAND_SAMPLE, kBandStatsWg)), dim3(kBS), 0,
+                           S(stream), row_ptr, col, m, out);
         PFK_LAUNCHED("k_band_stats");
     }
     return PF_OK;

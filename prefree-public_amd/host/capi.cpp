@@ -653,6 +653,8 @@ struct PlanScan {
     const int *list = nullptr;  // int4 (row, first nnz, end, 0) per long row, in no particular order
     long long cap = 0, listed = 0, desc = 0;
     bool checked = false;
+    std::vector<int> host;  // the first host_n entries of the list, copied with the statistics
+    long long host_n = 0;
     bool complete() const { return list && listed <= cap && checked; }
 };
 
@@ -701,10 +703,15 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     int st = PF_OK;
     if (scan && scan->complete() && scan->listed == cap) {
         // the planning scan listed every long row and counted the descents inside them: no second pass over col
-        std::vector<int> l4((size_t)(4 * cap));
-        st = pfk_memcpy_d2h(l4.data(), scan->list, l4.size() * sizeof(int), stream);
-        if (st == PF_OK) st = pfk_stream_sync(stream);
-        if (st != PF_OK) return from_kernel_layer(st, "long-row list");
+        std::vector<int> l4;
+        if (cap <= scan->host_n) {  // copied with the statistics
+            l4.assign(scan->host.begin(), scan->host.begin() + 4 * cap);
+        } else {
+            l4.resize((size_t)(4 * cap));
+            st = pfk_memcpy_d2h(l4.data(), scan->list, l4.size() * sizeof(int), stream);
+            if (st == PF_OK) st = pfk_stream_sync(stream);
+            if (st != PF_OK) return from_kernel_layer(st, "long-row list");
+        }
         for (long long k = 0; k < cap; ++k)
             for (int j = 0; j < 3; ++j) list[(size_t)(3 * k + j)] = l4[(size_t)(4 * k + j)];
         cnt[0] = (int)cap;
@@ -791,11 +798,26 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
                  b_part = dense ? up((size_t)nd * nwin * slot_bytes(dtype)) : up((size_t)nlt * slot_bytes(dtype)),
                  b_lt = up((size_t)nlt * 16), b_deal = up((size_t)nlt * 4), b_rt = lng ? up(((size_t)nd + 1) * 4) : 0,
                  b_half = up((size_t)p->m * value_bytes(dtype)), b_apart = up((size_t)p->m);
+    // a plan built without a workspace (a hybrid candidate) keeps its error flag at the head of the tables
+    const size_t b_err = p->err ? 0 : 256;
+    for (int i = 1; i < nd; ++i)  // ascending: a row listed twice would sit next to itself
+        if (rows[(size_t)i] == rows[(size_t)i - 1])
+            return fail(PF_ERR_KERNEL, "hybrid plan: the planning scan listed a row twice");
     void *w = nullptr;
-    PF_TRY(pfk_malloc(&w, b_rows + b_runs + b_map + b_seg + b_part + b_lt + b_deal + b_rt + b_half + b_apart),
+    PF_TRY(pfk_malloc(&w, b_err + b_half + b_apart + b_rows + b_runs + b_map + b_seg + b_part + b_lt + b_deal + b_rt),
            "hybrid tables");
     char *c = static_cast<char *>(w);
     p->ws_hyb = w;
+    // zeroed together below: the error flag, the second-half sums, the apart flags
+    if (b_err) p->err = reinterpret_cast<int *>(c);
+    c += b_err;
+    p->half_part = c;
+    p->half_part_bytes = b_half;
+    c += b_half;
+    p->row_apart = reinterpret_cast<unsigned char *>(c);
+    p->row_apart_bytes = b_apart;
+    c += b_apart;
+    // dense_rows and runs adjacent: one copy
     p->dense_rows = reinterpret_cast<int *>(c);
     c += b_rows;
     p->runs = reinterpret_cast<int *>(c);
@@ -812,11 +834,6 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     c += b_deal;
     p->long_row_tiles = lng ? reinterpret_cast<int *>(c) : nullptr;
     c += b_rt;
-    p->half_part = c;
-    p->half_part_bytes = b_half;
-    c += b_half;
-    p->row_apart = reinterpret_cast<unsigned char *>(c);
-    p->row_apart_bytes = b_apart;
     p->runs_bytes = b_runs;
     p->run_map_bytes = b_map;
     p->dense_seg_bytes = b_seg;
@@ -839,21 +856,14 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     // XCD's 4 MB L2 but a half of it nearly fits (x up to 24 MB).
     p->x_halves = xb > kXcdL2Bytes && xb <= 6 * kXcdL2Bytes;
     p->info.x_halves = p->x_halves ? 1 : 0;
-    st = pfk_memcpy_h2d(p->dense_rows, rows.data(), (size_t)nd * 4, stream);
-    // rows the runs never write (the long rows) keep a zero second-half sum
-    if (st == PF_OK) st = pfk_fill_zero(p->half_part, b_half, stream);
-    // exactly one byte set per row summed apart, 0 for every other row (the combine relies on it)
-    std::vector<unsigned char> apart((size_t)p->m, 0);
-    long long marked = 0;
-    for (long long i = 0; i < nd; ++i) {
-        unsigned char &b = apart[(size_t)rows[(size_t)i]];
-        marked += b == 0 ? 1 : 0;
-        b = 1;
-    }
-    if (st == PF_OK && marked != nd)
-        return fail(PF_ERR_KERNEL, "hybrid plan: the planning scan listed a row twice");
-    if (st == PF_OK && p->m > 0) st = pfk_memcpy_h2d(p->row_apart, apart.data(), apart.size(), stream);
-    if (st == PF_OK) st = pfk_memcpy_h2d(p->runs, runs.data(), (size_t)5 * R * 4, stream);
+    // the error flag clear; rows the runs never write (the long rows) keep a zero second-half sum; exactly one
+    // byte set per row summed apart, 0 for every other row (the combine relies on it: the rows are distinct)
+    st = pfk_fill_zero(w, b_err + b_half + b_apart, stream);
+    std::vector<int> stage((b_rows + b_runs) / 4, 0);  // alive until the stream is synchronised below
+    std::copy(rows.begin(), rows.end(), stage.begin());
+    std::copy(runs.begin(), runs.end(), stage.begin() + b_rows / 4);
+    if (st == PF_OK) st = pfk_memcpy_h2d(p->dense_rows, stage.data(), b_rows + b_runs, stream);
+    if (st == PF_OK) st = pfk_mark_rows(p->dense_rows, nd, p->row_apart, p->m, stream);
     if (st == PF_OK && timer) timer->start(stream);
     if (st == PF_OK && lng) {
         // deal: the tiles ordered by their first column, XCD k taking the k-th eighth
@@ -950,34 +960,33 @@ int plan_build(const pf_row_stats &s, const int *d_row_ptr, int m, int n, int nn
     p->nnz = nnz;
     p->info = info;
     p->stats = s;
-    // A hybrid candidate starts with the error flag alone: a hybrid plan runs without the split-row arrays
-    // (C5: their 7 MB took 0.3 ms to allocate), which come later if pf_plan_set_hybrid(plan, 0) asks.
+    // A hybrid candidate starts with no workspace: a hybrid plan keeps its error flag with its own tables and
+    // runs without the split-row arrays (C5: 7 MB, 0.3 ms to allocate), which come later if
+    // pf_plan_set_hybrid(plan, 0) asks.
     const bool candidate = want_hybrid && hybrid_candidate(s, n, dtype, info, d_col);
-    void *w = nullptr;
-    int rc = pfk_malloc(&w, candidate ? 256 : info.workspace_bytes);
-    if (rc != PF_OK) {
-        delete p;
-        return from_kernel_layer(rc, "plan workspace");
-    }
+    int rc = PF_OK;
     if (candidate) {
-        p->ws = w;
-        p->err = static_cast<int *>(w);
         p->split_ready = false;
     } else {
+        void *w = nullptr;
+        rc = pfk_malloc(&w, info.workspace_bytes);
+        if (rc != PF_OK) {
+            delete p;
+            return from_kernel_layer(rc, "plan workspace");
+        }
         plan_carve(p, w);
+        if (timer) timer->start(stream);
+        rc = plan_init(p, d_row_ptr, stream);
+        if (rc == PF_OK) rc = pfk_stream_sync(stream);
+        if (rc == PF_OK && timer) timer->stop(stream);
     }
-    if (timer) timer->start(stream);
-    rc = candidate ? pfk_fill_zero(p->err, 256, stream) : plan_init(p, d_row_ptr, stream);
-    if (rc == PF_OK) rc = pfk_stream_sync(stream);
-    if (rc == PF_OK && timer) timer->stop(stream);
     if (rc == PF_OK && d_col && !candidate) rc = try_band(p, d_row_ptr, d_col, stream, timer);
     if (rc == PF_OK && candidate) {
         rc = try_hybrid(p, d_row_ptr, d_col, stream, scan, timer);
-        if (rc == PF_OK && !p->hybrid) {  // stays split-row: its arrays now
+        if (rc == PF_OK && !p->hybrid) {  // stays split-row: its workspace now
             void *full = nullptr;
             rc = pfk_malloc(&full, info.workspace_bytes);
             if (rc == PF_OK) {
-                pfk_free(p->ws);
                 plan_carve(p, full);
                 rc = plan_init(p, d_row_ptr, stream);
                 if (rc == PF_OK) rc = pfk_stream_sync(stream);
@@ -1066,7 +1075,8 @@ int check_csr_stats(const pf_row_stats &s, int nnz)
 
 // Long rows the planning scan lists; a matrix with more of them scans again
 // when it tries the hybrid path.
-constexpr int kScanListCap = 4096;
+constexpr int kScanListCap = 8192;
+constexpr int kScanHostList = 1024;  // list entries copied back with the statistics (one copy, one wait)
 
 // Bytes of pf_spmv_noalloc's scratch taken by the row statistics block; the
 // workspace starts after it, 256-byte aligned.
@@ -1153,21 +1163,26 @@ int pf_plan_create_tuned(pf_plan **plan, const int *d_row_ptr, const int *d_col,
         unsigned long long h[PFK_STATS_WORDS];
         auto *d = static_cast<unsigned long long *>(buf);
         int *list = reinterpret_cast<int *>(static_cast<char *>(buf) + stats_b);
+        std::vector<unsigned long long> hb((stats_b + (size_t)kScanHostList * 16) / 8);
         timer.start(stream);
         st = pfk_plan_scan(d_row_ptr, d_col, m, n, nnz, d, list, kScanListCap, stream);
-        if (st == PF_OK) st = pfk_memcpy_d2h(h, d, sizeof h, stream);
+        if (st == PF_OK) st = pfk_memcpy_d2h(hb.data(), d, hb.size() * 8, stream);
         if (st == PF_OK) st = pfk_stream_sync(stream);
         if (st == PF_OK) timer.stop(stream);
         if (st != PF_OK) {
             pfk_free(buf);
             return from_kernel_layer(st, "planning scan");
         }
+        std::memcpy(h, hb.data(), sizeof h);
         decode_stats(h, d_col, m, nnz, &s);
         scan.list = list;
         scan.cap = kScanListCap;
         scan.listed = (long long)h[46];
         scan.desc = (long long)h[47];
         scan.checked = h[48] == 0;
+        scan.host_n = std::min<long long>(scan.listed, kScanHostList);
+        const int *hl = reinterpret_cast<const int *>(reinterpret_cast<const char *>(hb.data()) + stats_b);
+        scan.host.assign(hl, hl + 4 * scan.host_n);
     } else if (m > 0) {
         st = pf_row_stats_compute(d_row_ptr, d_col, m, n, nnz, &s, stream);
         if (st != PF_OK) return st;
@@ -1364,7 +1379,7 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
     // no row of a row-aligned tile is longer than this (longer rows take other plans), so the tile kernel can
     // load a tile's overflow with its nominal range
     a.ovf_cap = plan->info.row_aligned ? (int)std::min<long long>(PFK_ALIGN_ROW_MAX, plan->stats.max_row_len) : 0;
-    a.band_w = plan->info.band_w;  // used once the row map is recorded
+    a.band_w = a.row_map ? plan->info.band_w : 0;  // used once the row map is recorded; never without one
     const int dt = plan->info.dtype;
     if (plan->hybrid) {
         a.ntiles = plan->run_tiles;

@@ -118,6 +118,29 @@ def test_band_default_rule():
     torch.cuda.synchronize()
 
 
+def test_band_plan_searching_every_call():
+    """A band plan told to search its rows on every call (pf_plan_set_remember_rows(plan, 0)) has no row map:
+    its calls run the tiles' kernel, with the band plan's y; switching back records the map again."""
+    name, rp, col, n = CASES[0]
+    m = len(rp) - 1
+    val, x = oracle.initvec(len(col)), oracle.initvec(n)
+    d_rp, d_col, d_val, d_x = dev(rp), dev(col), dev(val), dev(x)
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device="cuda:0")
+    outs = []
+    with pf.Plan(d_rp, d_col, m, n, len(col), "f64", "auto") as p:
+        assert p.info.band_w > 0
+        for remember in (True, False, False, True, True):
+            p.set_remember_rows(remember)
+            y.fill_(float("nan"))
+            p.execute(d_rp, d_col, d_val, d_x, y)
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+        p.check()
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    assert_parity(rp, col, val, x, outs[0], "f64", exact=True, what=name)
+
+
 def test_band_refused_without_band():
     rp, col, _ = pf.synth_csr(2, seed=3, scale_n=300, dtypes=())  # x of 720 KB: no band
     with pf.Plan(dev(rp), dev(col), len(rp) - 1, len(rp) - 1, len(col), "f64", "auto") as p:

@@ -7,7 +7,7 @@ long rows (over 256 nnz) and the column descents inside them.  Checked here:
 * a single descent inside a dense row refuses the hybrid path wherever it falls, also across the
   boundary between two workgroups' ranges of col; a descent between two rows, or inside a short row, does
   not;
-* more long rows than the scan lists (4096) fall back to a scan of their own and decide the same way;
+* more long rows than the scan lists (8192) fall back to a scan of their own and decide the same way;
 * a single column out of range is refused wherever it falls;
 * plan timing: the wall time covers the GPU time, both positive.
 """
@@ -123,24 +123,29 @@ def test_descents_between_rows_or_in_short_rows_keep_hybrid():
 
 
 def test_more_long_rows_than_the_scan_lists():
-    """4200 dense rows (over the scan's list of 4096): the plan scans again and decides as before."""
+    """8300 dense rows (over the scan's list of 8192): the plan scans again and decides as before."""
     rng = np.random.default_rng(6)
-    n = 20000
-    lengths = []
-    for _ in range(4200):
-        lengths += [4100] + [int(v) for v in rng.integers(0, 8, size=2)]
-    rp, col = csr_from_lengths(lengths, n, rng)
+    n, nd, dl = 20000, 8300, 4100
+    short = rng.integers(0, 8, size=(nd, 2))
+    lengths = np.stack([np.full(nd, dl), short[:, 0], short[:, 1]], axis=1).ravel()
+    rp = np.zeros(len(lengths) + 1, dtype=np.int64)
+    np.cumsum(lengths, out=rp[1:])
+    key = np.repeat(np.arange(len(lengths), dtype=np.int64) * n, lengths) + rng.integers(0, n, size=int(rp[-1]))
+    col = (np.sort(key) % n).astype(np.int32)  # sorted within each row (repeats allowed)
+    rp = rp.astype(np.int32)
     info = _plan_info(rp, col, n)
-    assert info["hybrid"] == 1 and info["dense_rows"] == 4200, info
+    assert info["hybrid"] == 1 and info["dense_rows"] == nd, info
     r = int(np.flatnonzero(np.diff(rp) > 256)[-1])
     j = int(rp[r]) + 100
     c = col.copy()
+    while c[j] == c[j + 1]:
+        j += 1
     c[j], c[j + 1] = c[j + 1], c[j]
     assert c[j] > c[j + 1]
     assert _plan_info(rp, c, n)["hybrid"] == 0
     val, x = oracle.initvec(len(col)), oracle.initvec(n)
     y, _ = gpu_spmv(rp, col, val, x, "flat")
-    assert_parity(rp, col, val, x, y, "f64", exact=True, what="4200 dense rows")
+    assert_parity(rp, col, val, x, y, "f64", exact=True, what="8300 dense rows")
 
 
 @pytest.mark.parametrize("where", ["first", "last", "chunk_edge", "middle"])
