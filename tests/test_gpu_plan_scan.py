@@ -82,7 +82,8 @@ def test_sorted_dense_rows_go_hybrid():
     assert _plan_info(rp, col, n)["hybrid"] == 1
 
 
-@pytest.mark.parametrize("where", ["middle", "first_pair", "last_pair", "chunk_edge", "chunk_edge_next"])
+@pytest.mark.parametrize("where", ["middle", "first_pair", "last_pair", "chunk_edge", "chunk_edge_next",
+                                   "wave_edge", "lane_block_edge"])
 def test_one_descent_in_a_dense_row_refuses_hybrid(where):
     rp, col, n = _dense_matrix()
     lens = np.diff(rp)
@@ -96,6 +97,16 @@ def test_one_descent_in_a_dense_row_refuses_hybrid(where):
         j = a
     elif where == "last_pair":
         j = b - 2
+    elif where in ("wave_edge", "lane_block_edge"):
+        # k_col_check: lane i of a wave holds 4 consecutive nnz of its range, so the pair (j, j + 1) with
+        # j + 1 a multiple of 256 past the range's start crosses from a wave's last lane to the next wave
+        # (taken by a load, not from the neighbouring lane); 1024 crosses into the next block of vectors
+        step = 256 if where == "wave_edge" else 1024
+        k0 = (a // ch) * ch  # start of the range holding the row's first nnz
+        j = k0 + step - 1
+        while j < a + 1:
+            j += step
+        assert j + 1 < b
     else:  # the pair (j, j + 1) straddles two workgroups' ranges, or starts the next range
         k = -(-a // ch) * ch
         while k < a + 2:
