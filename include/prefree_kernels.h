@@ -225,7 +225,7 @@ int pfk_plan_scan(const int *row_ptr, const int *col, int m, int n, long long nn
 /* Planning statistic of the band kernel, no counterpart in the reference, over a sample of the rows (every
  * PFK_BAND_SAMPLE-th block of 256 rows): out[i] = the sampled nnz whose column lies within +-(64 << i) of their
  * row (i < PFK_BAND_WIDTHS), out[PFK_BAND_WIDTHS] = the sampled nnz; PFK_BAND_WIDTHS + 1 unsigned long long,
- * zeroed by the call.  A thread per row: for matrices whose rows hold at most PFK_ALIGN_ROW_MAX nnz. */
+ * zeroed by the call.  A thread per nnz of each sampled block, its row found by bisection of the block's row_ptr. */
 #define PFK_BAND_SAMPLE 16
 int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream);
 
