@@ -40,8 +40,8 @@ enum pf_status {
 
 /* ---- value types ----------------------------------------------------------- */
 /* PF_F16: val, x and y hold IEEE binary16 values (2 bytes each); products and row sums are formed in
- * fp32 and each row sum is rounded to half once.  Every variant: FLAT (tiles 1024, 2048; no hybrid or band
- * path), ADAPTIVE (its fp32 tiles), PREFREE (its tile-boundary rows' fp32 partials added in tile order by a
+ * fp32 and each row sum is rounded to half once.  Every variant: FLAT (tiles 1024, 2048; hybrid plans in
+ * dense mode without x halves; no band path), ADAPTIVE (its fp32 tiles), PREFREE (its tile-boundary rows' fp32 partials added in tile order by a
  * second kernel, where the reference adds half values with atomics). */
 enum pf_dtype { PF_F64 = 0, PF_F32 = 1, PF_F16 = 2 };
 

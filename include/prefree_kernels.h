@@ -145,7 +145,7 @@ typedef struct pfk_spmv_args {
 /* Bytes of one split-row partial (head / tail slot): fp32 in the fp16 mode. */
 #define PFK_SLOT_BYTES(dtype) ((dtype) == 0 ? 8 : 4)
 
-/* Columns per x window of a hybrid plan's dense-row kernel, at most (64 KB of LDS). */
+/* Columns per x window of a hybrid plan's dense-row kernel, at most (64 KB of LDS fp64/fp32, 32 KB fp16). */
 #define PFK_DENSE_WINDOW(dtype) ((dtype) == 0 ? 8192 : 16384)
 
 /* x windows of a dense-mode hybrid plan: the fewest of at most PFK_DENSE_WINDOW(dtype) columns, rounded up to a
@@ -164,7 +164,7 @@ static inline int pfk_dense_width(long long n, int n_win)
     return (int)((c + 63) / 64 * 64);
 }
 
-/* y = A x for a hybrid plan (PF_F64 / PF_F32): the runs' row-aligned tiles, the dense rows' window sums (or, in
+/* y = A x for a hybrid plan (PF_F64 / PF_F32, and PF_F16 with 2048-nnz run tiles and no x halves): the runs' row-aligned tiles, the dense rows' window sums (or, in
  * long mode, the long-row tiles) and their combine, three or four launches.  map_ready 0: the call searches rows and segment bounds (and records them
  * when run_map / dense_seg are given); 1: it reads them. */
 int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream);

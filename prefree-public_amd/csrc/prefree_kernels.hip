@@ -2388,10 +2388,13 @@ __global__ __launch_bounds__(kBS) void k_band_stats(const int *__restrict__ rp, 
 #endif
 template <typename T>
 struct DenseShape {
-    static constexpr int kW = sizeof(T) == 8 ? 8192 : 16384;  // x window: 64 KB of LDS
-    static constexpr int kG = PF_DENSE_G;                     // dense rows per workgroup
-    static constexpr int kU = PF_DENSE_U;                     // loads in flight per lane
-    static_assert(kW == PFK_DENSE_WINDOW(sizeof(T) == 8 ? PF_F64 : PF_F32), "window of the C ABI");
+    // x window: 64 KB of LDS, at most 16384 columns (fp16 windows of 32768 columns halve the workgroups: one per
+    // CU on C5, 640 us for k_dense against 470 for fp32)
+    static constexpr int kW = sizeof(T) == 8 ? 8192 : 16384;
+    static constexpr int kG = PF_DENSE_G;              // dense rows per workgroup
+    static constexpr int kU = PF_DENSE_U;              // loads in flight per lane
+    static_assert(kW == PFK_DENSE_WINDOW(sizeof(T) == 8 ? PF_F64 : sizeof(T) == 4 ? PF_F32 : PF_F16),
+                  "window of the C ABI");
 };
 
 struct DenseArgs {
@@ -2417,38 +2420,49 @@ __device__ __forceinline__ void dense_rows_stream(const Args<T> &a, const DenseA
                                                   int i0, int nk, int ms, int me)
 {
     using P = acc_t<T>;
-    constexpr int W = DenseShape<T>::kW, U = DenseShape<T>::kU;
+    // fp16: 4 consecutive nnz per lane and load (16-byte col, 8-byte val loads); a 2-byte val load per lane
+    // would cover one line per wave (C5 fp16 670 us against 503 for split-row tiles)
+    constexpr int V = sizeof(T) == 2 ? 4 : 1;
+    constexpr int W = DenseShape<T>::kW, U = DenseShape<T>::kU / V;
+    constexpr int B = kWave * U * V;  // nnz per batch
     const int lane = threadIdx.x & (kWave - 1);
     if (lane < nk && me == ms) static_cast<P *>(d.part)[(long long)(i0 + kWaves * lane) * d.nwin + w] = P(0);
     const uint64_t todo = __ballot(lane < nk && me > ms);
-    int cA[U], cB[U];
-    T vA[U], vB[U];
+    int cA[U][V], cB[U][V];
+    T vA[U][V], vB[U][V];
     P acc = P(0);
     // Batches start at the segment's first nnz rounded down to a multiple of 64,
     // so every 64-lane load covers whole 128-byte lines of col and val (a
     // segment starts anywhere; unaligned, a load touched one line more); the
     // lanes before the segment's start read the row's earlier nnz and add nothing.
     const int ma = ms & ~(kWave - 1);
-    const auto issue = [&](int k, int j, int (&c)[U], T (&v)[U]) {
+    const auto issue = [&](int k, int j, int (&c)[U][V], T (&v)[U][V]) {
         const int s = __builtin_amdgcn_readlane(ma, k), e = __builtin_amdgcn_readlane(me, k);
         const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.col + s, (long long)(e - s) * 4);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, (long long)(e - s) * (long long)sizeof(T));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.val + s, val_range_bytes<T>(e - s));
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-            load1(rc, rv, j + u * kWave + lane, c[u], v[u]);
+        for (int u = 0; u < U; ++u) {
+            if constexpr (V == 1)
+                load1(rc, rv, j + u * kWave + lane, c[u][0], v[u][0]);
+            else
+                load4(rc, rv, j / 4 + u * kWave + lane, c[u], v[u]);
+        }
     };
-    const auto consume = [&](int k, int j, const int (&c)[U], const T (&v)[U]) {
+    const auto consume = [&](int k, int j, const int (&c)[U][V], const T (&v)[U][V]) {
         const int base = __builtin_amdgcn_readlane(ma, k);
         const int lead = __builtin_amdgcn_readlane(ms, k) - base;
         const int len = __builtin_amdgcn_readlane(me, k) - base;
 #pragma unroll
         for (int u = 0; u < U; ++u) {  // no product for slots outside the segment (x may hold inf or NaN)
-            const T xv = sx[(c[u] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
-            const int q = j + u * kWave + lane;
-            if (q >= lead && q < len)
-                acc += P(v[u]) * P(xv);
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const T xv = sx[(c[u][e] - c0) & (W - 1)];  // the mask keeps every LDS read inside the window
+                const int q = V == 1 ? j + u * kWave + lane : j + 4 * (u * kWave + lane) + e;
+                if (q >= lead && q < len)
+                    acc += P(v[u][e]) * P(xv);
+            }
         }
-        if (j + kWave * U >= len) {  // the row's last batch
+        if (j + B >= len) {  // the row's last batch
             acc = wave_sum(acc);
             if (lane == 0) static_cast<P *>(d.part)[(long long)(i0 + kWaves * k) * d.nwin + w] = acc;
             acc = P(0);
@@ -2456,7 +2470,7 @@ __device__ __forceinline__ void dense_rows_stream(const Args<T> &a, const DenseA
     };
     const auto advance = [&](int &k, int &j) {  // the batch after (k, j); false at the end
         const int len = __builtin_amdgcn_readlane(me, k) - __builtin_amdgcn_readlane(ma, k);
-        j += kWave * U;
+        j += B;
         if (j < len) return true;
         const uint64_t rest = todo & ~((2ull << k) - 1ull);
         if (!rest) return false;
@@ -2599,7 +2613,8 @@ __global__ __launch_bounds__(kBS) void k_dense(Args<T> a, DenseArgs d)
     const int i_end = min(d.nd, (g + 1) * d.gsz);
     {  // the window x[c0, c0 + win) into LDS, 16 bytes per lane and load; zeros past n
         const long long have = max(0LL, min((long long)d.win, (long long)a.n - c0));
-        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (have > 0 ? c0 : 0), have * (long long)sizeof(T));
+        // fp16: whole dwords (the range check drops a half-covered one; the extra entry is past n, never read)
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (have > 0 ? c0 : 0), val_range_bytes<T>((int)have));
         constexpr int kPer = 16 / (int)sizeof(T);
         const int nv = min(d.win, W) / kPer;
 #pragma unroll 4
@@ -2816,7 +2831,6 @@ __global__ __launch_bounds__(kBS) void k_combine(Args<T> a, DenseArgs d, LongArg
         dense_sum_row<T>(a, d, i, lane);
 }
 
-// Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
 // flags[rows[i]] = 1 for every listed row inside the flags (planning).
 __global__ __launch_bounds__(kBS) void k_mark_rows(const int *__restrict__ rows, int count,
                                                    unsigned char *__restrict__ flags, long long nflags)
@@ -2827,6 +2841,7 @@ __global__ __launch_bounds__(kBS) void k_mark_rows(const int *__restrict__ rows,
     }
 }
 
+// Planning of long-row tiles: out[i] = col[idx[i]] (-1 for an index outside [0, nnz)).
 __global__ __launch_bounds__(kBS) void k_gather_cols(const int *__restrict__ col, long long nnz,
                                                      const int *__restrict__ idx, int count, int *__restrict__ out)
 {
@@ -4427,8 +4442,9 @@ int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream)
 int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
 {
     if (!a) return PF_ERR_INVALID;
-    if (dtype != PF_F64 && dtype != PF_F32) {
-        snprintf(g_err, sizeof g_err, "hybrid plans are fp64 or fp32");
+    if (dtype != PF_F64 && dtype != PF_F32 && dtype != PF_F16) return PF_ERR_INVALID;
+    if (dtype == PF_F16 && (a->x_halves || a->tile != 2048)) {  // fp16: one rounding per row, so no halves
+        snprintf(g_err, sizeof g_err, "fp16 hybrid plans: 2048-nnz run tiles, no x halves");
         return PF_ERR_UNSUPPORTED;
     }
     if (a->m == 0 && a->nnz == 0) return PF_OK;
@@ -4464,6 +4480,7 @@ int pfk_spmv_hybrid(int dtype, const pfk_spmv_args *a, void *stream)
         (a->x_halves && !room(a->row_apart, a->row_apart_bytes, (long long)a->m, "rows summed apart")))
         return PF_ERR_INVALID;
     if (dtype == PF_F64) return a->tile == 1024 ? launch_hybrid<double, 1024>(a, stream) : launch_hybrid<double, 2048>(a, stream);
+    if (dtype == PF_F16) return launch_hybrid<half_t, 2048>(a, stream);
     return a->tile == 1024 ? launch_hybrid<float, 1024>(a, stream) : launch_hybrid<float, 2048>(a, stream);
 }
 

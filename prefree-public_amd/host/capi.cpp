@@ -677,7 +677,7 @@ struct PlanTimer {
 
 bool hybrid_candidate(const pf_row_stats &s, long long n, int dtype, const pf_plan_info &info, const int *d_col)
 {
-    if (!d_col || (dtype != PF_F64 && dtype != PF_F32) || info.variant != PF_FLAT || info.row_aligned ||
+    if (!d_col || (dtype != PF_F64 && dtype != PF_F32 && dtype != PF_F16) || info.variant != PF_FLAT || info.row_aligned ||
         !uses_row_map(info.variant, info.tile) || s.n_long_rows < 1)
         return false;
     const long long t = dense_min(n, dtype);
@@ -854,7 +854,8 @@ int try_hybrid(pf_plan *p, const int *d_row_ptr, const int *d_col, void *stream,
     p->run_chunk = short_nnz < 4 * short_rows ? 0 : kChunkNnz;
     // The runs' random x gathers fall in half of x per XCD when x exceeds one
     // XCD's 4 MB L2 but a half of it nearly fits (x up to 24 MB).
-    p->x_halves = xb > kXcdL2Bytes && xb <= 6 * kXcdL2Bytes;
+    // fp16 sums each row once in fp32 and rounds it once: the halves' two sums would be rounded apart
+    p->x_halves = dtype != PF_F16 && xb > kXcdL2Bytes && xb <= 6 * kXcdL2Bytes;
     p->info.x_halves = p->x_halves ? 1 : 0;
     // the error flag clear; rows the runs never write (the long rows) keep a zero second-half sum; exactly one
     // byte set per row summed apart, 0 for every other row (the combine relies on it: the rows are distinct)
@@ -1305,6 +1306,8 @@ int pf_plan_set_x_halves(pf_plan *plan, int x_halves)
 {
     if (!plan || (x_halves != 0 && x_halves != 1)) return fail(PF_ERR_INVALID, "x_halves must be 0 or 1");
     if (!plan->ws_hyb) return fail(PF_ERR_UNSUPPORTED, "x halves are for the runs of hybrid plans");
+    if (x_halves && plan->info.dtype == PF_F16)
+        return fail(PF_ERR_UNSUPPORTED, "fp16 rounds each row once: no x halves");
     plan->x_halves = x_halves != 0;
     plan->info.x_halves = x_halves;
     return PF_OK;

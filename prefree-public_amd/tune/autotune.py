@@ -205,8 +205,7 @@ def time_candidates(spec, dtype, cfg, thresholds):
     auto.update({"us": round(us, 3), "gbps": round(bytes_eff / (us * 1e3), 1)})
     print(json.dumps({"matrix": spec, "auto": auto}), flush=True)
     cands = candidates(pf, dtype, cfg.get("candidates", {}))
-    if dtype != "f16":
-        cands.append({"variant": "flat", "tile": 0, "run": 0, "keep": 0, "ladder": 0, "hybrid": 1})
+    cands.append({"variant": "flat", "tile": 0, "run": 0, "keep": 0, "ladder": 0, "hybrid": 1})
     exact = values == "initvec"
     out_rows = []
     for c in cands:
@@ -278,6 +277,8 @@ def choose(per_class, band=0.01, guard=0.005, counter_fn=None, max_counted=3):
                 continue   # AUTO's configuration differs within the class: no row, the built-in rules decide
             pick = autos.pop()
             why = "no candidate beat AUTO's plan on every matrix: AUTO's configuration"
+            if pick not in mean:  # AUTO's own timings (its configuration was not among the candidates)
+                mean[pick] = sum(m["bytes"] / (m["auto"]["us"] * 1e3) for m in mats) / len(mats)
         row = dict(zip(("variant", "tile", "run", "keep", "ladder", "hybrid"), pick))
         row.update({"mean_gbps": round(mean.get(pick, 0.0), 1), "fastest": dict(zip(
             ("variant", "tile", "run", "keep", "ladder", "hybrid"), fastest)), "why": why,

@@ -68,8 +68,11 @@ def gpu_spmv(rp, col, val, x, variant="auto", tile=0, dtype="f64", fill=float("n
 
 
 def kat_exact_possible(rp, dtype):
-    """initVec values are integers <= 14; row sums stay exact below 2^53 (f64) / 2^24 (f32; fp16 sums
-    are formed in fp32 and rounded once, so they match the rounded exact sum)."""
+    """initVec values are integers <= 14; row sums stay exact below 2^53 (f64) / 2^24 (f32).  fp16 sums are
+    formed in fp32 and rounded once: exact below 2^24, and any sum of 65520 or more (nonnegative terms, so
+    every partial sum too) gives infinity either way, so fp16 always matches the rounded exact sum."""
+    if dtype == "f16":
+        return True
     longest = int(np.max(np.diff(rp))) if len(rp) > 1 else 0
     return longest * 196 < (2 ** 53 if dtype == "f64" else 2 ** 24)
 

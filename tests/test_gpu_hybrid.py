@@ -4,7 +4,8 @@ PF_AUTO makes a split-row FLAT plan hybrid when every row longer than 256 nnz
 is dense (at least the plan's threshold, 4096 nnz or more) and those rows'
 columns are sorted.  Checked through the C ABI against the CPU oracle:
 known-answer values bit for bit, U[-1,1] values within 1e-12 (f64) / 1e-5
-(f32) per row normalised by sum |a_ij x_j|, the first call (which searches rows
+(f32) / the fp16 bound per row normalised by sum |a_ij x_j| (fp16: dense mode,
+no x halves, each row rounded once), the first call (which searches rows
 and window bounds and records them) and later calls (which read them)
 bit-identical, the split-row path of the same plan within tolerance, and
 edge shapes: dense first and last rows, adjacent dense rows, empty rows and
@@ -52,7 +53,7 @@ def _case(name, n=60000, seed=3):
     return rp, col, n
 
 
-@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
 @pytest.mark.parametrize("name", sorted(SHAPES))
 def test_hybrid_shapes(name, dtype):
     rp, col, n = _case(name)
@@ -60,6 +61,8 @@ def test_hybrid_shapes(name, dtype):
     kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(n, NP[dtype])
     y, info = gpu_spmv(rp, col, kv, kx, "flat", dtype=dtype)
     assert info["hybrid"] == 1 and info["dense_rows"] == int(np.sum(np.diff(rp) > 256)), info
+    assert info["x_halves"] == 0 or dtype != "f16"  # fp16 rounds each row once: no halves
+    # fp16: the dense rows' KAT sums overflow binary16; the once-rounded model gives the same infinities
     assert_parity(rp, col, kv, kx, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"{name}/kat")
     val = rng.uniform(-1, 1, len(col)).astype(NP[dtype])
     x = rng.uniform(-1, 1, n).astype(NP[dtype])
@@ -67,7 +70,7 @@ def test_hybrid_shapes(name, dtype):
     assert_parity(rp, col, val, x, y, dtype, what=f"{name}/random")
 
 
-@pytest.mark.parametrize("dtype", ["f64", "f32"])
+@pytest.mark.parametrize("dtype", ["f64", "f32", "f16"])
 def test_hybrid_scaled_c5(dtype):
     rp, col, v = pf.synth_csr(5, seed=9, scale_n=200000, dtypes=(dtype,))
     x = pf.synth_x(5, len(rp) - 1, seed=9, dtypes=(dtype,))[dtype]
@@ -77,6 +80,16 @@ def test_hybrid_scaled_c5(dtype):
     kv, kx = oracle.initvec(len(col), NP[dtype]), oracle.initvec(len(x), NP[dtype])
     ky, _ = gpu_spmv(rp, col, kv, kx, "auto", dtype=dtype)
     assert_parity(rp, col, kv, kx, ky, dtype, exact=kat_exact_possible(rp, dtype), what="C5/200000/kat")
+
+
+def test_hybrid_f16_refuses_x_halves():
+    rp, col, n = _case("single_dense_middle")
+    with pf.Plan(dev(rp), dev(col), len(rp) - 1, n, len(col), "f16", "flat") as p:
+        assert p.info.hybrid == 1
+        with pytest.raises(pf.PrefreeError) as e:
+            p.set_x_halves(True)
+        assert e.value.status == 5
+    torch.cuda.synchronize()
 
 
 def test_hybrid_rectangular_and_duplicates():
