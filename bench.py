@@ -81,6 +81,8 @@ def kernel_name(info):
         return "k_prefree"
     if info["row_aligned"] and info.get("band_w"):
         return "k_band"
+    if info["tile"] <= 32:  # FLAT 2..32: row groups of that many lanes
+        return "k_vector"
     return {256: "k_flow", 4096: "k_tiles"}.get(info["tile"], "k_rows" if info["row_aligned"] else "k_flat")
 
 

@@ -186,6 +186,10 @@ int pfk_mark_rows(const int *rows, int count, unsigned char *flags, long long nf
 /* Longest row a row-aligned FLAT plan accepts. */
 #define PFK_ALIGN_ROW_MAX 256
 
+/* FLAT "tiles" 2, 4, 8, 16, 32: row groups, that many lanes per row and rows by index (k_vector: no tiles, no
+ * search, no workspace; for small matrices of short rows). */
+#define PFK_ROW_GROUP_TILE(t) ((t) == 2 || (t) == 4 || (t) == 8 || (t) == 16 || (t) == 32)
+
 int pfk_spmv_adaptive(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_flat(int dtype, const pfk_spmv_args *a, void *stream);
 int pfk_spmv_fixup(int dtype, int merged_keys, const pfk_spmv_args *a, void *stream);
@@ -197,7 +201,9 @@ int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream);
  * tile's first / last row), with each tile's row range in owner_row (2 ints per tile); a second kernel adds a
  * row's partials in tile order and stores it rounded to half once. */
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
-/* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count. */
+/* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count (at most
+ * PFK_MAX_TILES, which a buffer of that length always holds). */
+#define PFK_MAX_TILES 16
 int pfk_supported_tiles(int variant, int dtype, int *tiles, int cap);
 /* Long-row threshold the ADAPTIVE kernel uses for a tile size (-1 if unsupported). */
 int pfk_adaptive_long_row_min(int dtype, int tile);

@@ -426,8 +426,8 @@ def adaptive_long_row_min(dtype, tile) -> int:
 
 
 def supported_tiles(variant, dtype):
-    buf = (ctypes.c_int * 8)()
-    n = klib().pfk_supported_tiles(variant_code(variant), dtype_code(dtype), buf, 8)
+    buf = (ctypes.c_int * 16)()
+    n = min(16, klib().pfk_supported_tiles(variant_code(variant), dtype_code(dtype), buf, 16))
     return [buf[i] for i in range(n)]
 
 

@@ -156,9 +156,16 @@ int main(int argc, char **argv)
         std::printf("tiling: prefree, %d nnz per tile, %lld tiles\n", tile, nt);
     } else {
         const bool merged = variant == "adaptive";
-        int tiles[8];
-        const int ntl = pfk_supported_tiles(merged ? PF_ADAPTIVE : PF_FLAT, dtype, tiles, 8);
-        if (tile <= 0) tile = merged ? (ai.variant == PF_ADAPTIVE ? ai.tile : tiles[ntl - 1]) : tiles[ntl - 1];
+        int tiles[PFK_MAX_TILES];
+        const int ntl = pfk_supported_tiles(merged ? PF_ADAPTIVE : PF_FLAT, dtype, tiles, PFK_MAX_TILES);
+        int largest = 0;  // the largest nnz tile; FLAT's 2..32 are row groups, which have no nnz tiles
+        for (int i = 0; i < ntl; ++i)
+            if (!(!merged && PFK_ROW_GROUP_TILE(tiles[i]))) largest = std::max(largest, tiles[i]);
+        if (tile <= 0) tile = merged && ai.variant == PF_ADAPTIVE ? ai.tile : largest;
+        if (!merged && PFK_ROW_GROUP_TILE(tile)) {
+            std::fprintf(stderr, "pfstat: FLAT %d is a row group (%d lanes per row), not a tile of nnz\n", tile, tile);
+            return 2;
+        }
         const long long total = merged ? (long long)nnz + m : nnz;
         const long long nt = (total + tile - 1) / tile;
         check(pf_device_malloc((void **)&d_out, sizeof(int) * 8 * (size_t)nt), "device allocation");

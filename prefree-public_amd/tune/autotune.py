@@ -57,6 +57,7 @@ PKG_DIR = os.path.dirname(HERE)
 CLASSES = ("small", "medium", "large")
 ROW_CLASSES = ("short", "regular", "skewed", "dense")
 ALIGN_ROW_MAX = 256  # PFK_ALIGN_ROW_MAX, include/prefree_kernels.h
+ROW_GROUP_MAX = 32   # FLAT "tiles" 2..32 are row groups (PFK_ROW_GROUP_TILE)
 COPY_BYTES = 256 << 20
 
 
@@ -146,6 +147,9 @@ def make_plan(pf, d, m, n, nnz, dtype, c, stream):
             return None
         return p
     p = pf.Plan(d[0], d[1], m, n, nnz, dtype, c["variant"], c["tile"], stream=stream)
+    if c["variant"] == "flat" and c["tile"] <= ROW_GROUP_MAX and p.stats.max_row_len > ALIGN_ROW_MAX:
+        p.close()  # row groups (lanes per row) are for short rows: a dense row would take one group
+        return None
     if c["variant"] == "adaptive":
         p.set_run_tiles(c["run"])
         p.set_keep_cached(c["keep"])

@@ -167,10 +167,16 @@ def test_chunk_rule_and_grid():
 
 
 def test_select_auto_small_matrix():
-    """C1 shape (rows of 16): row-aligned FLAT.  With a row beyond 256 nnz, too few 512-key tiles
+    """C1 shape (rows of 16): FLAT row groups of 16 lanes per row (3/4 of the mean, rounded up to a power of
+    two); a larger matrix of short rows: row-aligned tiles.  With a row beyond 256 nnz, too few 512-key tiles
     for the device -> ADAPTIVE, 188-key tiles, one per run."""
     i = pf.select(make_stats(4096, 65536, 16), "f64", "auto")
-    assert i.variant == pf.FLAT and i.tile == 1024 and i.row_aligned == 1 and i.needs_fixup == 0
+    assert i.variant == pf.FLAT and i.tile == 16 and i.row_aligned == 1 and i.needs_fixup == 0
+    assert i.ntiles == 4096 * 16 // 256
+    for m, nnz, lanes in ((100000, 500000, 4), (1000, 1000, 2), (1000, 40000, 32), (10000, 70000, 8)):
+        assert pf.select(make_stats(m, nnz, 200), "f32", "auto").tile == lanes, (m, nnz)
+    i = pf.select(make_stats(1000000, 5000000, 20), "f64", "auto")  # over 2M nnz: tiles
+    assert i.variant == pf.FLAT and i.tile == 1024 and i.row_aligned == 1
     i = pf.select(make_stats(4096, 65536, 300), "f64", "auto")
     assert i.variant == pf.ADAPTIVE and i.tile == 188 and i.run_tiles == 1
     assert i.long_row_min == 64
@@ -226,7 +232,7 @@ def test_select_f16_auto_is_flat():
     assert short.variant == pf.FLAT and short.tile == 2048 and short.row_aligned == 1 and short.needs_fixup == 0
     dense = pf.select(make_stats(1000000, 315647995, 499000), "f16", "auto")
     assert dense.variant == pf.FLAT and dense.tile == 2048 and dense.row_aligned == 0 and dense.needs_fixup == 1
-    assert pf.supported_tiles("flat", "f16") == [1024, 2048]
+    assert pf.supported_tiles("flat", "f16") == [1024, 2048, 2, 4, 8, 16, 32]
     assert pf.supported_tiles("adaptive", "f16") == pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
     assert pf.supported_tiles("prefree", "f16") == [512, 1024]
     a = pf.select(make_stats(1000, 5000, 5), "f16", "adaptive")
@@ -244,8 +250,10 @@ def test_select_rejects_bad_arguments():
 def test_supported_tiles():
     assert pf.supported_tiles("adaptive", "f64") == [188, 238, 494, 512]
     assert pf.supported_tiles("adaptive", "f32") == [440, 494, 1024]
-    assert pf.supported_tiles("flat", "f64") == [256, 1024, 2048, 4096]
-    assert pf.supported_tiles("flat", "f32") == [256, 1024, 2048, 4096]
+    groups = [2, 4, 8, 16, 32]  # FLAT row groups: lanes per row
+    assert pf.supported_tiles("flat", "f64") == [256, 1024, 2048, 4096] + groups
+    assert pf.supported_tiles("flat", "f32") == [256, 1024, 2048, 4096] + groups
+    assert pf.supported_tiles("flat", "f16") == [1024, 2048] + groups
     assert pf.supported_tiles("prefree", "f64") == [512, 1024]
 
 

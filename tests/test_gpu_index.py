@@ -32,9 +32,10 @@ def cases():
 CASES = cases()
 
 
-# FLAT 256 (k_flow) finds rows by scanning forward, not by tile descriptors; parity tests cover it.
+# FLAT 256 (k_flow) finds rows by scanning forward and FLAT 2..32 (row groups) index rows directly, not by
+# tile descriptors; parity tests cover both.
 TILES = [(True, t) for t in pf.supported_tiles("adaptive", "f64")] + \
-        [(False, t) for t in pf.supported_tiles("flat", "f64") if t != 256]
+        [(False, t) for t in pf.supported_tiles("flat", "f64") if t > 256]
 
 
 @pytest.mark.parametrize("spread,run", [(0, 0), (1, 1), (64, 3), (1000, 8), (64, 64)])

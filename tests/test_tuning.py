@@ -184,7 +184,7 @@ def test_offline_tuner_score_time_then_counters_then_guard(table):
     assert (sel.variant, sel.tile, sel.ladder) == (pf.PREFREE, 512, 4)
     assert "small 5000000 short f64 auto 0 0 0 0 1" in text
     sel = pf.select(make_stats(10000, 20000, 3), "f64", "auto")            # small, short: not measured, the rules
-    assert (sel.variant, sel.tile) == (pf.FLAT, 2048)
+    assert (sel.variant, sel.tile) == (pf.FLAT, 2)                         # row groups of 2 lanes (2 nnz per row)
     sel = pf.select(make_stats(2000000, 15266620, 200000), "f64", "auto")  # medium, skewed
     assert (sel.variant, sel.tile) == (pf.FLAT, 1024)
 
