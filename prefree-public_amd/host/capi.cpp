@@ -50,7 +50,10 @@ constexpr int kFlowTile = 256;
 bool uses_row_map(int variant, int tile) { return variant == PF_FLAT && (tile == 1024 || tile == 2048); }
 
 constexpr long long kXcdL2Bytes = 4LL << 20;  // MI355X: 4 MB of L2 per XCD
-constexpr long long kRowGroupNnzMax = 1LL << 21;  // AUTO's row groups: matrices of at most 2M nnz
+// AUTO's row groups: at most 2^18 rows whose values and columns fit the 256 MB MALL
+constexpr long long kRowGroupRowsMax = 1LL << 18;
+constexpr long long kRowGroupBytesMax = 256LL << 20;
+constexpr long long kChipLanes = 256LL * 2048;  // lanes resident on the chip: 256 CUs x 32 waves x 64
 
 // Tiles per XCD list of an x-window schedule: an even share plus 2% slack.
 long long sched_cap(long long ntiles) { return (ntiles + kXcds - 1) / kXcds + ntiles / 400 + 1; }
@@ -283,7 +286,35 @@ bool table_choice(const pf_row_stats &s, int dtype, Choice &c)
     return false;
 }
 
+// Lanes per row of a row-group plan (powers of two, 2..32): never more than the longest row needs for
+// one pass; about half the mean row where the rows outnumber the chip's lanes (a lane's few loads in a row
+// keep more in flight than idle lanes do), else as many as still fit the chip's resident lanes, up to four
+// times the mean row or a quarter of the longest (more waves cost launch time where the rows are short).
+// Measured on MI355X, graph-timed, uniform random columns, us per SpMV (fp64): 2048 rows of 2 nnz: 8 lanes
+// 1.82 (2 lanes 2.19); 32768 x 2: 8 lanes 2.17 (16: 2.46); 131072 x 2: 4 lanes 3.27 (2: 3.65, 8: 3.80);
+// 131072 x 8: 4 lanes 7.37 (16: 7.50); 131072 x 32: 16 lanes 24.8 (32: 25.6, 8: 27.1); 262144 x 2:
+// 2 lanes 5.35 (4: 5.63).
+int row_group_lanes(const pf_row_stats &s)
+{
+    int lat = 2;
+    while (lat < 32 && lat < s.max_row_len) lat <<= 1;
+    const double mean = (double)s.nnz / (double)s.m;
+    int thr = 2;  // the power of two nearest half the mean row
+    while (thr < 32 && 0.5 * mean >= thr * 1.4142135623730951) thr <<= 1;
+    const double cap = std::max(4.0 * mean, s.max_row_len / 4.0);
+    int fill = 2;
+    while (fill < 32 && 2LL * fill * s.m <= kChipLanes && 2 * fill <= cap) fill <<= 1;
+    return std::min(lat, std::max(thr, fill));
+}
+
 // PF_AUTO: a tuning-table row if one matches; else
+//   * at most 2^18 rows, none longer than PFK_ALIGN_ROW_MAX, values and
+//     columns within 256 MB (MALL-resident across calls): FLAT row groups,
+//     row_group_lanes lanes per row (k_vector: no tiles, no workspace, one
+//     launch; fp64 C1 1.9 us per SpMV in a graph against 3.5 for 1024-nnz
+//     tiles; 131072 rows of 32 nnz 24.8 against 28.7; 262144 x 64 86 against
+//     99; 262144 x 128, 403 MB, 239 against 192 for 2048-nnz tiles; 393216 x
+//     8, 23.8 for 1024-nnz tiles against 24.3 for the best row groups);
 //   * no row longer than PFK_ALIGN_ROW_MAX, or fp16 values (FLAT only): FLAT
 //     (1024 nnz per tile for fp64, 2048 for fp32 / fp16 or for rows of under
 //     4 nnz on average), row-aligned when the rows fit: one launch per call;
@@ -304,14 +335,9 @@ Choice auto_choice(const pf_row_stats &s, int dtype)
     if (table_choice(s, dtype, c)) return c;
     const long long m = s.m, nnz = s.nnz;
     c.variant = PF_FLAT;
-    // A small matrix of short rows: row groups, a power of two of lanes per row near 3/4 of the mean row
-    // (C1, 16 nnz per row: 16 lanes, 1.9 us per SpMV in a graph against 3.5 for 1024-nnz tiles; they lose
-    // from about 4M nnz on: 5M nnz of 5 per row 61.6 against 59.4 us)
-    if (s.max_row_len <= PFK_ALIGN_ROW_MAX && nnz <= kRowGroupNnzMax && m > 0) {
-        const long long want = (3 * nnz + 4 * m - 1) / (4 * m);
-        int lanes = 2;
-        while (lanes < 32 && lanes < want) lanes <<= 1;
-        c.tile = lanes;
+    if (s.max_row_len <= PFK_ALIGN_ROW_MAX && m > 0 && m <= kRowGroupRowsMax &&
+        nnz * (value_bytes(dtype) + 4) <= kRowGroupBytesMax) {
+        c.tile = row_group_lanes(s);
         return c;
     }
     if (s.max_row_len <= PFK_ALIGN_ROW_MAX || dtype == PF_F16) {

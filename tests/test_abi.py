@@ -166,17 +166,45 @@ def test_chunk_rule_and_grid():
                 assert grid % 8 == 0 and ntiles <= grid < ntiles + 8 * rounds, (ntiles, tile, chunk, grid)
 
 
+def _lanes(m, nnz, max_len):
+    """The row-group lanes rule restated: at most one pass for the longest row; at least the power of two
+    nearest half the mean row, or the most lanes (up to 4x the mean row or a quarter of the longest) that
+    fit the chip's 2^19 resident lanes; 2..32."""
+    lat = min(32, max(2, 1 << (max_len - 1).bit_length()))
+    thr = 2
+    while thr < 32 and nnz / m / 2 >= thr * 2 ** 0.5:
+        thr *= 2
+    fill = 2
+    while fill < 32 and 2 * fill * m <= 1 << 19 and 2 * fill <= max(4 * nnz / m, max_len / 4):
+        fill *= 2
+    return min(lat, max(thr, fill))
+
+
 def test_select_auto_small_matrix():
-    """C1 shape (rows of 16): FLAT row groups of 16 lanes per row (3/4 of the mean, rounded up to a power of
-    two); a larger matrix of short rows: row-aligned tiles.  With a row beyond 256 nnz, too few 512-key tiles
-    for the device -> ADAPTIVE, 188-key tiles, one per run."""
+    """C1 shape (rows of 16): FLAT row groups of 16 lanes per row (the longest row, in one pass); up to 2^18
+    rows of at most 256 nnz whose values and columns fit 256 MB: row groups; beyond: row-aligned tiles.
+    With a row beyond 256 nnz, too few 512-key tiles for the device -> ADAPTIVE, 188-key tiles, one per run."""
     i = pf.select(make_stats(4096, 65536, 16), "f64", "auto")
     assert i.variant == pf.FLAT and i.tile == 16 and i.row_aligned == 1 and i.needs_fixup == 0
     assert i.ntiles == 4096 * 16 // 256
-    for m, nnz, lanes in ((100000, 500000, 4), (1000, 1000, 2), (1000, 40000, 32), (10000, 70000, 8)):
-        assert pf.select(make_stats(m, nnz, 200), "f32", "auto").tile == lanes, (m, nnz)
-    i = pf.select(make_stats(1000000, 5000000, 20), "f64", "auto")  # over 2M nnz: tiles
+    cases = ((100000, 500000, 200, 4),      # lanes that fill the chip
+             (1000, 1000, 200, 32),         # latency: the longest row, capped at 32
+             (10000, 70000, 8, 8),          # latency: the longest row
+             (32768, 65536, 10, 8),         # the longest row would overfill the chip: the filling lanes
+             (262144, 262144 * 32, 60, 16),  # throughput: half the mean row
+             (262144, 262144 * 8, 40, 4),
+             (262144, 262144 * 5, 5, 2),    # C2 at 512^2
+             (200000, 200000 * 128, 200, 32))
+    for m, nnz, mx, lanes in cases:
+        assert _lanes(m, nnz, mx) == lanes, (m, nnz, mx)
+        i = pf.select(make_stats(m, nnz, mx), "f32", "auto")
+        assert (i.variant, i.tile) == (pf.FLAT, lanes), (m, nnz, mx)
+    i = pf.select(make_stats(1000000, 5000000, 20), "f64", "auto")  # over 2^18 rows: tiles
     assert i.variant == pf.FLAT and i.tile == 1024 and i.row_aligned == 1
+    i = pf.select(make_stats(262145, 262145 * 5, 20), "f64", "auto")
+    assert i.variant == pf.FLAT and i.tile == 1024
+    i = pf.select(make_stats(200000, 200000 * 128, 200), "f64", "auto")  # 307 MB of values and columns: tiles
+    assert i.variant == pf.FLAT and i.tile == 1024
     i = pf.select(make_stats(4096, 65536, 300), "f64", "auto")
     assert i.variant == pf.ADAPTIVE and i.tile == 188 and i.run_tiles == 1
     assert i.long_row_min == 64

@@ -131,7 +131,10 @@ def _cand(v, t, us, gbps, run=0, ladder=0, hybrid=0, ok=True):
 
 
 def _mat(name, auto, cands):
-    return {"matrix": name, "auto": auto, "candidates": cands}
+    """A matrix as time_candidates returns it: AUTO's built-in rules first, timed as AUTO's own plan."""
+    same = [c for c in cands if all(c[k] == auto[k] for k in ("variant", "tile", "run", "ladder", "hybrid"))]
+    rules = dict(_cand("auto", 0, auto["us"], same[0]["gbps"], hybrid=1))
+    return {"matrix": name, "auto": auto, "candidates": [rules] + cands}
 
 
 def test_offline_tuner_score_time_then_counters_then_guard(table):
@@ -147,7 +150,7 @@ def test_offline_tuner_score_time_then_counters_then_guard(table):
             _mat("c", dict(auto_flat, tile=2048, hybrid=1),
                  [_cand("flat", 2048, 10.0, 500, hybrid=1), _cand("flat", 2048, 10.04, 498.0),
                   _cand("adaptive", 512, 30.0, 166, run=4)])],
-        # faster on the mean but slower than AUTO on one matrix: AUTO's configuration stays
+        # faster on the mean but slower than AUTO on one matrix: the built-in rules stay
         ("medium", "skewed"): [
             _mat("d", auto_flat, [_cand("flat", 1024, 10.0, 100), _cand("flat", 2048, 5.0, 200)]),
             _mat("e", auto_flat, [_cand("flat", 1024, 10.0, 100), _cand("flat", 2048, 10.5, 95)])],
@@ -166,25 +169,29 @@ def test_offline_tuner_score_time_then_counters_then_guard(table):
     dense = best[("large", "dense")]
     assert (dense["variant"], dense["tile"], dense["hybrid"]) == ("flat", 2048, 0)
     assert dense["fastest"]["hybrid"] == 1 and "fewest HBM bytes" in dense["why"]
-    assert sorted(x for x in seen if x[0] == "c") == [("c", "flat", 2048, 0), ("c", "flat", 2048, 1)]
-    assert (best[("medium", "skewed")]["tile"], best[("medium", "skewed")]["variant"]) == (1024, "flat")
-    assert best[("large", "short")]["tile"] == 1024
-    # without counters the fastest of the tie wins
+    assert sorted(x for x in seen if x[0] == "c") == [("c", "auto", 0, 1), ("c", "flat", 2048, 0),
+                                                       ("c", "flat", 2048, 1)]
+    assert best[("medium", "skewed")]["variant"] == "auto" and "built-in rules" in best[("medium", "skewed")]["why"]
+    assert best[("large", "short")]["variant"] == "auto"  # AUTO's flat 1024 and the rules tie; the rules come first
+    # without counters the fastest of the tie wins; on equal time the rules (listed first) stay
     best2 = at.choose(per_class, band=0.01, guard=0.005)
-    assert best2[("large", "dense")]["hybrid"] == 1
+    assert best2[("large", "dense")]["variant"] == "auto"
+    per_class[("large", "dense")][0]["candidates"][1]["gbps"] = 503.0  # the hybrid plan 0.6% faster
+    assert at.choose(per_class, band=0.01, guard=0.005)[("large", "dense")]["hybrid"] == 1
 
     th = {"small_upper": 5000000, "medium_upper": 20000000}
     at.write_table({"f64": best}, th, str(table), "test device")
     text = table.read_text()
     assert "small 5000000 regular f64 prefree 512 0 0 4 0" in text
     assert "large -1 dense f64 flat 2048 0 0 0 0" in text
+    assert "medium 20000000 skewed f64 auto 0 0 0 0 1" in text
     pf.set_tuning_table(str(table))
     assert pf.tuning_table() == str(table)
     sel = pf.select(make_stats(10000, 160000, 16), "f64", "auto")          # small, regular
     assert (sel.variant, sel.tile, sel.ladder) == (pf.PREFREE, 512, 4)
     assert "small 5000000 short f64 auto 0 0 0 0 1" in text
     sel = pf.select(make_stats(10000, 20000, 3), "f64", "auto")            # small, short: not measured, the rules
-    assert (sel.variant, sel.tile) == (pf.FLAT, 2)                         # row groups of 2 lanes (2 nnz per row)
+    assert (sel.variant, sel.tile) == (pf.FLAT, 4)                         # row groups: the longest row, 3 nnz
     sel = pf.select(make_stats(2000000, 15266620, 200000), "f64", "auto")  # medium, skewed
     assert (sel.variant, sel.tile) == (pf.FLAT, 1024)
 
