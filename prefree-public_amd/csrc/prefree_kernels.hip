@@ -3164,8 +3164,8 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
 // q sums products a + q, a + q + L, ... of its row in order, the group's DPP /
 // swizzle tree adds the L lane sums, and the group's first lane stores y.
 // Every index is clamped to the matrix: a row_ptr changed after planning reads
-// in bounds.  C1 in a HIP graph: 1.89 us per SpMV with L = 16 against 3.50 for
-// 1024-nnz tiles (4.00 in a launch loop against 2.84 for rocSPARSE's row split).
+// in bounds.  C1 in a HIP graph: 1.85 us per SpMV with L = 16 against 3.50 for
+// 1024-nnz tiles (2.49 in a launch loop against 2.73 for rocSPARSE's row split).
 template <typename T, int L>
 __global__ __launch_bounds__(kBS) void k_vector(Args<T> a)
 {
