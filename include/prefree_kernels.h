@@ -201,6 +201,13 @@ int pfk_adaptive_owners(int dtype, const pfk_spmv_args *a, void *stream);
  * tile's first / last row), with each tile's row range in owner_row (2 ints per tile); a second kernel adds a
  * row's partials in tile order and stores it rounded to half once. */
 int pfk_spmv_prefree(int dtype, const pfk_spmv_args *a, void *stream);
+/* The row map of a row-aligned FLAT plan (tile 1024 or 2048 nnz, ntiles = ceil(nnz / tile)), searched afresh
+ * from row_ptr: entry t of ntiles + 1 in a->row_map (room for (ntiles + 1) int2, row_map_bytes) is (f,
+ * row_ptr[f]) with f the first row whose row_ptr is at or above t·tile (entry 0: row 0; entry ntiles: row m),
+ * as the tiles kernel's search records it (guess_spread / guess_a / guess_b steer the search as there).  Band
+ * plans run it before the band kernel on a first call and on every call that remembers no rows.  Replaces the
+ * reference's pre-pass pre_start_rowPerTile (src/spmv_kernel/preFreeSpMV.cu:3-28) for these plans. */
+int pfk_row_map(const pfk_spmv_args *a, void *stream);
 /* Tile sizes compiled in for a variant: writes up to `cap` sizes, returns the count (at most
  * PFK_MAX_TILES, which a buffer of that length always holds). */
 #define PFK_MAX_TILES 16

@@ -210,6 +210,7 @@ def klib() -> ctypes.CDLL:
         _sig(K.pfk_device_name, [ctypes.c_char_p, _i])
         _sig(K.pfk_probe_gather, [_i, _vp, _ll, _vp, _ll, _vp, _ll, _i, _vp])
         _sig(K.pfk_band_stats, [_vp, _vp, _i, _vp, _vp])
+        _sig(K.pfk_row_map, [ctypes.POINTER(SpmvArgs), _vp])
         _sig(K.pfk_last_error, [], ctypes.c_char_p)
         _klib = K
     return _klib

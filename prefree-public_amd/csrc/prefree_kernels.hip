@@ -3155,6 +3155,35 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
     }
 }
 
+// ---- k_row_map: a row-aligned plan's row map, searched afresh --------------
+//
+// Entry t (0 <= t <= ntiles) of a row-aligned plan's row map is (f, row_ptr[f])
+// with f the first row whose row_ptr is at or above t * K (entry 0: row 0;
+// entry ntiles: row m), what k_rows's search records.  One wave per entry,
+// with k_rows's interpolated probe round and closing rounds.  The band kernel
+// reads steps from the map and cannot search: a band plan's first call, and
+// every call of one that remembers nothing, runs this kernel before it.
+__global__ __launch_bounds__(kBS) void k_row_map(const int *__restrict__ rp, int m, int nnz, int K, long long ntiles,
+                                                 int spread, double ga, double gb, int2 *__restrict__ map)
+{
+    const long long t = (long long)blockIdx.x * (kBS / kWave) + (long long)(threadIdx.x / kWave);
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    if (t > ntiles)
+        return;  // whole waves
+    int f = 0, r = 0;
+    if (t == 0) {
+        r = rp[0];
+    } else if (t == ntiles) {
+        f = m;
+        r = rp[m];
+    } else {  // 0 < t * K < nnz: the wave searches, every lane active
+        const uint32_t key = (uint32_t)(t * K);
+        const RowProbe probe = row_probe_issue(rp, m, key, nnz, spread, ga, gb, lane);
+        f = row_probe_finish(rp, m, key, probe, lane, r) + 1;
+    }
+    if (lane == 0) map[t] = make_int2(f, r);
+}
+
 // ---- k_vector: row groups (FLAT "tiles" 2..32) — small matrices -----------
 //
 // For a matrix small enough that its SpMV is a few dependent memory round trips
@@ -4713,6 +4742,27 @@ int pfk_row_stats(const int *row_ptr, const int *col, int m, int n, long long nn
                   unsigned long long *d_out, void *stream)
 {
     return launch_stats(row_ptr, col, m, n, nnz, d_out, nullptr, 0, stream);
+}
+
+int pfk_row_map(const pfk_spmv_args *a, void *stream)
+{
+    if (!a || !a->row_ptr || !a->row_map || a->m <= 0 || a->nnz <= 0 || !a->row_aligned ||
+        (a->tile != 1024 && a->tile != 2048)) {
+        snprintf(g_err, sizeof g_err, "pfk_row_map: a row-aligned FLAT plan of 1024 or 2048 nnz per tile");
+        return PF_ERR_INVALID;
+    }
+    const long long nt = a->ntiles;
+    if (nt != ((long long)a->nnz + a->tile - 1) / a->tile) {
+        snprintf(g_err, sizeof g_err, "pfk_row_map: %lld tiles for %d nnz of %d per tile", nt, a->nnz, a->tile);
+        return PF_ERR_INVALID;
+    }
+    if (!room(a->row_map, a->row_map_bytes, (nt + 1) * 8, "row map")) return PF_ERR_INVALID;
+    const long long waves = kBS / kWave;
+    hipLaunchKernelGGL(k_row_map, dim3((unsigned)((nt + 1 + waves - 1) / waves)), dim3(kBS), 0, S(stream),
+                       a->row_ptr, a->m, (int)a->nnz, a->tile, nt, a->guess_spread, a->guess_a, a->guess_b,
+                       reinterpret_cast<int2 *>(a->row_map));
+    PFK_LAUNCHED("k_row_map");
+    return PF_OK;
 }
 
 int pfk_band_stats(const int *row_ptr, const int *col, int m, unsigned long long *out, void *stream)

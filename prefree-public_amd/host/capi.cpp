@@ -1487,8 +1487,17 @@ int pf_plan_execute(pf_plan *plan, const int *d_row_ptr, const int *d_col, const
         if (plan->info.needs_fixup) PF_TRY(pfk_spmv_fixup(dt, 1, &a, stream), "split-row combine");
         return PF_OK;
     case PF_FLAT:
+        // The band kernel reads its steps from the row map and does not search: a band plan's first call, and
+        // every call of a plan that remembers no rows, searches the map afresh first (one wave per tile).
+        if (plan->info.band_w > 0 && plan->info.row_aligned && plan->row_map &&
+            (!plan->remember_rows || !plan->map_ready)) {
+            a.row_map = plan->row_map;
+            a.band_w = plan->info.band_w;
+            PF_TRY(pfk_row_map(&a, stream), "row map");
+            a.map_ready = 1;
+        }
         PF_TRY(pfk_spmv_flat(dt, &a, stream), "flat kernel");  // tile 256 launches its own combine
-        if (a.row_map) plan->map_ready = true;  // later calls on this stream read the recorded rows
+        if (a.row_map && plan->remember_rows) plan->map_ready = true;  // later calls read the recorded rows
         if (plan->info.needs_fixup && plan->info.tile != kFlowTile)
             PF_TRY(pfk_spmv_fixup(dt, 0, &a, stream), "split-row combine");
         return PF_OK;

@@ -1,17 +1,22 @@
 """The band kernel (k_band) on the GPU, through the C ABI.
 
 Row-aligned FLAT plans of matrices whose columns lie mostly within +-w of their row keep each step's band of
-x in an LDS ring (pf_plan_set_band; on by default for matrices of under 4 nnz per row).  The plan's first
-call searches rows with the tiles' kernel and records the row map; later calls run the band kernel.  Checked
-against the CPU oracle and against the tiles' own kernel on the same plan:
+x in an LDS ring (pf_plan_set_band; on by default for matrices of under 4 nnz per row).  The band kernel reads
+its steps from the plan's row map: the plan's first call searches the map afresh (k_row_map, one wave per tile)
+and later calls read it; a plan that remembers no rows searches it on every call.  Checked against the CPU
+oracle and against the tiles' own kernel on the same plan:
 
 * known-answer values bit for bit; U[-1,1] values within 1e-12 (fp64) / 1e-5 (fp32) of sum |a_ij x_j|;
 * the band kernel's y equals the tiles' kernel's y bit for bit (both sum each row in nnz order);
 * scaled C4 and C2, banded matrices with outliers, bands wider and narrower than the columns' spread,
   steps of very many empty rows (windows that jump), rectangular x, fp64 and fp32;
 * graph replays of a band plan equal its eager calls;
-* pf_plan_set_band is refused for a plan without a band.
+* pf_plan_set_band is refused for a plan without a band;
+* the row-map search (pfk_row_map) gives, for every tile t, the first row whose row_ptr is at or above t·tile
+  (numpy's searchsorted, side "left"), with its row_ptr, whatever the search's guess parameters.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -119,8 +124,8 @@ def test_band_default_rule():
 
 
 def test_band_plan_searching_every_call():
-    """A band plan told to search its rows on every call (pf_plan_set_remember_rows(plan, 0)) has no row map:
-    its calls run the tiles' kernel, with the band plan's y; switching back records the map again."""
+    """A band plan told to search its rows on every call (pf_plan_set_remember_rows(plan, 0)) searches its row
+    map afresh before each band kernel, with the remembering plan's y; switching back records the map again."""
     name, rp, col, n = CASES[0]
     m = len(rp) - 1
     val, x = oracle.initvec(len(col)), oracle.initvec(n)
@@ -198,3 +203,60 @@ def test_band_stats_sample(case):
     pf.band_stats(dev(rp), dev(col), len(rp) - 1, out)
     torch.cuda.synchronize()
     assert out.cpu().tolist() == _band_stats_np(rp, col), case
+
+
+def _row_map_cases():
+    rng = np.random.default_rng(77)
+    out = []
+    lens = rng.poisson(2.5, 300000)
+    lens[rng.random(300000) < 0.3] = 0
+    out.append(("poisson_empty", lens))
+    out.append(("exact_256", np.full(8192, 256)))                      # every tile boundary a row start
+    lens = rng.integers(0, 9, 200000)
+    lens[50000:150000] = 0                                             # 100k empty rows in one stretch
+    out.append(("empty_stretch", lens))
+    out.append(("one_tile", rng.integers(0, 4, 300)))                  # nnz under a tile
+    out.append(("multiple", np.full(4096, 4)))                         # nnz a multiple of both tiles
+    lens = rng.integers(0, 3, 400000)
+    lens[-1000:] = 200                                                 # a dense tail
+    out.append(("dense_tail", lens))
+    return out
+
+
+@pytest.mark.parametrize("name,lens", _row_map_cases(), ids=[c[0] for c in _row_map_cases()])
+@pytest.mark.parametrize("tile", [1024, 2048])
+def test_row_map_search(name, lens, tile):
+    rp = np.zeros(len(lens) + 1, dtype=np.int64)
+    np.cumsum(lens, out=rp[1:])
+    m, nnz = len(lens), int(rp[-1])
+    nt = -(-nnz // tile)
+    f = [0] + [int(np.searchsorted(rp, t * tile, side="left")) for t in range(1, nt)] + [m]
+    want = np.array([(r, rp[r]) for r in f], dtype=np.int64)
+    d_rp = dev(rp.astype(np.int32))
+    out = torch.full((2 * (nt + 1),), -7, dtype=torch.int32, device="cuda:0")
+    K = pf.klib()
+    guesses = [(0, 0.0, 0.0), (16, 0.0, 0.0), (1, m / nnz, 3.0), (4, 1e-3, -5.0)]
+    for spread, ga, gb in guesses:
+        out.fill_(-7)
+        a = pf.SpmvArgs(row_ptr=d_rp.data_ptr(), m=m, nnz=nnz, tile=tile, ntiles=nt, row_aligned=1,
+                        row_map=out.data_ptr(), row_map_bytes=8 * (nt + 1), guess_spread=spread, guess_a=ga,
+                        guess_b=gb)
+        print(f"row map {name} tile={tile} m={m} nnz={nnz} guess=({spread}, {ga}, {gb})", flush=True)
+        assert K.pfk_row_map(ctypes.byref(a), None) == 0, K.pfk_last_error()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().astype(np.int64).reshape(-1, 2)
+        bad = np.nonzero((got != want).any(axis=1))[0]
+        assert bad.size == 0, (name, tile, spread, ga, gb, bad[:5], got[bad[:5]], want[bad[:5]])
+
+
+def test_row_map_refuses_bad_args():
+    K = pf.klib()
+    fake = 0x10000  # never dereferenced: refused on the host
+    a = pf.SpmvArgs(row_ptr=fake, m=100, nnz=5000, tile=1024, ntiles=5, row_aligned=1, row_map=fake,
+                    row_map_bytes=8 * 5)
+    assert K.pfk_row_map(ctypes.byref(a), None) == 1 and b"row map" in K.pfk_last_error()
+    a.row_map_bytes = 8 * 6
+    a.ntiles = 4
+    assert K.pfk_row_map(ctypes.byref(a), None) == 1  # ntiles is not ceil(nnz / tile)
+    a.ntiles, a.tile = 5, 512
+    assert K.pfk_row_map(ctypes.byref(a), None) == 1
