@@ -422,7 +422,7 @@ def measure(pf, torch, cfg, dt, args, steps, warmup, want_cpu):
         if (info["variant_name"] == "flat" and info["row_aligned"] and info["tile"] == 1024 and not info.get("hybrid")
                 and info["ntiles"] >= 2048):
             own = dict(own, tile_2048=search_time(2048))
-        rec["search"] = dict(own, what="every call searches row_ptr for each tile's rows inside the tile kernel, with "
+        rec["search"] = dict(own, what="every call searches row_ptr for each tile's rows inside the tile kernel (a band plan: in a row-map kernel before the band kernel), with "
                                        "the plan's own tile (tile_2048: the same with 2048-nnz tiles); "
                                        "vs_recorded_rows against the hot plan's recorded-rows time")
 
