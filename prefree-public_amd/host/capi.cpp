@@ -368,8 +368,9 @@ bool tile_supported(int variant, int dtype, int tile)
 }
 
 // Workgroups launched: ADAPTIVE runs of run_tiles tiles, four waves per
-// workgroup, runs dealt evenly to the XCDs; one tile per workgroup otherwise
-// (FLAT 1024/2048: tiles padded to whole rounds of XCD chunks).
+// workgroup, runs dealt evenly to the XCDs; row groups ntiles workgroups; one
+// tile per workgroup otherwise (FLAT 1024/2048: tiles padded to whole rounds
+// of XCD chunks).
 void set_grid(pf_plan_info &r)
 {
     if (r.variant == PF_ADAPTIVE || (r.variant == PF_FLAT && r.tile == kFlowTile)) {
@@ -379,6 +380,8 @@ void set_grid(pf_plan_info &r)
         r.grid = ((tx + 3) / 4) * kXcds;
     } else if (uses_row_map(r.variant, r.tile)) {
         r.grid = pfk_flat_grid(r.ntiles, r.tile, r.chunk_nnz);
+    } else if (r.variant == PF_FLAT && PFK_ROW_GROUP_TILE(r.tile)) {
+        r.grid = r.ntiles;  // row groups: one workgroup per 256 lanes, by index
     } else {
         r.grid = ((r.ntiles + kXcds - 1) / kXcds) * kXcds;
     }

@@ -186,7 +186,7 @@ def test_select_auto_small_matrix():
     With a row beyond 256 nnz, too few 512-key tiles for the device -> ADAPTIVE, 188-key tiles, one per run."""
     i = pf.select(make_stats(4096, 65536, 16), "f64", "auto")
     assert i.variant == pf.FLAT and i.tile == 16 and i.row_aligned == 1 and i.needs_fixup == 0
-    assert i.ntiles == 4096 * 16 // 256
+    assert i.ntiles == 4096 * 16 // 256 and i.grid == i.ntiles  # workgroups of 256 lanes, launched as many
     cases = ((100000, 500000, 200, 4),      # lanes that fill the chip
              (1000, 1000, 200, 32),         # latency: the longest row, capped at 32
              (10000, 70000, 8, 8),          # latency: the longest row
