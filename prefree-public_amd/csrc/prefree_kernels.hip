@@ -3158,30 +3158,60 @@ __global__ __launch_bounds__(kBS) void k_fixup(Args<T> a, int K)
 // ---- k_row_map: a row-aligned plan's row map, searched afresh --------------
 //
 // Entry t (0 <= t <= ntiles) of a row-aligned plan's row map is (f, row_ptr[f])
-// with f the first row whose row_ptr is at or above t * K (entry 0: row 0;
-// entry ntiles: row m), what k_rows's search records.  One wave per entry,
-// with k_rows's interpolated probe round and closing rounds.  The band kernel
-// reads steps from the map and cannot search: a band plan's first call, and
-// every call of one that remembers nothing, runs this kernel before it.
+// with f the first row whose row_ptr is at or above v = t * K (entry 0: row 0;
+// entry ntiles: row m), what k_rows's search records.  The band kernel reads
+// its steps from the map and cannot search: a band plan's first call, and
+// every call of one that remembers no rows, runs this kernel before it.
+// A group of kMapLanes lanes per entry, so that every entry's search is in
+// flight at once (C4: 24,416 entries, 6,104 waves): the first round probes
+// kMapLanes rows around the plan's interpolated guess, 4 x guess_spread apart
+// (the span k_rows's 64 probes cover), each later round kMapLanes rows evenly
+// inside the bracket left, which it cuts about 17-fold.  The bracket
+// (lo, hi] always holds the answer: row_ptr[lo] < v <= row_ptr[hi], lo = -1
+// standing for "below every row"; probes are non-decreasing in the lane, so
+// the lanes whose row_ptr lies below v are the group's lowest.
+constexpr int kMapLanes = 16;
+
 __global__ __launch_bounds__(kBS) void k_row_map(const int *__restrict__ rp, int m, int nnz, int K, long long ntiles,
                                                  int spread, double ga, double gb, int2 *__restrict__ map)
 {
-    const long long t = (long long)blockIdx.x * (kBS / kWave) + (long long)(threadIdx.x / kWave);
+    const long long t = ((long long)blockIdx.x * kBS + threadIdx.x) / kMapLanes;
     const int lane = (int)(threadIdx.x & (kWave - 1));
-    if (t > ntiles)
-        return;  // whole waves
-    int f = 0, r = 0;
-    if (t == 0) {
-        r = rp[0];
-    } else if (t == ntiles) {
-        f = m;
-        r = rp[m];
-    } else {  // 0 < t * K < nnz: the wave searches, every lane active
-        const uint32_t key = (uint32_t)(t * K);
-        const RowProbe probe = row_probe_issue(rp, m, key, nnz, spread, ga, gb, lane);
-        f = row_probe_finish(rp, m, key, probe, lane, r) + 1;
+    const int q = lane & (kMapLanes - 1);
+    const int base = lane - q;  // the group's first lane in the wave
+    const bool search = t > 0 && t < ntiles;  // whole groups
+    const uint32_t v = search ? (uint32_t)(t * K) : 0u;
+    int lo = -1, hi = m;
+    int khi = (t <= ntiles) ? rp[m] : 0;  // row_ptr[hi], issued beside the first round
+    // first round: around the guess
+    const double g = ga > 0.0 ? ga * (double)v + gb : (nnz > 0 ? (double)v * ((double)m / (double)nnz) : 0.0);
+    const long long gc = (long long)fmin(fmax(g, 0.0), (double)m);  // (NaN: 0)
+    const long long step0 = 4LL * max(spread, 1);
+    int p = (int)min(max(gc + (long long)(q - kMapLanes / 2) * step0, 0LL), (long long)m);
+    int k = search ? rp[p] : 0;
+    for (;;) {
+        const unsigned below = (unsigned)(__ballot(search && k < (int)v) >> base) & ((1u << kMapLanes) - 1);
+        const int nb = __popc(below);  // probes below v: lanes 0 .. nb - 1 of the group
+        const int plo = __shfl(p, base + max(nb - 1, 0));
+        const int phi = __shfl(p, base + min(nb, kMapLanes - 1));
+        const int khn = __shfl(k, base + min(nb, kMapLanes - 1));
+        if (search) {
+            if (nb > 0) lo = max(lo, plo);
+            if (nb < kMapLanes && phi < hi) { hi = phi; khi = khn; }
+        }
+        if (!__ballot(search && hi - lo > 1))
+            break;
+        // kMapLanes probes evenly inside (lo, hi), the last at most hi - 1
+        const int step = hi - lo > 1 ? (hi - lo + kMapLanes) / (kMapLanes + 1) : 1;
+        p = search && hi - lo > 1 ? (int)min((long long)lo + (long long)(q + 1) * step, (long long)hi - 1) : max(lo, 0);
+        k = search && hi - lo > 1 ? rp[p] : 0;
     }
-    if (lane == 0) map[t] = make_int2(f, r);
+    if (q == 0 && t <= ntiles) {
+        if (t == 0)
+            map[0] = make_int2(0, rp[0]);
+        else
+            map[t] = search ? make_int2(hi, khi) : make_int2(m, khi);
+    }
 }
 
 // ---- k_vector: row groups (FLAT "tiles" 2..32) — small matrices -----------
@@ -4757,8 +4787,8 @@ int pfk_row_map(const pfk_spmv_args *a, void *stream)
         return PF_ERR_INVALID;
     }
     if (!room(a->row_map, a->row_map_bytes, (nt + 1) * 8, "row map")) return PF_ERR_INVALID;
-    const long long waves = kBS / kWave;
-    hipLaunchKernelGGL(k_row_map, dim3((unsigned)((nt + 1 + waves - 1) / waves)), dim3(kBS), 0, S(stream),
+    const long long per_wg = kBS / kMapLanes;
+    hipLaunchKernelGGL(k_row_map, dim3((unsigned)((nt + 1 + per_wg - 1) / per_wg)), dim3(kBS), 0, S(stream),
                        a->row_ptr, a->m, (int)a->nnz, a->tile, nt, a->guess_spread, a->guess_a, a->guess_b,
                        reinterpret_cast<int2 *>(a->row_map));
     PFK_LAUNCHED("k_row_map");
