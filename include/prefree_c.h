@@ -219,8 +219,13 @@ int pf_plan_destroy(pf_plan *plan);
  * tiles and XCD chunks; PREFREE tiles x its five reduction ladders and the
  * ordinary-load cache policy when asked by `flags`), each as the best of two
  * batches of `reps` back-to-back SpMVs, and switches the plan to the fastest.
- * The plan's own configuration (a hybrid plan included) is the first candidate.
- * d_y holds A·x on return.  Synchronises `stream`; allocates temporary plans.
+ * FLAT row groups (tiles 2..32) are candidates where no row exceeds 256 nnz.
+ * When the plan's own call takes under 20 us launched one by one (bound by the
+ * host's launch rate), every candidate is timed instead as one captured HIP
+ * graph of max(reps, 20) calls on a stream of the tuner's own, so `stream`
+ * must not be capturing.  The plan's own configuration (a hybrid plan
+ * included) is the first candidate.  d_y holds A·x on return.  Synchronises
+ * `stream`; allocates temporary plans and, for graphs, a stream and a graph.
  * The online counterpart of the reference tuner
  * (scripts/profile_and_generate.py:319-418), which compiled and timed each
  * candidate as a separate program. */

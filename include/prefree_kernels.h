@@ -283,6 +283,13 @@ int pfk_event_destroy(void *e);
 int pfk_event_record(void *e, void *s);
 int pfk_event_sync(void *e);
 int pfk_event_elapsed_ms(float *ms, void *start, void *stop);
+/* A HIP graph of the work queued on `stream` (a non-null stream) between pfk_graph_begin and pfk_graph_end
+ * (capture mode thread-local), instantiated into *exec; pfk_graph_end always ends the capture, and on failure
+ * sets *exec to NULL.  pf_plan_autotune times launch-bound plans this way. */
+int pfk_graph_begin(void *stream);
+int pfk_graph_end(void *stream, void **exec);
+int pfk_graph_launch(void *exec, void *stream);
+int pfk_graph_destroy(void *exec);
 int pfk_device_count(int *n);
 int pfk_get_device(int *dev);  /* the calling thread's current device */
 int pfk_device_name(char *buf, int len);

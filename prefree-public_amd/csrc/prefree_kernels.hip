@@ -4976,6 +4976,45 @@ int pfk_event_elapsed_ms(float *ms, void *start, void *stop)
     return PF_OK;
 }
 
+int pfk_graph_begin(void *stream)
+{
+    if (!stream) {
+        snprintf(g_err, sizeof g_err, "pfk_graph_begin: the null stream cannot be captured");
+        return PF_ERR_INVALID;
+    }
+    PFK_HIP(hipStreamBeginCapture(S(stream), hipStreamCaptureModeThreadLocal));
+    return PF_OK;
+}
+
+int pfk_graph_end(void *stream, void **exec)
+{
+    if (!exec) return PF_ERR_INVALID;
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    PFK_HIP(hipStreamEndCapture(S(stream), &g));
+    hipGraphExec_t x = nullptr;
+    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);  // the executable graph keeps its own copy
+    if (e != hipSuccess) {
+        snprintf(g_err, sizeof g_err, "hipGraphInstantiate: %s", hipGetErrorString(e));
+        return PF_ERR_HIP;
+    }
+    *exec = x;
+    return PF_OK;
+}
+
+int pfk_graph_launch(void *exec, void *stream)
+{
+    PFK_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), S(stream)));
+    return PF_OK;
+}
+
+int pfk_graph_destroy(void *exec)
+{
+    if (exec) PFK_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)));
+    return PF_OK;
+}
+
 int pfk_device_count(int *n) { PFK_HIP(hipGetDeviceCount(n)); return PF_OK; }
 
 int pfk_get_device(int *dev) { PFK_HIP(hipGetDevice(dev)); return PF_OK; }

@@ -99,6 +99,43 @@ def test_autotune_picks_a_correct_faster_configuration(cfg, scale):
         assert_parity(rp, col, v["f64"], x, y2.cpu().numpy(), "f64", what=f"C{cfg} tuned plan")
 
 
+@pytest.mark.gpu
+def test_autotune_times_launch_bound_plans_as_graphs():
+    """C1 (65k nnz) launched call by call is bound by the host's launch rate: pf_plan_autotune then times every
+    candidate as a captured graph, so its figures fall below the eager per-call time, and it keeps a correct
+    plan whose graph time is no worse than the default's."""
+    import torch
+    from gpu_util import DEV, assert_parity, dev
+    rp, col, v = pf.synth_csr(1, seed=4)
+    m = len(rp) - 1
+    x = pf.synth_x(1, m, seed=4)["f64"]
+    d = [dev(rp), dev(col), dev(v["f64"]), dev(x)]
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device=DEV)
+    with pf.Plan(d[0], d[1], m, m, len(col), "f64", "auto") as p:
+        s = torch.cuda.current_stream()
+        for _ in range(5):
+            p.execute(*d, y, stream=s)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(200):
+            p.execute(*d, y, stream=s)
+        e1.record(s)
+        torch.cuda.synchronize()
+        eager_us = e0.elapsed_time(e1) * 1e3 / 200
+        print(f"C1 eager {eager_us:.2f} us per call", flush=True)
+        r = p.autotune(*d, y, reps=50)
+        torch.cuda.synchronize()
+        print(f"C1 autotune {r}", flush=True)
+        assert r["us"] <= r["default_us"]
+        assert r["default_us"] < eager_us, (r, eager_us)  # graph-timed: below the launch-bound eager time
+        assert_parity(rp, col, v["f64"], x, y.cpu().numpy(), "f64", what="C1 autotune y")
+        y.fill_(float("nan"))
+        p.execute(*d, y)
+        torch.cuda.synchronize()
+        p.check()
+        assert_parity(rp, col, v["f64"], x, y.cpu().numpy(), "f64", what="C1 tuned plan")
+
+
 def _autotune_module():
     import importlib.util
     import os
