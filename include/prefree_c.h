@@ -117,10 +117,11 @@ typedef struct pf_plan_info {
                                 is centred on row guess_a * key + guess_b with a spacing of 1 (the line of
                                 pf_row_stats, chosen when at most m / 256 rows lie over 28 rows from it); 0:
                                 key * m / nnz with guess_spread */
-    int band_w;              /* row-aligned FLAT plans, fp64 / fp32: > 0 when calls after the first run the band
-                                kernel, which keeps x[first row - band_w, last row + band_w) of each step of 4096
-                                nnz in LDS (85% or more of the columns lie within +-band_w of their row); 0: the
-                                tiles' own kernel.  See pf_plan_set_band. */
+    int band_w;              /* row-aligned FLAT plans, fp64 / fp32: > 0 when calls run the band kernel, which
+                                keeps x[first row - band_w, last row + band_w) of each step of 4096 nnz in LDS
+                                (85% or more of the columns lie within +-band_w of their row) and reads its steps
+                                from the row map (searched by pfk_row_map on a first call and on every call of a
+                                plan that remembers no rows); 0: the tiles' own kernel.  See pf_plan_set_band. */
 } pf_plan_info;
 
 typedef struct pf_plan pf_plan;

@@ -2023,8 +2023,9 @@ __global__ __launch_bounds__(kBS) void k_rows(Args<T> a, int *__restrict__ map, 
 // offset the range check turns into zeros), so the compiler's wait counts
 // stay exact across the pipeline.  Rows of at most kThreadMax nnz are summed
 // by one lane in nnz order (bit-identical to spmv_serial), longer rows (at
-// most PFK_ALIGN_ROW_MAX) by a wave.  The plan's first call, which searches
-// rows and records the map, runs k_rows; later calls run this kernel.
+// most PFK_ALIGN_ROW_MAX) by a wave.  The map is the plan's recorded one, or
+// one k_row_map searched just before (a first call, or a plan that remembers
+// no rows).
 constexpr int kBandBS = 1024;
 constexpr int kBandWaves = kBandBS / kWave;
 constexpr int kBandPer = 5;                         // elements per thread: a step and its last row's overflow
