@@ -24,7 +24,10 @@ each matrix.  A class's score:
      are no slower than AUTO's plan on any matrix of the class (beyond the
      timing noise `auto_guard`), rocprofv3 FETCH_SIZE + WRITE_SIZE per SpMV
      (every kernel of a step, scaled by a 256 MiB copy kernel measured in the
-     same profiled process) decides: the fewest HBM bytes wins.  Equal time,
+     same profiled process) decides: the fewest HBM bytes wins.  A third pass
+     (TCC_HIT_sum, TCC_MISS_sum) records each counted candidate's L2 hit rate
+     in the results beside its bytes.  (MALL hits are not separable on gfx950:
+     TCC_EA0_RDREQ_DRAM_sum reads the same as TCC_EA0_RDREQ_sum.)  Equal time,
      fewer bytes leaves more of HBM to whatever runs beside the SpMV and
      loses less when the 256 MB MALL does not hold the matrix.
   3. guard: a winner must not be slower than AUTO's plan on any matrix of the
@@ -369,6 +372,17 @@ def measure(args):
     torch.cuda.synchronize()
 
 
+def step_count(rows, counter, calls=20):
+    """A counter's reading per SpMV step (every kernel dispatched once per call, `calls` times or more, summed
+    per step; the copy kernel and the once-only planning and searching dispatches left out), unscaled."""
+    by_kernel = collections.defaultdict(list)
+    for r in rows:
+        if r["Counter_Name"] == counter and "neg" not in r["Kernel_Name"]:
+            by_kernel[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    step = [v for v in by_kernel.values() if len(v) >= calls - 1]
+    return sum(sum(v) / len(v) for v in step) if step else None
+
+
 def step_bytes(rows, counter, calls=20):
     """Bytes per SpMV step from one counter pass: every kernel dispatched once per call (`calls` times or
     more; planning kernels and the plan's first, searching call run once) summed per step, scaled by the
@@ -410,6 +424,17 @@ def counters_for(matrix, dtype, c):
         out[counter.lower() + "_bytes"] = b
         out[counter.lower() + "_scale"] = round(scale / 1024, 4)
     out["traffic_bytes"] = out["fetch_size_bytes"] + out["write_size_bytes"]
+    # L2 hit rate of the step (reported beside the bytes, not scored): one more pass with two TCC counters
+    d = os.path.join(tmp, "TCC")
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", "TCC_HIT_sum", "TCC_MISS_sum", "--output-format", "csv",
+           "-d", d, "-o", "run", "--", sys.executable, os.path.abspath(__file__), "--measure", matrix, dtype,
+           c["variant"], str(c["tile"]), str(c["run"]), str(c["keep"]), str(c["ladder"]), str(c["hybrid"])]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=150, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"))
+    if r.returncode == 0:
+        rows = list(csv.DictReader(open(os.path.join(d, "run_counter_collection.csv"))))
+        hit, miss = step_count(rows, "TCC_HIT_sum"), step_count(rows, "TCC_MISS_sum")
+        if hit is not None and miss is not None and hit + miss > 0:
+            out["l2_hit_rate"] = round(hit / (hit + miss), 4)
     print(json.dumps({"matrix": matrix, "counters": c, **out}), flush=True)
     return out
 

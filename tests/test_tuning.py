@@ -249,6 +249,20 @@ def test_step_bytes_sums_the_kernels_of_a_step():
     assert b == int(150 * scale)
 
 
+def test_step_count_sums_the_kernels_of_a_step_unscaled():
+    at = _autotune_module()
+    rows = []
+    for i in range(20):
+        rows.append({"Counter_Name": "TCC_HIT_sum", "Kernel_Name": "k_a<double>", "Counter_Value": "30"})
+        rows.append({"Counter_Name": "TCC_HIT_sum", "Kernel_Name": "k_b<double, 1>", "Counter_Value": "12"})
+        rows.append({"Counter_Name": "TCC_MISS_sum", "Kernel_Name": "k_a<double>", "Counter_Value": "10"})
+    rows.append({"Counter_Name": "TCC_HIT_sum", "Kernel_Name": "k_row_stats", "Counter_Value": "999"})
+    rows.append({"Counter_Name": "TCC_HIT_sum", "Kernel_Name": "neg_kernel", "Counter_Value": "5000"})
+    assert at.step_count(rows, "TCC_HIT_sum") == 42
+    assert at.step_count(rows, "TCC_MISS_sum") == 10
+    assert at.step_count(rows, "TCC_EA0_RDREQ_sum") is None
+
+
 def test_offline_tuner_merges_runs_per_dtype(tmp_path):
     import json
     at = _autotune_module()
