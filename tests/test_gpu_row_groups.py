@@ -70,3 +70,25 @@ def test_auto_takes_row_groups_for_small_short_rows():
     col = (np.arange(3 * m, dtype=np.int64) * 7919 % m).astype(np.int32)
     y, info = gpu_spmv(rp, col, oracle.initvec(len(col)), oracle.initvec(m), "auto")
     assert info["tile"] in (1024, 2048) and info["row_aligned"] == 1, info
+
+
+def test_row_groups_at_the_rule_bounds():
+    """2^18 rows of up to 256 nnz: fp32 values and columns within 256 MB take row groups (half the mean row of
+    48: 32 lanes), the same pattern at 128 nnz per row in fp64 (403 MB) takes tiles; both against the oracle."""
+    rng = np.random.default_rng(17)
+    m = 1 << 18
+    for dtype, lam, want_groups in (("f32", 48.0, True), ("f64", 128.0, False)):
+        lens = np.minimum(rng.poisson(lam, m), 256)
+        rp = np.zeros(m + 1, dtype=np.int64)
+        np.cumsum(lens, out=rp[1:])
+        rp = rp.astype(np.int32)
+        col = rng.integers(0, m, int(rp[-1])).astype(np.int32)
+        val = oracle.initvec(len(col), NP[dtype])
+        x = oracle.initvec(m, NP[dtype])
+        print(f"bounds {dtype} nnz={len(col)}", flush=True)
+        y, info = gpu_spmv(rp, col, val, x, "auto", dtype=dtype)
+        groups = info["variant_name"] == "flat" and info["tile"] <= 32
+        assert groups == want_groups, (dtype, info)
+        if want_groups:
+            assert info["tile"] == 32, info
+        assert_parity(rp, col, val, x, y, dtype, exact=kat_exact_possible(rp, dtype), what=f"bounds {dtype}")
