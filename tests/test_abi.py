@@ -180,6 +180,32 @@ def _lanes(m, nnz, max_len):
     return min(lat, max(thr, fill))
 
 
+def test_row_group_lanes_properties():
+    """Over random shapes inside AUTO's row-group bounds: the lanes are a power of two in 2..32, never more than
+    one pass of the longest row needs (beyond 2), at least the power of two nearest half the mean row (up to
+    that bound), and the plan reports one workgroup per 256 lanes."""
+    import math
+    import random
+    rnd = random.Random(5)
+    for _ in range(400):
+        m = rnd.randint(1, 1 << 18)
+        mean = rnd.uniform(0.05, 200.0)
+        mx = rnd.randint(max(1, int(mean)), 256)
+        nnz = min(int(mean * m), mx * m)
+        i = pf.select(make_stats(m, nnz, mx), "f32", "auto")
+        if nnz * 8 > 256 << 20:
+            assert i.tile >= 1024, (m, nnz, mx)
+            continue
+        L = i.tile
+        assert i.variant == pf.FLAT and L in (2, 4, 8, 16, 32), (m, nnz, mx, L)
+        lat = min(32, max(2, 1 << (mx - 1).bit_length()))
+        assert L <= lat, (m, nnz, mx, L)
+        h = nnz / m / 2
+        thr = 2 if h <= 0 else min(32, max(2, 2 ** math.floor(math.log2(h) + 0.5)))
+        assert L >= min(lat, thr), (m, nnz, mx, L)
+        assert i.grid == i.ntiles == max(1, -(-m * L // 256))
+
+
 def test_select_auto_small_matrix():
     """C1 shape (rows of 16): FLAT row groups of 16 lanes per row (the longest row, in one pass); up to 2^18
     rows of at most 256 nnz whose values and columns fit 256 MB: row groups; beyond: row-aligned tiles.
