@@ -2114,8 +2114,14 @@ __device__ __forceinline__ void band_load_cv(const Args<T> &a, const BandStep &d
 #pragma unroll
     for (int k = 0; k < kBandPer; ++k) {
         const int q = k * kBandBS + (int)threadIdx.x;
+        // col and val non-temporal, which most likely leaves more of the MALL to x for the outside gathers
+        // (C4 269.1 -> 260.6 us with val so loaded, fp32 209.7 -> 203.4; row_ptr so loaded too: 263.2, 209.4)
+        static_assert(sizeof(T) == 8 || sizeof(T) == 4, "fp64 / fp32");
         c[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(rc, q * 4, 0, kAuxNt);
-        v[k] = buf_load(rv, (uint32_t)(q * (int)sizeof(T)), (T *)nullptr);
+        if constexpr (sizeof(T) == 8)
+            v[k] = __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(rv, q * 8, 0, kAuxNt));
+        else
+            v[k] = __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b32(rv, q * 4, 0, kAuxNt));
     }
 }
 
